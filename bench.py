@@ -1,0 +1,358 @@
+#!/usr/bin/env python3
+"""Sparse decode step benchmark on one MI355X.
+
+Workload (one decode step of one layer for a batch, Llama-3-8B head shape):
+16 requests x 32 query heads / 8 KV heads x head_dim 128, bf16, 32768 tokens
+of context per request in pages of 64 (512 pages), Quest selects 32 pages
+(2048 rows, sink and last page forced). Residency over the selected pages:
+16 resident in the pool (the last two pages among them), 8 already in the hot
+buffer, 8 missing (their rows come from pinned host memory). The hot buffer
+holds H = 4096 rows per request, fully occupied, in a random LRU order. Q/K/V
+are N(0,1) from a seeded generator.
+
+One step = Quest score + top-k (nhs_quest_select) -> row resolution
+(nhs_resolve_rows) -> host-row gather on a side stream (nhs_gather_rows)
+-> attention (nhs_attend_rows). The resolver's tags/LRU are restored from a
+saved copy at the start of every step (a 0.8 MB device copy, inside the timed
+region) so every step has the same 25% misses. Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "nano-hisparse_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "decode tokens/s at 1 GPU; sparse-attn+gather step µs; achieved HBM/PCIe GB/s"
+HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+PCIE_PEAK = 64.0e9  # PCIe Gen5 x16, one direction, bytes/s
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-steps", type=int, default=3, help="steps of the CPU oracle baseline (0 to skip)")
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--context", type=int, default=32768)
+    ap.add_argument("--seed", type=int, default=42)
+    return ap.parse_args()
+
+
+class Workload:
+    q_heads, kv_heads, head_dim, page = 32, 8, 128, 64
+    top_pages = 32
+    resident_pages, hot_pages = 16, 8  # of the selected pages; the rest miss
+
+    def __init__(self, batch, context, seed, device):
+        import torch
+
+        from nano_hisparse import row_kernels as rk
+
+        self.batch, self.context, self.device = batch, context, device
+        B, Hq, Hkv, D, P = batch, self.q_heads, self.kv_heads, self.head_dim, self.page
+        n_pages = context // P
+        self.n_pages = n_pages
+        self.K = self.top_pages * P
+        self.H = 2 * self.K
+        dtype = torch.bfloat16
+        gen = torch.Generator(device=device).manual_seed(seed)
+        # Host store: one host page per logical page, request b owns [b*n_pages, (b+1)*n_pages).
+        self.host = torch.empty(B * n_pages, 2, P, Hkv, D, dtype=dtype, pin_memory=True)
+        mn = torch.empty(B, n_pages, Hkv, D, dtype=dtype, device=device)
+        mx = torch.empty_like(mn)
+        chunk = 256
+        for start in range(0, B * n_pages, chunk):
+            blk = torch.randn(min(chunk, B * n_pages - start), 2, P, Hkv, D, generator=gen, device=device).to(dtype)
+            self.host[start : start + blk.shape[0]].copy_(blk)
+            flat_mn = mn.view(B * n_pages, Hkv, D)
+            flat_mx = mx.view(B * n_pages, Hkv, D)
+            flat_mn[start : start + blk.shape[0]] = blk[:, 0].amin(1)
+            flat_mx[start : start + blk.shape[0]] = blk[:, 0].amax(1)
+        self.minimum, self.maximum = mn, mx
+        self.q = torch.randn(B, Hq, D, generator=gen, device=device).to(dtype)
+        self.lengths = torch.full((B,), context, dtype=torch.int64, device=device)
+
+        pages, _, _ = rk.quest_batched(self.q, mn, mx, self.lengths, P, self.top_pages)
+        pages = pages.cpu()
+        rng = torch.Generator().manual_seed(seed + 1)
+        hot_blocks = self.H // P
+        per_req_blocks = hot_blocks + self.resident_pages
+        self.pool = torch.empty(B * per_req_blocks, 2, P, Hkv, D, dtype=dtype, device=device)
+        source = torch.arange(B * n_pages, dtype=torch.int32).view(B, n_pages)
+        resident = torch.full((B, n_pages), -1, dtype=torch.int32)
+        hot = torch.empty(B, hot_blocks, dtype=torch.int32)
+        tags = torch.full((B, self.H), -1, dtype=torch.int32)
+        lru = torch.empty(B, self.H, dtype=torch.int64)
+        self.classes = []
+        for b in range(B):
+            sel = pages[b].tolist()
+            tail = [p for p in sel if p >= n_pages - 2]
+            rest = [p for p in sel if p < n_pages - 2]
+            order = [rest[i] for i in torch.randperm(len(rest), generator=rng).tolist()]
+            res_pages = tail + order[: self.resident_pages - len(tail)]
+            hot_pg = order[self.resident_pages - len(tail) : self.resident_pages - len(tail) + self.hot_pages]
+            miss_pg = order[self.resident_pages - len(tail) + self.hot_pages :]
+            self.classes.append((res_pages, hot_pg, miss_pg))
+            base = b * per_req_blocks
+            hot[b] = torch.arange(base, base + hot_blocks, dtype=torch.int32)
+            for i, p in enumerate(res_pages):
+                blk = base + hot_blocks + i
+                resident[b, p] = blk
+                self.pool[blk].copy_(self.host[b * n_pages + p])
+            # hot rows of the hot-hit pages at random slots; every other slot
+            # holds a row of some unselected, non-resident page
+            slots = torch.randperm(self.H, generator=rng)
+            wanted = torch.tensor([(b * n_pages + p) * P + o for p in hot_pg for o in range(P)], dtype=torch.int32)
+            selected = set(sel)
+            others = torch.tensor([p for p in range(n_pages) if p not in selected], dtype=torch.int64)
+            filler_pages = others[torch.randperm(others.numel(), generator=rng)]
+            filler = (b * n_pages + filler_pages[:, None]) * P + torch.arange(P)
+            filler = filler.flatten()[: self.H - wanted.numel()].to(torch.int32)
+            tags[b, slots[: wanted.numel()]] = wanted
+            tags[b, slots[wanted.numel() :]] = filler
+            lru[b] = torch.randperm(self.H, generator=rng)
+            # load the hot rows' contents into their hot-buffer rows
+            for s in slots[: wanted.numel()].tolist():
+                host_row = int(tags[b, s])
+                hb, ho = divmod(host_row, P)
+                db = int(hot[b, s // P])
+                self.pool[db, :, s % P].copy_(self.host[hb, :, ho])
+        self.source = source.to(device)
+        self.resident = resident.to(device)
+        self.hot = hot.to(device)
+        self.tags0, self.lru0 = tags.to(device), lru.to(device)
+        self.tags, self.lru = self.tags0.clone(), self.lru0.clone()
+        self.alias = rk.MappedHost(self.host)
+        self.out = torch.empty(B, Hq, D, dtype=dtype, device=device)
+        self.workspace = None
+        self.row_bytes = 2 * Hkv * D * 2
+        self.selected_pages = pages
+
+    # algorithmic bytes per launch (one decode step of one layer for the batch)
+    def attention_bytes(self, valid_rows):
+        return valid_rows * self.row_bytes + self.batch * (2 * self.q_heads * self.head_dim * 2 + 8 * self.K)
+
+    def quest_bytes(self):
+        return self.batch * (self.n_pages * self.kv_heads * self.head_dim * 2 * 2 + self.q_heads * self.head_dim * 2)
+
+
+def run_step(w, rk, compute, transfer, events=None):
+    """One sparse decode step; `events` (dict of name -> (start, end)) are
+    recorded on the stream each kernel runs on."""
+    import torch
+
+    def ev(name, stream, which):
+        if events is not None:
+            events[name][which].record(stream)
+
+    w.tags.copy_(w.tags0)
+    w.lru.copy_(w.lru0)
+    ev("quest", compute, 0)
+    _, positions, _ = rk.quest_batched(w.q, w.minimum, w.maximum, w.lengths, w.page, w.top_pages)
+    ev("quest", compute, 1)
+    ev("resolve", compute, 0)
+    physical, miss_host, miss_dev, counts = rk.resolve_batched(
+        positions, w.source, w.resident, w.hot, w.tags, w.lru, w.lengths, w.page
+    )
+    ev("resolve", compute, 1)
+    resolved = torch.cuda.Event()
+    resolved.record(compute)
+    transfer.wait_event(resolved)
+    with torch.cuda.stream(transfer):
+        ev("gather", transfer, 0)
+        rk.gather_plan(w.alias, w.pool, miss_host, miss_dev, w.page)
+        ev("gather", transfer, 1)
+    gathered = torch.cuda.Event()
+    gathered.record(transfer)
+    compute.wait_event(gathered)
+    miss_host.record_stream(transfer)
+    miss_dev.record_stream(transfer)
+    ev("attention", compute, 0)
+    rk.attend_batched(w.q, w.pool, physical, w.page, out=w.out, workspace=w.workspace)
+    ev("attention", compute, 1)
+    return physical, counts
+
+
+def cpu_baseline(w, steps):
+    """The C oracle (single-threaded port of the reference CPU path) on the
+    same inputs: Quest select, resolve, gather, attention for the batch."""
+    import numpy as np
+    import torch
+
+    import oracle
+
+    q = w.q.cpu()
+    mn, mx = w.minimum.cpu(), w.maximum.cpu()
+    lengths = w.lengths.cpu()
+    pool = w.pool.cpu()
+    source, resident, hot = w.source.cpu().numpy(), w.resident.cpu().numpy(), w.hot.cpu().numpy()
+    tags0 = w.tags0.cpu().numpy().astype(np.int64)
+    lru0 = w.lru0.cpu().numpy()
+    times = []
+    physical = None
+    for _ in range(steps):
+        tags, lru = tags0.copy(), lru0.copy()
+        t0 = time.perf_counter()
+        _, _, positions = oracle.quest_select(q, mn, mx, lengths, w.page, w.top_pages)
+        positions = positions.numpy()
+        physical = np.empty((w.batch, w.K), np.int64)
+        mhs, mds = [], []
+        for b in range(w.batch):
+            ph, mh, md, _ = oracle.resolve_rows(
+                positions[b], source[b], resident[b], hot[b], tags[b], lru[b], int(lengths[b]), w.page
+            )
+            physical[b] = ph
+            mhs.append(mh)
+            mds.append(md)
+        oracle.gather_rows(w.host, pool, np.concatenate(mhs), np.concatenate(mds), w.page)
+        oracle.attend_rows(q, pool, torch.from_numpy(physical), w.page)
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), physical
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the sparse decode step shards by "
+            "request with no exchange, so the N-GPU figure would be N independent copies of this one)",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    import torch
+
+    from nano_hisparse import _hip
+    from nano_hisparse import row_kernels as rk
+
+    _hip.load()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    print(f"[bench] building workload batch={args.batch} context={args.context}", file=sys.stderr, flush=True)
+    w = Workload(args.batch, args.context, args.seed, device)
+    w.workspace = torch.empty(
+        _hip.load().nhs_attend_workspace_bytes(w.batch, w.q_heads, w.head_dim, w.K), dtype=torch.uint8, device=device
+    )
+    compute = torch.cuda.current_stream(device)
+    transfer = torch.cuda.Stream(device=device)
+
+    names = ("quest", "resolve", "gather", "attention")
+    for _ in range(args.warmup):
+        physical, counts = run_step(w, rk, compute, transfer)
+    torch.cuda.synchronize()
+    counts_sum = counts.sum(0).tolist()
+    valid_rows = int((physical >= 0).sum())
+    print(f"[bench] counts resident/hot/miss = {counts_sum}, valid rows {valid_rows}", file=sys.stderr, flush=True)
+
+    # timed region: K steps, synchronized on both sides
+    per_step = [{n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for n in names}
+                for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record(compute)
+    for i in range(args.steps):
+        run_step(w, rk, compute, transfer, per_step[i])
+    end.record(compute)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    kernel_us = {n: 1e3 * sum(e[n][0].elapsed_time(e[n][1]) for e in per_step) / args.steps for n in names}
+
+    # measured pinned H2D copy ceiling (copy engine), for reference
+    probe = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(probe.shape, dtype=torch.uint8, device=device)
+    dst.copy_(probe, non_blocking=True)
+    torch.cuda.synchronize()
+    h2d = []
+    for _ in range(3):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        dst.copy_(probe, non_blocking=True)
+        b.record()
+        torch.cuda.synchronize()
+        h2d.append(probe.numel() / (a.elapsed_time(b) * 1e-3))
+    del probe, dst
+
+    attn_bytes = w.attention_bytes(valid_rows)
+    gather_bytes = counts_sum[2] * w.row_bytes
+    tokens_per_s = w.batch / (ms_per_step * 1e-3)
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "sparse decode step of one layer (quest select + resolve + host-row gather + attention), "
+            "Llama-3-8B heads 32q/8kv/128, bf16, page 64, 32 pages = 2048 rows selected of 32768, "
+            "selected pages 50% resident / 25% hot / 25% host misses, hot rows 4096 per request",
+            "batch": w.batch,
+            "context": w.context,
+            "parallelism": "single GPU",
+        },
+        "step_us": round(ms_per_step * 1e3, 2),
+        "kernel_us": {n: round(v, 2) for n, v in kernel_us.items()},
+        "roofline": {
+            "kernel": "nhs_attend_rows (attend_split_kernel + attend_combine_kernel)",
+            "bound": "hbm",
+            "achieved": round(attn_bytes / (kernel_us["attention"] * 1e-6) / 1e9, 1),
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(attn_bytes / (kernel_us["attention"] * 1e-6) / HBM_PEAK, 4),
+            "traffic": None,
+            "algorithmic_bytes": attn_bytes,
+        },
+        "gather_roofline": {
+            "kernel": "nhs_gather_rows (gather_rows_kernel)",
+            "bound": "pcie",
+            "achieved": round(gather_bytes / (kernel_us["gather"] * 1e-6) / 1e9, 2),
+            "peak": PCIE_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(gather_bytes / (kernel_us["gather"] * 1e-6) / PCIE_PEAK, 4),
+            "measured_h2d_copy_gbs": round(max(h2d) / 1e9, 2),
+            "algorithmic_bytes": gather_bytes,
+        },
+        "quest_gbs": round(w.quest_bytes() / (kernel_us["quest"] * 1e-6) / 1e9, 1),
+        "wall_s_timed": round(wall, 3),
+    }
+    if args.cpu_steps > 0:
+        print(f"[bench] CPU oracle baseline, {args.cpu_steps} steps", file=sys.stderr, flush=True)
+        cpu_s, cpu_physical = cpu_baseline(w, args.cpu_steps)
+        if not (torch.from_numpy(cpu_physical) == physical.cpu()).all():
+            raise RuntimeError("GPU resolved rows differ from the CPU oracle")
+        result["cpu_baseline"] = {
+            "value": round(w.batch / cpu_s, 2),
+            "unit": "tokens/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"{args.cpu_steps} full steps of the same workload (median step {cpu_s:.3f} s)",
+        }
+        try:
+            model = subprocess.run(["bash", "-c", "lscpu | grep 'Model name' | head -1"], capture_output=True,
+                                   text=True).stdout.split(":")[-1].strip()
+        except OSError:
+            model = ""
+        result["cpu_baseline"]["host"] = f"{model} ({os.cpu_count()} CPUs visible)"
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

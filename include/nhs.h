@@ -1,0 +1,171 @@
+/*
+ * nhs.h - C ABI of the MI355X (gfx950) sparse-decode library, libnhs_hip.so.
+ *
+ * Every entry point takes plain device pointers, element counts and strides
+ * (in elements, not bytes, unless the name says bytes), enqueues its kernels
+ * on the given hipStream_t (passed as void*; NULL means the null stream) and
+ * returns an int status without synchronising. No entry point allocates
+ * device or host memory: the caller owns every buffer, including workspaces,
+ * whose size is returned by the matching *_workspace_bytes function. All
+ * kernels are capturable in a HIP graph (no host readback, no memset nodes).
+ *
+ * Status: NHS_OK (0) on success, a negative NHS_ERR_* for an argument the
+ * library rejects before launching anything, or a positive hipError_t from
+ * the launch. nhs_last_error() returns a message for the last failure on the
+ * calling thread.
+ *
+ * Memory layouts (shared with the Python side):
+ *   pool  [blocks, 2, page_size, kv_heads, head_dim]   K plane 0, V plane 1
+ *   host  [host_pages, 2, page_size, kv_heads, head_dim] (pinned, same layout)
+ *   A physical row r lives in block r / page_size at offset r % page_size;
+ *   its K bytes and its V bytes are each kv_heads*head_dim contiguous elements.
+ */
+#ifndef NHS_H
+#define NHS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  NHS_OK = 0,
+  NHS_ERR_INVALID = -1,     /* argument out of range or inconsistent */
+  NHS_ERR_UNSUPPORTED = -2, /* no kernel for this shape / dtype */
+  NHS_ERR_WORKSPACE = -3    /* caller workspace smaller than required */
+};
+
+/* Element types for pools, host KV, queries, bounds and outputs. */
+enum { NHS_F32 = 0, NHS_F16 = 1, NHS_BF16 = 2 };
+
+/* Library limits (checked; exceeding one returns NHS_ERR_UNSUPPORTED). */
+#define NHS_MAX_POSITIONS 4096   /* resolver: selected positions per item */
+#define NHS_MAX_HOT_ROWS 32768   /* resolver: hot rows per item (hybrid.py:36) */
+#define NHS_MAX_SELECT_PAGES 16384 /* selectors: pages scored per request */
+
+int nhs_abi_version(void);
+const char* nhs_last_error(void);
+
+/*
+ * Device alias of pinned host memory allocated by hipHostMalloc (torch's
+ * pin_memory=True). The library never registers or unregisters memory.
+ * Replaces MappedHost, nano_hisparse/row_kernels.py:10-32 (a libcuda
+ * cuPointerGetAttribute call through ctypes).
+ */
+int nhs_host_device_ptr(const void* pinned_host, void** device_alias);
+
+/*
+ * Host-row gather: for each plan entry i in [0, n_entries) with
+ * miss_host_rows[i] >= 0 and miss_device_rows[i] >= 0, copy the K plane row
+ * and the V plane row (plane_bytes = kv_heads*head_dim*element_size each)
+ * from host row miss_host_rows[i] to pool row miss_device_rows[i]. Plans of
+ * several requests may be concatenated. Rows are copied with coalesced
+ * 16-byte loads from the host alias over PCIe. plane_bytes must be a
+ * multiple of 4.
+ * Replaces _gather / gather_rows, nano_hisparse/row_kernels.py:35-70
+ * (CPU twin nano_hisparse/hybrid.py:452-459).
+ */
+int nhs_gather_rows(const void* host_alias, void* pool,
+                    const int64_t* miss_host_rows, const int64_t* miss_device_rows,
+                    int64_t n_entries, int32_t page_size, int64_t plane_bytes,
+                    void* stream);
+
+/*
+ * Physical-row GQA decode attention, split-K over rows with an online
+ * softmax and a combine pass. For request b and query head h (kv head
+ * h / (q_heads / kv_heads)):
+ *   out[b,h] = softmax_r(q[b,h] . K[row] * head_dim^-0.5) . V[row]
+ * over the rows rows[b, h, c] >= 0 (c < n_rows); rows < 0 are masked and a
+ * head with no valid row yields zeros. rows_head_stride == 0 means every
+ * query head of a request shares one row list (the default shared
+ * selection); otherwise each head has its own list. Accumulation is fp32;
+ * out has the query's dtype. head_dim*kv element size must be a multiple of
+ * 16 bytes and at most 1024 bytes.
+ * Replaces _attend / attend_rows, nano_hisparse/row_kernels.py:73-135 (torch
+ * twin nano_hisparse/attention.py:26-35).
+ */
+int64_t nhs_attend_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_dim,
+                                   int32_t n_rows);
+int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                    int64_t q_head_stride, const void* pool, int32_t kv_dtype,
+                    const int64_t* rows, int64_t rows_batch_stride, int64_t rows_head_stride,
+                    int64_t rows_col_stride, int32_t batch, int32_t n_rows, int32_t q_heads,
+                    int32_t kv_heads, int32_t head_dim, int32_t page_size, void* out,
+                    int64_t out_batch_stride, int64_t out_head_stride, void* workspace,
+                    int64_t workspace_bytes, void* stream);
+
+/*
+ * Row resolver for `batch` independent (request, layer) items, one
+ * workgroup each, with no host round trip. Item b reads positions[b, :n]
+ * (int32 or int64 per positions_i64), its page tables source/resident
+ * [n_pages] and hot block table hot[ceil(hot_rows/page_size)], and updates
+ * its row tags[hot_rows] (int32, -1 empty) and LRU permutation
+ * lru[hot_rows] (int64) in place. It writes physical[b, :n] (input order,
+ * -1 for padding, duplicates and rows without host backing),
+ * miss_host[b, :n] / miss_device[b, :n] (compact prefix in ascending
+ * logical order, then -1) and counts[b, 0:3] = unique resident hits, hot
+ * hits, misses; counts_total[0:3] (may be NULL) is incremented by them.
+ * lengths[b] (int64, may be NULL to use `length` for every item) is the
+ * causal length. Bit-exact with resolve_rows,
+ * nano_hisparse/row_index.py:62-140.
+ */
+int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t positions_i64,
+                     int64_t positions_stride, const int32_t* source, const int32_t* resident,
+                     int64_t page_table_stride, int32_t n_pages, const int32_t* hot,
+                     int64_t hot_stride, int32_t* tags, int64_t tags_stride, int64_t* lru,
+                     int64_t lru_stride, int32_t hot_rows, const int64_t* lengths,
+                     int64_t length, int32_t page_size, int64_t* physical, int64_t* miss_host,
+                     int64_t* miss_device, int64_t plan_stride, int64_t* counts,
+                     int64_t* counts_total, void* stream);
+
+/*
+ * Quest page selection for `batch` requests. Request b scores each of its
+ * count = ceil(lengths[b]/page_size) pages (count is clamped to max_pages):
+ *   score[p] = (sum_h sum_d max(q[h,d]*min[p,h/g,d], q[h,d]*max[p,h/g,d])) / q_heads
+ * in fp32 with a fixed summation order (per lane: sequential over its 16
+ * bytes of bound elements; across lanes: pairwise tree; across heads:
+ * sequential h = 0..q_heads-1). Page count-1, and page 0 when keep_sink and
+ * top_pages > 1 and count > 1, score +inf. The top_pages pages by (score
+ * descending, page ascending) are written ascending to pages[b, :top_pages]
+ * (-1 padded when count < top_pages) and expanded to causal token positions
+ * positions[b, :top_pages*page_size] (ascending, -1 padded). scores[b, :]
+ * (max_pages floats) is scratch that keeps the scores.
+ * minimum/maximum are [max_pages, kv_heads, head_dim] per request.
+ * Replaces quest_selection, nano_hisparse/selection.py:69-91.
+ */
+int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                     int64_t q_head_stride, const void* minimum, const void* maximum,
+                     int32_t bounds_dtype, int64_t bounds_batch_stride, int32_t q_heads,
+                     int32_t kv_heads, int32_t head_dim, const int64_t* lengths, int64_t length,
+                     int32_t page_size, int32_t max_pages, int32_t top_pages, int32_t keep_sink,
+                     float* scores, int32_t* pages, int32_t* positions, void* stream);
+
+/*
+ * Page-mean selection ("mean" selector) for `batch` requests: the query is
+ * averaged over each GQA group, dotted with the fp32 per-page mean keys
+ * summaries[p, kv_heads, head_dim], pages {0, count-1} ({count-1} when
+ * top_pages == 1) are always kept and the best top_pages - |kept| other
+ * pages (score descending, page ascending) are added. Output layout as in
+ * nhs_quest_select. Replaces select_pages, nano_hisparse/selection.py:119-145.
+ */
+int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                    int64_t q_head_stride, const float* summaries, int64_t summaries_batch_stride,
+                    int32_t q_heads, int32_t kv_heads, int32_t head_dim, const int64_t* lengths,
+                    int64_t length, int32_t page_size, int32_t max_pages, int32_t top_pages,
+                    float* scores, int32_t* pages, int32_t* positions, void* stream);
+
+/*
+ * Legacy per-head selections: out[h, c] = columns[h, c] in [0, n) ?
+ * shared_rows[columns[h, c]] : -1 for h < heads, c < width.
+ * Replaces the head_columns branch of resolve_rows,
+ * nano_hisparse/row_index.py:130-134.
+ */
+int nhs_expand_columns(const int64_t* shared_rows, int64_t n, const int64_t* columns,
+                       int64_t heads, int64_t width, int64_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NHS_H */

@@ -1,0 +1,104 @@
+// Host-row gather: copies missed KV rows from pinned host memory (read by the
+// compute units through the host alias, over PCIe) into hot-buffer rows of
+// the device pool. A row is two planes (K and V) of plane_bytes each; in both
+// the host and the pool layout a block is [2, page_size, kv_heads, head_dim],
+// so plane `pl` of row r starts at ((r/P)*2*P + pl*P + r%P) * plane_bytes.
+//
+// Each workgroup takes kRowsPerBlock consecutive plan entries. A thread owns
+// vector column c of every plane and issues the loads of all its rows before
+// the stores, so each lane keeps kRowsPerBlock 16-byte PCIe reads in flight.
+// Plan entries past a request's misses are -1; a workgroup whose entries are
+// all -1 returns after reading them.
+#include "nhs_common.h"
+
+namespace nhs {
+
+constexpr int kGatherThreads = 256;
+constexpr int kRowsPerBlock = 8;
+
+template <typename V>
+__global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char* __restrict__ host,
+                                                                     char* __restrict__ pool,
+                                                                     const int64_t* __restrict__ miss_host,
+                                                                     const int64_t* __restrict__ miss_dev,
+                                                                     int64_t n_entries, int page_size,
+                                                                     int64_t plane_bytes) {
+  __shared__ int64_t src_base[kRowsPerBlock];
+  __shared__ int64_t dst_base[kRowsPerBlock];
+  __shared__ int live;
+  const int64_t first = (int64_t)blockIdx.x * kRowsPerBlock;
+  const int64_t block_bytes = 2 * (int64_t)page_size * plane_bytes;
+  if (threadIdx.x == 0) live = 0;
+  __syncthreads();
+  if (threadIdx.x < kRowsPerBlock) {
+    int64_t i = first + threadIdx.x;
+    int64_t s = -1, d = -1;
+    if (i < n_entries) {
+      s = miss_host[i];
+      d = miss_dev[i];
+    }
+    if (s >= 0 && d >= 0) {
+      src_base[threadIdx.x] = (s / page_size) * block_bytes + (s % page_size) * plane_bytes;
+      dst_base[threadIdx.x] = (d / page_size) * block_bytes + (d % page_size) * plane_bytes;
+      atomicAdd(&live, 1);
+    } else {
+      src_base[threadIdx.x] = -1;
+      dst_base[threadIdx.x] = -1;
+    }
+  }
+  __syncthreads();
+  if (live == 0) return;
+
+  int64_t sb[kRowsPerBlock], db[kRowsPerBlock];
+#pragma unroll
+  for (int r = 0; r < kRowsPerBlock; ++r) {
+    sb[r] = src_base[r];
+    db[r] = dst_base[r];
+  }
+  const int vecs_per_plane = (int)(plane_bytes / (int64_t)sizeof(V));
+  const int64_t plane_stride = (int64_t)page_size * plane_bytes;
+  for (int c = threadIdx.x; c < 2 * vecs_per_plane; c += kGatherThreads) {
+    const int plane = c >= vecs_per_plane;
+    const int64_t off = plane * plane_stride + (int64_t)(c - plane * vecs_per_plane) * (int64_t)sizeof(V);
+    V buf[kRowsPerBlock];
+#pragma unroll
+    for (int r = 0; r < kRowsPerBlock; ++r)
+      if (sb[r] >= 0) buf[r] = *reinterpret_cast<const V*>(host + sb[r] + off);
+#pragma unroll
+    for (int r = 0; r < kRowsPerBlock; ++r)
+      if (db[r] >= 0) *reinterpret_cast<V*>(pool + db[r] + off) = buf[r];
+  }
+}
+
+}  // namespace nhs
+
+extern "C" int nhs_gather_rows(const void* host_alias, void* pool, const int64_t* miss_host_rows,
+                               const int64_t* miss_device_rows, int64_t n_entries, int32_t page_size,
+                               int64_t plane_bytes, void* stream) {
+  using namespace nhs;
+  if (!host_alias || !pool || !miss_host_rows || !miss_device_rows)
+    return fail(NHS_ERR_INVALID, "nhs_gather_rows: null pointer");
+  if (n_entries < 0 || page_size < 1 || plane_bytes < 4 || plane_bytes % 4)
+    return fail(NHS_ERR_INVALID, "nhs_gather_rows: need n_entries >= 0, page_size >= 1, plane_bytes a multiple of 4");
+  if (n_entries == 0) return NHS_OK;
+  if (plane_bytes / 4 > 0x3fffffff) return fail(NHS_ERR_UNSUPPORTED, "nhs_gather_rows: rows too wide");
+  const uintptr_t align = (uintptr_t)host_alias | (uintptr_t)pool;
+  const int64_t blocks = (n_entries + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (blocks > 0x7fffffff) return fail(NHS_ERR_UNSUPPORTED, "nhs_gather_rows: too many plan entries");
+  hipStream_t s = (hipStream_t)stream;
+  if (plane_bytes % 16 == 0 && align % 16 == 0) {
+    hipLaunchKernelGGL(gather_rows_kernel<uint4>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s,
+                       (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size,
+                       plane_bytes);
+  } else if (plane_bytes % 8 == 0 && align % 8 == 0) {
+    hipLaunchKernelGGL(gather_rows_kernel<uint2>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s,
+                       (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size,
+                       plane_bytes);
+  } else {
+    if (align % 4) return fail(NHS_ERR_INVALID, "nhs_gather_rows: host and pool must be 4-byte aligned");
+    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s,
+                       (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size,
+                       plane_bytes);
+  }
+  return launch_status("nhs_gather_rows");
+}

@@ -1,0 +1,439 @@
+// Row resolver: logical token positions -> physical pool rows, with resident
+// lookup, hot-row lookup and LRU miss assignment, for `batch` independent
+// (request, layer) items in one launch (one 1024-thread workgroup per item).
+//
+// The semantics are those of resolve_rows (nano_hisparse/row_index.py:62-140),
+// restated as LDS passes instead of sorts over the hot rows:
+//  1. keys (norm << 32 | input index), norm = raw if 0 <= raw < length else
+//     length, bitonic-sorted in LDS: sorted order = ascending logical, and
+//     the first entry of each run of equal positions is its first occurrence
+//     in the input.
+//  2. per sorted entry: page/offset, source and resident tables, host row,
+//     valid / resident_hit / needs_hot.
+//  3. an LDS hash of the host rows that need the hot buffer.
+//  4. one coalesced pass over tags: a tag found in the hash is a hot hit for
+//     that host row and marks its slot protected.
+//  5. victims = lru stably partitioned (unprotected first): the lru values
+//     are staged in LDS and ranked in 1024-slot chunks with wave ballots.
+//  6. miss ranks by a block scan; assigned slot = victims[rank].
+//  7. physical rows (scattered back to input order), compact miss plan, tag
+//     writes for misses, counts.
+//  8. lru stably partitioned by category (untouched, inserted, hit), ranked
+//     the same way.
+#include "nhs_common.h"
+
+namespace nhs {
+
+constexpr int kResolveThreads = 1024;
+constexpr int kMaxK = NHS_MAX_POSITIONS;          // sorted entries per item
+constexpr int kMaxH = NHS_MAX_HOT_ROWS;           // hot rows per item
+constexpr int kKPerThread = kMaxK / kResolveThreads;  // 4
+constexpr int kHashCap = 2 * kMaxK;                // load factor <= 1/2
+
+struct ResolveArgs {
+  int n;  // positions per item
+  const void* positions;
+  int positions_i64;
+  int64_t positions_stride;
+  const int32_t* source;
+  const int32_t* resident;
+  int64_t page_stride;
+  int n_pages;
+  const int32_t* hot;
+  int64_t hot_stride;
+  int32_t* tags;
+  int64_t tags_stride;
+  int64_t* lru;
+  int64_t lru_stride;
+  int hot_rows;
+  const int64_t* lengths;
+  int64_t length;
+  int page_size;
+  FastDiv page_div;
+  int64_t* physical;
+  int64_t* miss_host;
+  int64_t* miss_device;
+  int64_t plan_stride;
+  int64_t* counts;
+  int64_t* counts_total;
+};
+
+struct ResolveShared {
+  union {
+    uint64_t keys[kMaxK];  // phase 1-2
+    struct {
+      int32_t hkey[kHashCap];  // phase 3-4: wanted host rows
+      int32_t hslot[kHashCap]; // hot slot holding that host row, or -1
+    } hash;
+    uint16_t lru16[kMaxH];     // phase 5-8: the item's lru, staged
+  } u;
+  uint32_t prot[kMaxH / 32];  // protected slot bits
+  uint32_t ins[kMaxH / 32];   // inserted slot bits
+  int32_t victims[kMaxK];     // victims[0 .. min(n, H)-1]
+  int64_t scan64[kResolveThreads / 64 + 1];
+  int32_t wcount[2][kResolveThreads / 64][4];  // per-wave category counts, double-buffered
+};
+
+// Ranks within one 1024-slot chunk: for category `cat` (0..3, or -1 for an
+// empty slot) returns the number of lower threads of the block with the same
+// category and writes the chunk's per-category totals to tot[4]. One barrier;
+// the count table alternates between two buffers, so a buffer is rewritten
+// only after every thread has passed the next chunk's barrier.
+__device__ __forceinline__ int chunk_rank(int cat, int32_t (*wcount)[kResolveThreads / 64][4], int parity,
+                                          int* tot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  int mine = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    uint64_t m = __ballot(cat == c);
+    if (cat == c) mine = __popcll(m & lt);
+    if (lane == 0) wcount[parity][wave][c] = __popcll(m);
+  }
+  __syncthreads();
+  int before = 0;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) tot[c] = 0;
+#pragma unroll 1
+  for (int w = 0; w < kResolveThreads / 64; ++w) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      int v = wcount[parity][w][c];
+      tot[c] += v;
+      if (w < wave && c == cat) before += v;
+    }
+  }
+  return before + mine;
+}
+
+__device__ __forceinline__ uint32_t hash_row(int32_t key) { return (uint32_t)key * 2654435761u; }
+
+__device__ __forceinline__ int hash_find(const int32_t* hkey, int32_t key) {
+  uint32_t h = hash_row(key) & (kHashCap - 1);
+  while (true) {
+    int32_t k = hkey[h];
+    if (k == key) return (int)h;
+    if (k == -1) return -1;
+    h = (h + 1) & (kHashCap - 1);
+  }
+}
+
+__global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveArgs a) {
+  __shared__ ResolveShared sh;
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int n = a.n;
+  const int H = a.hot_rows;
+  const int P = a.page_size;
+  const int64_t length = a.lengths ? a.lengths[b] : a.length;
+  int kp = 1;
+  while (kp < n) kp <<= 1;
+
+  // ---- 1. keys and bitonic sort -------------------------------------------
+  for (int i = tid; i < kp; i += kResolveThreads) {
+    uint64_t key = ~0ull;
+    if (i < n) {
+      int64_t raw = a.positions_i64
+                        ? static_cast<const int64_t*>(a.positions)[(int64_t)b * a.positions_stride + i]
+                        : (int64_t) static_cast<const int32_t*>(a.positions)[(int64_t)b * a.positions_stride + i];
+      int64_t norm = (raw >= 0 && raw < length) ? raw : length;
+      key = ((uint64_t)norm << 32) | (uint32_t)i;
+    }
+    sh.u.keys[i] = key;
+  }
+  __syncthreads();
+  for (int k = 2; k <= kp; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = tid; i < kp; i += kResolveThreads) {
+        int ixj = i ^ j;
+        if (ixj > i) {
+          uint64_t x = sh.u.keys[i], y = sh.u.keys[ixj];
+          bool up = (i & k) == 0;
+          if ((x > y) == up) {
+            sh.u.keys[i] = y;
+            sh.u.keys[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- 2. per sorted entry (thread owns a contiguous run of entries) -------
+  const int per = (n + kResolveThreads - 1) / kResolveThreads;  // <= kKPerThread
+  const int j0 = tid * per;
+  int64_t host[kKPerThread];
+  int32_t in_idx[kKPerThread], res_blk[kKPerThread], off[kKPerThread];
+  bool run_start[kKPerThread], rhit[kKPerThread], nhot[kKPerThread];
+#pragma unroll
+  for (int q = 0; q < kKPerThread; ++q) {
+    int j = j0 + q;
+    rhit[q] = nhot[q] = run_start[q] = false;
+    host[q] = -1;
+    in_idx[q] = 0;
+    res_blk[q] = -1;
+    off[q] = 0;
+    if (q < per && j < n) {
+      uint64_t key = sh.u.keys[j];
+      int64_t lg = (int64_t)(key >> 32);
+      in_idx[q] = (int32_t)(key & 0xffffffffu);
+      run_start[q] = j == 0 || (int64_t)(sh.u.keys[j - 1] >> 32) != lg;
+      bool unique = lg < length && run_start[q];
+      // Positions are < 2^31 (int32 host tags); page = min(lg / P, n_pages - 1).
+      uint32_t pg = a.page_div.div((uint32_t)lg);
+      int32_t o = (int32_t)((uint32_t)lg - pg * (uint32_t)P);
+      int64_t page = pg < (uint32_t)(a.n_pages - 1) ? (int64_t)pg : (int64_t)(a.n_pages - 1);
+      int64_t src = a.source[(int64_t)b * a.page_stride + page];
+      int64_t res = a.resident[(int64_t)b * a.page_stride + page];
+      off[q] = o;
+      host[q] = src * P + o;
+      bool valid = unique && src >= 0;
+      rhit[q] = valid && res >= 0;
+      nhot[q] = valid && !rhit[q];
+      res_blk[q] = (int32_t)res;
+    }
+  }
+  __syncthreads();  // keys are dead from here on; the union becomes the hash
+
+  // ---- 3. hash of host rows that need the hot buffer -----------------------
+  for (int i = tid; i < kHashCap; i += kResolveThreads) {
+    sh.u.hash.hkey[i] = -1;
+    sh.u.hash.hslot[i] = -1;
+  }
+  for (int i = tid; i < kMaxH / 32; i += kResolveThreads) {
+    sh.prot[i] = 0u;
+    sh.ins[i] = 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kKPerThread; ++q) {
+    if (!nhot[q]) continue;
+    int32_t key = (int32_t)host[q];
+    uint32_t h = hash_row(key) & (kHashCap - 1);
+    while (true) {
+      int32_t prev = atomicCAS(&sh.u.hash.hkey[h], -1, key);
+      if (prev == -1 || prev == key) break;
+      h = (h + 1) & (kHashCap - 1);
+    }
+  }
+  __syncthreads();
+
+  // ---- 4. scan tags: hot hits and protected slots ---------------------------
+  int32_t* tags = a.tags + (int64_t)b * a.tags_stride;
+  for (int s = tid; s < H; s += kResolveThreads) {
+    int32_t t = tags[s];
+    if (t >= 0) {
+      int h = hash_find(sh.u.hash.hkey, t);
+      if (h >= 0) {
+        sh.u.hash.hslot[h] = s;
+        atomicOr(&sh.prot[s >> 5], 1u << (s & 31));
+      }
+    }
+  }
+  __syncthreads();
+
+  bool hhit[kKPerThread], miss[kKPerThread];
+  int32_t slot[kKPerThread];
+  int local_miss = 0;
+#pragma unroll
+  for (int q = 0; q < kKPerThread; ++q) {
+    hhit[q] = miss[q] = false;
+    slot[q] = 0;
+    if (nhot[q]) {
+      int h = hash_find(sh.u.hash.hkey, (int32_t)host[q]);
+      int32_t es = sh.u.hash.hslot[h];
+      hhit[q] = es >= 0;
+      miss[q] = !hhit[q];
+      slot[q] = es;
+      local_miss += miss[q];
+    }
+  }
+
+  // ---- 5. victims: lru stably partitioned, unprotected slots first ---------
+  __syncthreads();  // the hash is dead; the union now stages the lru
+  const int64_t* lru_in = a.lru + (int64_t)b * a.lru_stride;
+  for (int r = tid; r < H; r += kResolveThreads) {
+    int64_t v = lru_in[r];  // a permutation of [0, H); clamped so bad input stays in bounds
+    sh.u.lru16[r] = (uint16_t)(v < 0 ? 0 : v >= H ? H - 1 : v);
+  }
+  int local_prot = 0;
+  for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) local_prot += __popc(sh.prot[i]);
+  const int64_t n_prot = block_sum<int64_t>(local_prot, sh.scan64);  // barrier: lru16 staged
+  const int64_t n_unprot = H - n_prot;
+  const int vlimit = n < H ? n : H;
+  auto prot_bit = [&](int v) { return (int)((sh.prot[v >> 5] >> (v & 31)) & 1u); };
+  auto ins_bit = [&](int v) { return (int)((sh.ins[v >> 5] >> (v & 31)) & 1u); };
+  {
+    int64_t base_u = 0, base_p = 0;
+    int parity = 0;
+    for (int c0 = 0; c0 < H; c0 += kResolveThreads, parity ^= 1) {
+      const int r = c0 + tid;
+      int v = r < H ? sh.u.lru16[r] : 0;
+      int cat = r < H ? prot_bit(v) : -1;  // 0 unprotected, 1 protected
+      int tot[4];
+      int within = chunk_rank(cat, sh.wcount, parity, tot);
+      if (cat >= 0) {
+        int64_t rank = cat == 0 ? base_u + within : n_unprot + base_p + within;
+        if (rank < vlimit) sh.victims[rank] = v;
+      }
+      base_u += tot[0];
+      base_p += tot[1];
+    }
+  }
+  __syncthreads();  // victims complete
+
+  // ---- 6. miss ranks ----------------------------------------------------------
+  int64_t n_miss;
+  int64_t miss_before = block_exclusive_scan<int64_t>(local_miss, sh.scan64, &n_miss);
+
+  // ---- 7. physical rows, plan, tag writes, counts ----------------------------
+  int64_t* phys_out = a.physical + (int64_t)b * a.plan_stride;
+  int64_t* mh = a.miss_host + (int64_t)b * a.plan_stride;
+  int64_t* md = a.miss_device + (int64_t)b * a.plan_stride;
+  const int32_t* hot = a.hot + (int64_t)b * a.hot_stride;
+  int local_rhit = 0, local_hhit = 0;
+  {
+    int64_t rank = miss_before;
+#pragma unroll
+    for (int q = 0; q < kKPerThread; ++q) {
+      int j = j0 + q;
+      if (!(q < per && j < n)) continue;
+      int64_t phys = -1;
+      if (rhit[q]) {
+        phys = (int64_t)res_blk[q] * P + off[q];
+        ++local_rhit;
+      } else if (nhot[q]) {
+        int32_t s;
+        if (hhit[q]) {
+          s = slot[q];
+          ++local_hhit;
+        } else {
+          int64_t vr = rank < H - 1 ? rank : H - 1;
+          s = sh.victims[vr];
+        }
+        uint32_t sb = a.page_div.div((uint32_t)s);
+        int64_t hp = (int64_t)hot[sb] * P + (int64_t)((uint32_t)s - sb * (uint32_t)P);
+        phys = hp;
+        if (miss[q]) {
+          mh[rank] = host[q];
+          md[rank] = hp;
+          tags[s] = (int32_t)host[q];
+          atomicOr(&sh.ins[s >> 5], 1u << (s & 31));
+          ++rank;
+        }
+      }
+      phys_out[in_idx[q]] = run_start[q] ? phys : -1;
+    }
+  }
+  for (int i = tid; i < n; i += kResolveThreads)
+    if (i >= n_miss) {
+      mh[i] = -1;
+      md[i] = -1;
+    }
+  int64_t n_rhit = block_sum<int64_t>(local_rhit, sh.scan64);
+  int64_t n_hhit = block_sum<int64_t>(local_hhit, sh.scan64);
+  if (tid == 0) {
+    int64_t* c = a.counts + (int64_t)b * 3;
+    c[0] = n_rhit;
+    c[1] = n_hhit;
+    c[2] = n_miss;
+    if (a.counts_total) {
+      atomicAdd((unsigned long long*)&a.counts_total[0], (unsigned long long)n_rhit);
+      atomicAdd((unsigned long long*)&a.counts_total[1], (unsigned long long)n_hhit);
+      atomicAdd((unsigned long long*)&a.counts_total[2], (unsigned long long)n_miss);
+    }
+  }
+  __syncthreads();  // ins bits complete
+
+  // ---- 8. lru stably partitioned by category ----------------------------------
+  // category = inserted + 2 * protected: 0 untouched, 1 inserted, 2 hit.
+  int local_cnt[4] = {0, 0, 0, 0};
+  for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) {
+    uint32_t in = sh.ins[i], pr = sh.prot[i];
+    uint32_t valid_bits = (i == (H - 1) / 32 && (H & 31)) ? ((1u << (H & 31)) - 1u) : 0xffffffffu;
+    local_cnt[1] += __popc(in & ~pr & valid_bits);
+    local_cnt[2] += __popc(pr & ~in & valid_bits);
+    local_cnt[3] += __popc(in & pr & valid_bits);
+  }
+  int64_t start[4];
+  start[1] = block_sum<int64_t>(local_cnt[1], sh.scan64);
+  start[2] = block_sum<int64_t>(local_cnt[2], sh.scan64);
+  start[3] = block_sum<int64_t>(local_cnt[3], sh.scan64);
+  // start[c] = number of slots in lower categories
+  start[0] = 0;
+  {
+    int64_t n1 = start[1], n2 = start[2], n3 = start[3];
+    int64_t n0 = H - n1 - n2 - n3;
+    start[1] = n0;
+    start[2] = n0 + n1;
+    start[3] = n0 + n1 + n2;
+    (void)n3;
+  }
+  int64_t* lru_out = a.lru + (int64_t)b * a.lru_stride;
+  {
+    int parity = 0;
+    for (int c0 = 0; c0 < H; c0 += kResolveThreads, parity ^= 1) {
+      const int r = c0 + tid;
+      int v = r < H ? sh.u.lru16[r] : 0;
+      int cat = r < H ? ins_bit(v) + 2 * prot_bit(v) : -1;
+      int tot[4];
+      int within = chunk_rank(cat, sh.wcount, parity, tot);
+      if (cat >= 0) {
+        int64_t pos = start[cat] + within;
+        if (pos < H) lru_out[pos] = v;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) start[c] += tot[c];
+    }
+  }
+}
+
+}  // namespace nhs
+
+extern "C" int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t positions_i64,
+                                int64_t positions_stride, const int32_t* source, const int32_t* resident,
+                                int64_t page_table_stride, int32_t n_pages, const int32_t* hot, int64_t hot_stride,
+                                int32_t* tags, int64_t tags_stride, int64_t* lru, int64_t lru_stride,
+                                int32_t hot_rows, const int64_t* lengths, int64_t length, int32_t page_size,
+                                int64_t* physical, int64_t* miss_host, int64_t* miss_device, int64_t plan_stride,
+                                int64_t* counts, int64_t* counts_total, void* stream) {
+  using namespace nhs;
+  if (!positions || !source || !resident || !hot || !tags || !lru || !physical || !miss_host || !miss_device ||
+      !counts)
+    return fail(NHS_ERR_INVALID, "nhs_resolve_rows: null pointer");
+  if (batch < 0 || n < 1 || n_pages < 1 || hot_rows < 1 || page_size < 1)
+    return fail(NHS_ERR_INVALID, "nhs_resolve_rows: need n, n_pages, hot_rows, page_size >= 1");
+  if (n > kMaxK || hot_rows > kMaxH)
+    return fail(NHS_ERR_UNSUPPORTED, "nhs_resolve_rows: n <= %d and hot_rows <= %d required", kMaxK, kMaxH);
+  if (!lengths && (length < 0 || length >= (1ll << 31)))
+    return fail(NHS_ERR_INVALID, "nhs_resolve_rows: length must be in [0, 2^31)");
+  if (batch == 0) return NHS_OK;
+  ResolveArgs a;
+  a.n = n;
+  a.positions = positions;
+  a.positions_i64 = positions_i64;
+  a.positions_stride = positions_stride;
+  a.source = source;
+  a.resident = resident;
+  a.page_stride = page_table_stride;
+  a.n_pages = n_pages;
+  a.hot = hot;
+  a.hot_stride = hot_stride;
+  a.tags = tags;
+  a.tags_stride = tags_stride;
+  a.lru = lru;
+  a.lru_stride = lru_stride;
+  a.hot_rows = hot_rows;
+  a.lengths = lengths;
+  a.length = length;
+  a.page_size = page_size;
+  a.page_div = FastDiv((uint32_t)page_size);
+  a.physical = physical;
+  a.miss_host = miss_host;
+  a.miss_device = miss_device;
+  a.plan_stride = plan_stride;
+  a.counts = counts;
+  a.counts_total = counts_total;
+  hipLaunchKernelGGL(resolve_rows_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0, (hipStream_t)stream, a);
+  return launch_status("nhs_resolve_rows");
+}

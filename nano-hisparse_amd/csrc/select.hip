@@ -1,0 +1,467 @@
+// Page selectors: Quest min/max-bound scoring (selection.py:69-91) and the
+// page-mean selector (selection.py:119-145), each followed by one shared
+// top-k per request, page -> token expansion and -1 padding.
+//
+// Scoring (one wave per page, 4 waves per workgroup): a page's bounds for one
+// KV head are head_dim contiguous elements, read as E-element chunks by
+// `lpr` lanes (a power of two; lanes past head_dim/E contribute +0.0). Every
+// lane sums its chunk sequentially, the lanes of a head are summed by the
+// pairwise DPP tree of group_sum(), and lane 0 of the wave sums the heads
+// sequentially. This order is fixed and restated by the CPU oracle, so the
+// scores and the chosen pages are bit-identical to it. FMA contraction is
+// disabled in this file so that products are rounded before they are added.
+//
+// Selection (one 1024-thread workgroup per request): keys are the scores
+// mapped to order-preserving uint32 (required pages get the maximum key); a
+// 4-pass 8-bit radix select finds the key of the k-th best page, ties at that
+// key go to the lowest page indices (block scan), and the chosen pages are
+// emitted in ascending order (block scan) and expanded to token positions.
+#include <math.h>
+
+#include "nhs_common.h"
+
+#pragma clang fp contract(off)
+
+namespace nhs {
+
+constexpr int kScoreThreads = 256;
+constexpr int kScoreWaves = kScoreThreads / kWave;
+constexpr int kPagesPerBlock = 32;
+constexpr int kSelectThreads = 1024;
+constexpr int kMaxSelectPerThread = NHS_MAX_SELECT_PAGES / kSelectThreads;  // 16
+
+enum { kModeQuest = 0, kModeMean = 1 };
+
+struct ScoreArgs {
+  const void* q;
+  int q_dtype;
+  int64_t q_bs, q_hs;
+  const void* lo;   // quest: minimum; mean: summaries (fp32)
+  const void* hi;   // quest: maximum
+  int64_t b_bs;     // elements between requests' bound tensors
+  int q_heads, kv_heads, head_dim;
+  int lanes_used, lpr_log2;
+  const int64_t* lengths;
+  int64_t length;
+  int page_size, max_pages;
+  float* scores;
+};
+
+__device__ __forceinline__ float torch_maximum(float a, float b) {
+  // torch.maximum propagates NaN from either operand.
+  if (a != a || b != b) return a + b;
+  return a > b ? a : b;
+}
+
+__device__ __forceinline__ int page_count(const int64_t* lengths, int64_t length, int b, int page_size, int max_pages) {
+  int64_t len = lengths ? lengths[b] : length;
+  if (len <= 0) return 0;
+  int64_t c = (len + page_size - 1) / page_size;
+  return (int)(c < max_pages ? c : max_pages);
+}
+
+// Quest bounds score: (sum_h sum_d max(q*min, q*max)) / q_heads.
+template <typename T, int E>
+__global__ __launch_bounds__(kScoreThreads) void quest_score_kernel(ScoreArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ float smem[];
+  float* qs = smem;                                   // [q_heads * head_dim]
+  float* hs = smem + a.q_heads * a.head_dim;          // [waves][q_heads]
+  const int b = blockIdx.y;
+  const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
+  const int p_begin = blockIdx.x * kPagesPerBlock;
+  if (p_begin >= count) return;
+  for (int i = threadIdx.x; i < a.q_heads * a.head_dim; i += kScoreThreads) {
+    int h = i / a.head_dim, d = i - h * a.head_dim;
+    qs[i] = load_elem(a.q, a.q_dtype, (int64_t)b * a.q_bs + (int64_t)h * a.q_hs + d);
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lpr = 1 << a.lpr_log2;
+  const int heads_per_pass = kWave >> a.lpr_log2;
+  const int sub = lane & (lpr - 1);
+  const int group = a.q_heads / a.kv_heads;
+  const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
+  for (int it = 0; it < kPagesPerBlock / kScoreWaves; ++it) {
+    const int p = p_begin + it * kScoreWaves + wave;
+    const bool live = p < count;
+    for (int kh0 = 0; kh0 < a.kv_heads; kh0 += heads_per_pass) {
+      const int kh = kh0 + (lane >> a.lpr_log2);
+      const bool data = live && kh < a.kv_heads && sub < a.lanes_used;
+      float mn[E], mx[E];
+      if (data) {
+        int64_t idx = (int64_t)b * a.b_bs + (int64_t)p * page_elems + (int64_t)kh * a.head_dim + sub * E;
+        load_vec<T, E>(a.lo, idx, mn);
+        load_vec<T, E>(a.hi, idx, mx);
+      }
+      for (int g = 0; g < group; ++g) {
+        const int h = (kh < a.kv_heads ? kh : 0) * group + g;
+        float t = 0.f;
+        if (data) {
+          const float* qh = qs + h * a.head_dim + sub * E;
+          t = torch_maximum(qh[0] * mn[0], qh[0] * mx[0]);
+#pragma unroll
+          for (int e = 1; e < E; ++e) t = t + torch_maximum(qh[e] * mn[e], qh[e] * mx[e]);
+        }
+        t = group_sum(t, lpr);
+        if (live && kh < a.kv_heads && sub == 0) hs[wave * a.q_heads + h] = t;
+      }
+    }
+    __syncthreads();
+    if (live && lane == 0) {
+      float total = hs[wave * a.q_heads];
+      for (int h = 1; h < a.q_heads; ++h) total = total + hs[wave * a.q_heads + h];
+      a.scores[(int64_t)b * a.max_pages + p] = total / (float)a.q_heads;
+    }
+    __syncthreads();
+  }
+}
+
+// Page-mean score: sum_kh sum_d gq[kh,d] * summary[p,kh,d], with
+// gq = (sum_g q[kh*G+g]) / G.
+template <int E>
+__global__ __launch_bounds__(kScoreThreads) void mean_score_kernel(ScoreArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ float smem[];
+  float* gq = smem;                                   // [kv_heads * head_dim]
+  float* hs = smem + a.kv_heads * a.head_dim;         // [waves][kv_heads]
+  const int b = blockIdx.y;
+  const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
+  const int p_begin = blockIdx.x * kPagesPerBlock;
+  if (p_begin >= count) return;
+  const int group = a.q_heads / a.kv_heads;
+  for (int i = threadIdx.x; i < a.kv_heads * a.head_dim; i += kScoreThreads) {
+    int kh = i / a.head_dim, d = i - kh * a.head_dim;
+    float s = load_elem(a.q, a.q_dtype, (int64_t)b * a.q_bs + (int64_t)(kh * group) * a.q_hs + d);
+    for (int g = 1; g < group; ++g)
+      s = s + load_elem(a.q, a.q_dtype, (int64_t)b * a.q_bs + (int64_t)(kh * group + g) * a.q_hs + d);
+    gq[i] = s / (float)group;
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lpr = 1 << a.lpr_log2;
+  const int heads_per_pass = kWave >> a.lpr_log2;
+  const int sub = lane & (lpr - 1);
+  const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
+  for (int it = 0; it < kPagesPerBlock / kScoreWaves; ++it) {
+    const int p = p_begin + it * kScoreWaves + wave;
+    const bool live = p < count;
+    for (int kh0 = 0; kh0 < a.kv_heads; kh0 += heads_per_pass) {
+      const int kh = kh0 + (lane >> a.lpr_log2);
+      const bool data = live && kh < a.kv_heads && sub < a.lanes_used;
+      float t = 0.f;
+      if (data) {
+        float sv[E];
+        int64_t idx = (int64_t)b * a.b_bs + (int64_t)p * page_elems + (int64_t)kh * a.head_dim + sub * E;
+        load_vec<F32, E>(a.lo, idx, sv);
+        const float* g = gq + kh * a.head_dim + sub * E;
+        t = g[0] * sv[0];
+#pragma unroll
+        for (int e = 1; e < E; ++e) t = t + g[e] * sv[e];
+      }
+      t = group_sum(t, lpr);
+      if (live && kh < a.kv_heads && sub == 0) hs[wave * a.kv_heads + kh] = t;
+    }
+    __syncthreads();
+    if (live && lane == 0) {
+      float total = hs[wave * a.kv_heads];
+      for (int kh = 1; kh < a.kv_heads; ++kh) total = total + hs[wave * a.kv_heads + kh];
+      a.scores[(int64_t)b * a.max_pages + p] = total;
+    }
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ uint32_t order_key(float s) {
+  if (s != s) return 0xfffffffeu;  // NaN ranks just below required pages
+  uint32_t u = __float_as_uint(s);
+  if (u == 0x80000000u) u = 0u;  // -0.0 ties with +0.0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+struct SelectArgs {
+  const float* scores;
+  const int64_t* lengths;
+  int64_t length;
+  int page_size, max_pages, top_pages, keep_sink, mode;
+  FastDiv page_div;
+  int32_t* pages;
+  int32_t* positions;
+};
+
+__global__ __launch_bounds__(kSelectThreads) void select_topk_kernel(SelectArgs a) {
+  __shared__ int32_t chosen[NHS_MAX_SELECT_PAGES];
+  __shared__ int32_t hist[256];
+  __shared__ int32_t scan[kSelectThreads / 64 + 1];
+  __shared__ int32_t pick[2];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
+  const int64_t len = a.lengths ? a.lengths[b] : a.length;
+  const int k = a.top_pages < count ? a.top_pages : count;
+  const int per = (count + kSelectThreads - 1) / kSelectThreads;  // <= 16
+  const int p0 = tid * per;
+
+  bool sel[kMaxSelectPerThread];
+#pragma unroll
+  for (int q = 0; q < kMaxSelectPerThread; ++q) sel[q] = q < per && p0 + q < count;
+
+  if (a.top_pages < count) {
+    const float* sc = a.scores + (int64_t)b * a.max_pages;
+    const bool second = a.mode == kModeQuest ? (a.keep_sink && a.top_pages > 1 && count > 1) : a.top_pages > 1;
+    uint32_t key[kMaxSelectPerThread];
+#pragma unroll
+    for (int q = 0; q < kMaxSelectPerThread; ++q) {
+      int p = p0 + q;
+      key[q] = 0u;
+      if (q < per && p < count)
+        key[q] = (p == count - 1 || (second && p == 0)) ? 0xffffffffu : order_key(sc[p]);
+    }
+    uint32_t prefix = 0u, pmask = 0u;
+    int need = k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      if (tid < 256) hist[tid] = 0;
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kMaxSelectPerThread; ++q)
+        if (q < per && p0 + q < count && (key[q] & pmask) == prefix) atomicAdd(&hist[(key[q] >> shift) & 255u], 1);
+      __syncthreads();
+      if (tid < 64) {
+        // lane l holds bins 255-4l .. 252-4l (descending digit order)
+        int c[4], csum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          c[i] = hist[255 - 4 * tid - i];
+          csum += c[i];
+        }
+        int incl = csum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          int o = __shfl_up(incl, d);
+          if (tid >= d) incl += o;
+        }
+        int before = incl - csum;
+        if (before < need && incl >= need) {
+          int cum = before;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (cum + c[i] >= need) {
+              pick[0] = 255 - 4 * tid - i;
+              pick[1] = need - cum;
+              break;
+            }
+            cum += c[i];
+          }
+        }
+      }
+      __syncthreads();
+      prefix |= (uint32_t)pick[0] << shift;
+      pmask |= 255u << shift;
+      need = pick[1];
+      __syncthreads();
+    }
+    // prefix is the key of the k-th best page; `need` pages with that key
+    // are taken, lowest page index first.
+    int local_ties = 0;
+#pragma unroll
+    for (int q = 0; q < kMaxSelectPerThread; ++q) local_ties += sel[q] && key[q] == prefix;
+    int total_ties;
+    int tie_rank = block_exclusive_scan<int>(local_ties, scan, &total_ties);
+#pragma unroll
+    for (int q = 0; q < kMaxSelectPerThread; ++q) {
+      if (!sel[q]) continue;
+      if (key[q] == prefix) {
+        sel[q] = tie_rank < need;
+        ++tie_rank;
+      } else {
+        sel[q] = key[q] > prefix;
+      }
+    }
+  }
+
+  int local = 0;
+#pragma unroll
+  for (int q = 0; q < kMaxSelectPerThread; ++q) local += sel[q];
+  int n_sel;
+  int out = block_exclusive_scan<int>(local, scan, &n_sel);
+#pragma unroll
+  for (int q = 0; q < kMaxSelectPerThread; ++q)
+    if (sel[q]) chosen[out++] = p0 + q;
+  for (int i = n_sel + tid; i < a.top_pages; i += kSelectThreads) chosen[i] = -1;
+  __syncthreads();
+  int32_t* pages = a.pages + (int64_t)b * a.top_pages;
+  for (int i = tid; i < a.top_pages; i += kSelectThreads) pages[i] = chosen[i];
+  const int P = a.page_size;
+  const int64_t n_pos = (int64_t)a.top_pages * P;
+  int32_t* pos = a.positions + (int64_t)b * n_pos;
+  for (int64_t i = tid; i < n_pos; i += kSelectThreads) {
+    uint32_t j = a.page_div.div((uint32_t)i);
+    int32_t p = chosen[j];
+    int64_t t = (int64_t)p * P + (int64_t)((uint32_t)i - j * (uint32_t)P);
+    pos[i] = (p >= 0 && t < len) ? (int32_t)t : -1;
+  }
+}
+
+static int check_select_common(const char* who, int32_t batch, const void* query, int q_dtype, int32_t q_heads,
+                               int32_t kv_heads, int32_t head_dim, const int64_t* lengths, int64_t length,
+                               int32_t page_size, int32_t max_pages, int32_t top_pages, float* scores,
+                               int32_t* pages, int32_t* positions) {
+  if (!query || !scores || !pages || !positions) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
+  if (!valid_dtype(q_dtype)) return fail(NHS_ERR_INVALID, "%s: bad query dtype", who);
+  if (batch < 0 || q_heads < 1 || kv_heads < 1 || head_dim < 1 || page_size < 1 || max_pages < 1 ||
+      top_pages < 1 || q_heads % kv_heads)
+    return fail(NHS_ERR_INVALID, "%s: invalid shape or page budget", who);
+  if (max_pages > NHS_MAX_SELECT_PAGES || top_pages > NHS_MAX_SELECT_PAGES)
+    return fail(NHS_ERR_UNSUPPORTED, "%s: at most %d pages", who, NHS_MAX_SELECT_PAGES);
+  if ((int64_t)top_pages * page_size >= (1ll << 31))
+    return fail(NHS_ERR_UNSUPPORTED, "%s: top_pages * page_size must be < 2^31", who);
+  if (!lengths && (length < 0 || length >= (1ll << 31)))
+    return fail(NHS_ERR_INVALID, "%s: length must be in [0, 2^31)", who);
+  return NHS_OK;
+}
+
+// Chunking of a bound row (head_dim elements of `esize` bytes) into lanes:
+// 16-byte chunks when the row is a multiple of 16 bytes, else one element
+// per lane (head_dim <= 64). Returns elements per lane, or 0 if unsupported.
+static int chunk_elems(int head_dim, int esize) {
+  if ((head_dim * esize) % 16 == 0 && head_dim * esize / 16 <= 64) return 16 / esize;
+  if (head_dim <= 64) return 1;
+  return 0;
+}
+
+static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, const char* who) {
+  hipLaunchKernelGGL(select_topk_kernel, dim3((unsigned)batch), dim3(kSelectThreads), 0, stream, s);
+  return launch_status(who);
+}
+
+}  // namespace nhs
+
+extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                                int64_t q_head_stride, const void* minimum, const void* maximum,
+                                int32_t bounds_dtype, int64_t bounds_batch_stride, int32_t q_heads, int32_t kv_heads,
+                                int32_t head_dim, const int64_t* lengths, int64_t length, int32_t page_size,
+                                int32_t max_pages, int32_t top_pages, int32_t keep_sink, float* scores,
+                                int32_t* pages, int32_t* positions, void* stream) {
+  using namespace nhs;
+  const char* who = "nhs_quest_select";
+  int st = check_select_common(who, batch, query, q_dtype, q_heads, kv_heads, head_dim, lengths, length, page_size,
+                               max_pages, top_pages, scores, pages, positions);
+  if (st != NHS_OK) return st;
+  if (!minimum || !maximum) return fail(NHS_ERR_INVALID, "%s: null bounds", who);
+  if (!valid_dtype(bounds_dtype)) return fail(NHS_ERR_INVALID, "%s: bad bounds dtype", who);
+  if ((int64_t)q_heads * head_dim + 4 * q_heads > 16384)
+    return fail(NHS_ERR_UNSUPPORTED, "%s: q_heads * head_dim too large", who);
+  const int esize = elem_size(bounds_dtype);
+  const int E = chunk_elems(head_dim, esize);
+  if (E == 0) return fail(NHS_ERR_UNSUPPORTED, "%s: head_dim %d unsupported", who, head_dim);
+  if (E > 1 && ((uintptr_t)minimum | (uintptr_t)maximum) % 16)
+    return fail(NHS_ERR_INVALID, "%s: bounds must be 16-byte aligned", who);
+  if (batch == 0) return NHS_OK;
+  hipStream_t s = (hipStream_t)stream;
+  ScoreArgs a;
+  a.q = query;
+  a.q_dtype = q_dtype;
+  a.q_bs = q_batch_stride;
+  a.q_hs = q_head_stride;
+  a.lo = minimum;
+  a.hi = maximum;
+  a.b_bs = bounds_batch_stride;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.lanes_used = head_dim / E;
+  a.lpr_log2 = ilog2(a.lanes_used);
+  a.lengths = lengths;
+  a.length = length;
+  a.page_size = page_size;
+  a.max_pages = max_pages;
+  a.scores = scores;
+  dim3 grid((unsigned)((max_pages + kPagesPerBlock - 1) / kPagesPerBlock), (unsigned)batch);
+  size_t lds = ((size_t)q_heads * head_dim + (size_t)kScoreWaves * q_heads) * sizeof(float);
+  if (top_pages < max_pages) {  // scores are not needed when every page is kept
+    switch (bounds_dtype * 16 + E) {
+      case NHS_F32 * 16 + 4: hipLaunchKernelGGL((quest_score_kernel<F32, 4>), grid, dim3(kScoreThreads), lds, s, a); break;
+      case NHS_F32 * 16 + 1: hipLaunchKernelGGL((quest_score_kernel<F32, 1>), grid, dim3(kScoreThreads), lds, s, a); break;
+      case NHS_F16 * 16 + 8: hipLaunchKernelGGL((quest_score_kernel<F16, 8>), grid, dim3(kScoreThreads), lds, s, a); break;
+      case NHS_F16 * 16 + 1: hipLaunchKernelGGL((quest_score_kernel<F16, 1>), grid, dim3(kScoreThreads), lds, s, a); break;
+      case NHS_BF16 * 16 + 8: hipLaunchKernelGGL((quest_score_kernel<BF16, 8>), grid, dim3(kScoreThreads), lds, s, a); break;
+      default: hipLaunchKernelGGL((quest_score_kernel<BF16, 1>), grid, dim3(kScoreThreads), lds, s, a); break;
+    }
+    st = launch_status(who);
+    if (st != NHS_OK) return st;
+  }
+  SelectArgs sa;
+  sa.scores = scores;
+  sa.lengths = lengths;
+  sa.length = length;
+  sa.page_size = page_size;
+  sa.max_pages = max_pages;
+  sa.top_pages = top_pages;
+  sa.keep_sink = keep_sink;
+  sa.mode = kModeQuest;
+  sa.page_div = FastDiv((uint32_t)page_size);
+  sa.pages = pages;
+  sa.positions = positions;
+  return launch_select(sa, batch, s, who);
+}
+
+extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                               int64_t q_head_stride, const float* summaries, int64_t summaries_batch_stride,
+                               int32_t q_heads, int32_t kv_heads, int32_t head_dim, const int64_t* lengths,
+                               int64_t length, int32_t page_size, int32_t max_pages, int32_t top_pages, float* scores,
+                               int32_t* pages, int32_t* positions, void* stream) {
+  using namespace nhs;
+  const char* who = "nhs_mean_select";
+  int st = check_select_common(who, batch, query, q_dtype, q_heads, kv_heads, head_dim, lengths, length, page_size,
+                               max_pages, top_pages, scores, pages, positions);
+  if (st != NHS_OK) return st;
+  if (!summaries) return fail(NHS_ERR_INVALID, "%s: null summaries", who);
+  if ((int64_t)kv_heads * head_dim + 4 * kv_heads > 16384)
+    return fail(NHS_ERR_UNSUPPORTED, "%s: kv_heads * head_dim too large", who);
+  const int E = chunk_elems(head_dim, 4);
+  if (E == 0) return fail(NHS_ERR_UNSUPPORTED, "%s: head_dim %d unsupported", who, head_dim);
+  if (E > 1 && (uintptr_t)summaries % 16) return fail(NHS_ERR_INVALID, "%s: summaries must be 16-byte aligned", who);
+  if (batch == 0) return NHS_OK;
+  hipStream_t s = (hipStream_t)stream;
+  ScoreArgs a;
+  a.q = query;
+  a.q_dtype = q_dtype;
+  a.q_bs = q_batch_stride;
+  a.q_hs = q_head_stride;
+  a.lo = summaries;
+  a.hi = nullptr;
+  a.b_bs = summaries_batch_stride;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.head_dim = head_dim;
+  a.lanes_used = head_dim / E;
+  a.lpr_log2 = ilog2(a.lanes_used);
+  a.lengths = lengths;
+  a.length = length;
+  a.page_size = page_size;
+  a.max_pages = max_pages;
+  a.scores = scores;
+  dim3 grid((unsigned)((max_pages + kPagesPerBlock - 1) / kPagesPerBlock), (unsigned)batch);
+  size_t lds = ((size_t)kv_heads * head_dim + (size_t)kScoreWaves * kv_heads) * sizeof(float);
+  if (top_pages < max_pages) {
+    if (E == 4)
+      hipLaunchKernelGGL((mean_score_kernel<4>), grid, dim3(kScoreThreads), lds, s, a);
+    else
+      hipLaunchKernelGGL((mean_score_kernel<1>), grid, dim3(kScoreThreads), lds, s, a);
+    st = launch_status(who);
+    if (st != NHS_OK) return st;
+  }
+  SelectArgs sa;
+  sa.scores = scores;
+  sa.lengths = lengths;
+  sa.length = length;
+  sa.page_size = page_size;
+  sa.max_pages = max_pages;
+  sa.top_pages = top_pages;
+  sa.keep_sink = 1;
+  sa.mode = kModeMean;
+  sa.page_div = FastDiv((uint32_t)page_size);
+  sa.pages = pages;
+  sa.positions = positions;
+  return launch_select(sa, batch, s, who);
+}

@@ -1,0 +1,285 @@
+"""Launchers for the gfx950 kernels of libnhs_hip.so, on torch tensors.
+
+These replace nano_hisparse/row_kernels.py of the reference (Triton `_gather`
+and `_attend`, and `MappedHost` through libcuda) and add batched launchers
+for the selectors and the resolver. Every launcher validates shapes, dtypes
+and devices, then enqueues on the current torch stream of the tensors'
+device without synchronising. Tensors must live on a GPU: there is no CPU
+kernel path. Host-logic tests that run without a GPU install a CPU kernel
+provider explicitly (set_cpu_provider); the library never installs one.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _hip
+
+_DTYPES = {torch.float32: _hip.NHS_F32, torch.float16: _hip.NHS_F16, torch.bfloat16: _hip.NHS_BF16}
+
+_cpu_provider = None
+
+
+def set_cpu_provider(provider):
+    """Install (or clear, with None) the object that computes for CPU tensors.
+
+    Only test harnesses use this, to run the host control plane without a GPU.
+    It must offer resolve_rows, gather_rows, attend_rows, quest_positions and
+    mean_positions with the signatures of the functions below.
+    """
+    global _cpu_provider
+    _cpu_provider = provider
+
+
+def cpu_provider(what: str):
+    if _cpu_provider is None:
+        raise RuntimeError(
+            f"{what}: nano_hisparse computes on the GPU through libnhs_hip.so; "
+            "CPU tensors are not supported (no CPU kernel provider is installed)"
+        )
+    return _cpu_provider
+
+
+def dtype_code(dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}") from None
+
+
+def _ptr(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _require_gpu(what, *tensors):
+    device = tensors[0].device
+    if device.type != "cuda":
+        raise ValueError(f"{what}: tensors must be on a GPU")
+    for t in tensors:
+        if t is not None and t.device != device:
+            raise ValueError(f"{what}: all tensors must be on {device}")
+    return device
+
+
+class MappedHost:
+    """Device alias of pinned host memory that torch allocated.
+
+    The library only queries the alias (hipHostGetDevicePointer); it never
+    registers or unregisters the allocation, which torch owns.
+    Replaces MappedHost of the reference (row_kernels.py:10-32).
+    """
+
+    def __init__(self, tensor: torch.Tensor):
+        if not tensor.is_pinned():
+            raise ValueError("row gather requires pinned host backing")
+        lib = _hip.load()
+        alias = ctypes.c_void_p()
+        _hip.check(lib.nhs_host_device_ptr(_ptr(tensor), ctypes.byref(alias)), "nhs_host_device_ptr")
+        self.tensor, self.dtype, self.pointer = tensor, tensor.dtype, alias.value
+
+    def data_ptr(self):
+        return self.pointer
+
+
+# ---- gather ----------------------------------------------------------------------
+
+
+def gather_plan(host: MappedHost, pool, miss_host, miss_device, page_size):
+    """Copy plan rows from the pinned host store into pool rows.
+
+    miss_host / miss_device: int64 device tensors of equal numel (any shape,
+    contiguous); -1 entries are skipped.
+    """
+    device = _require_gpu("gather_rows", pool, miss_host, miss_device)
+    if miss_host.dtype != torch.int64 or miss_device.dtype != torch.int64:
+        raise ValueError("gather plans must be int64")
+    if miss_host.numel() != miss_device.numel() or not (miss_host.is_contiguous() and miss_device.is_contiguous()):
+        raise ValueError("gather plans must be contiguous and of equal size")
+    if host.dtype != pool.dtype:
+        raise ValueError("host and pool dtypes differ")
+    plane_bytes = pool[0, 0, 0].numel() * pool.element_size()
+    lib = _hip.load()
+    status = lib.nhs_gather_rows(
+        ctypes.c_void_p(host.data_ptr()), _ptr(pool), _ptr(miss_host), _ptr(miss_device), miss_host.numel(),
+        page_size, plane_bytes, _stream(device),
+    )
+    _hip.check(status, "nhs_gather_rows")
+
+
+def gather_rows(host, pool, plan, config):
+    """Reference signature (row_kernels.py:58-70): gather one RowPlan's misses."""
+    gather_plan(host, pool, plan.miss_host_rows, plan.miss_device_rows, config.page_size)
+
+
+# ---- attention ------------------------------------------------------------------
+
+
+def attend_batched(query, pool, rows, page_size, out=None, workspace=None):
+    """GQA attention of query [B, Hq, D] over rows [B, N] (shared by all heads
+    of a request) or [B, Hq, N] (one list per head), int64 pool rows with -1
+    masked. Returns out [B, Hq, D] in the query's dtype."""
+    device = _require_gpu("attend_rows", query, pool, rows)
+    if query.ndim != 3 or pool.ndim != 5 or rows.ndim not in (2, 3) or rows.dtype != torch.int64:
+        raise ValueError("attend_rows: expected query [B, Hq, D], pool [blocks, 2, P, Hkv, D], int64 rows")
+    B, Hq, D = query.shape
+    kv_heads = pool.shape[3]
+    if pool.shape[4] != D or pool.shape[2] != page_size or Hq % kv_heads:
+        raise ValueError("attend_rows: query/pool head shape mismatch")
+    if query.stride(2) != 1 or not pool.is_contiguous():
+        raise ValueError("attend_rows: query rows and the pool must be contiguous")
+    if rows.shape[0] != B or (rows.ndim == 3 and rows.shape[1] != Hq):
+        raise ValueError("attend_rows: rows do not match the query batch/heads")
+    if pool.shape[0] * page_size >= 2**31:
+        raise ValueError("attend_rows: pool rows must be < 2^31")
+    n_rows = rows.shape[-1]
+    r_bs, r_cs = rows.stride(0), rows.stride(-1)
+    r_hs = rows.stride(1) if rows.ndim == 3 else 0
+    if rows.ndim == 3 and r_hs == 0:
+        rows = rows[:, 0]  # an expanded shared list
+    lib = _hip.load()
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=query.dtype, device=device)
+    need = lib.nhs_attend_workspace_bytes(B, Hq, D, max(n_rows, 1))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
+    if n_rows == 0:
+        return out.zero_()
+    status = lib.nhs_attend_rows(
+        _ptr(query), dtype_code(query.dtype), query.stride(0), query.stride(1), _ptr(pool), dtype_code(pool.dtype),
+        _ptr(rows), r_bs, r_hs, r_cs, B, n_rows, Hq, kv_heads, D, page_size, _ptr(out), out.stride(0),
+        out.stride(1), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(device),
+    )
+    _hip.check(status, "nhs_attend_rows")
+    return out
+
+
+def attend_rows(query, pool, rows, config):
+    """Reference signature (row_kernels.py:116-135): query [Hq, D], rows
+    [Hq, N] (a stride-0 expansion when shared) -> [Hq, D]."""
+    return attend_batched(query.unsqueeze(0), pool, rows.unsqueeze(0), config.page_size)[0]
+
+
+# ---- resolver ---------------------------------------------------------------------
+
+
+def resolve_batched(positions, source, resident, hot, tags, lru, lengths, page_size, counts_total=None):
+    """Resolve B items at once; every table has a leading batch dimension.
+
+    positions [B, K] int32/int64; source/resident [B, n_pages] int32;
+    hot [B, blocks] int32; tags [B, H] int32 and lru [B, H] int64 (updated in
+    place); lengths: int, or int64 tensor [B]. Returns (physical, miss_host,
+    miss_device, counts[B, 3]) as int64 device tensors; counts_total [3] is
+    incremented when given.
+    """
+    device = _require_gpu("resolve_rows", positions, source, resident, hot, tags, lru)
+    B, K = positions.shape
+    if positions.dtype not in (torch.int32, torch.int64) or positions.stride(1) != 1:
+        raise ValueError("positions must be a [B, K] int32/int64 tensor with unit stride")
+    for name, t, dt in (("source", source, torch.int32), ("resident", resident, torch.int32),
+                        ("hot", hot, torch.int32), ("tags", tags, torch.int32), ("lru", lru, torch.int64)):
+        if t.dtype != dt or t.ndim != 2 or t.shape[0] != B or t.stride(1) != 1:
+            raise ValueError(f"{name} must be a [B, n] {dt} tensor with unit stride")
+    if source.shape != resident.shape or source.stride(0) != resident.stride(0):
+        raise ValueError("source and resident tables must have the same shape and strides")
+    H = tags.shape[1]
+    if lru.shape[1] != H or hot.shape[1] * page_size < H:
+        raise ValueError("tags/lru/hot table sizes disagree")
+    lengths_t = None
+    length = 0
+    if isinstance(lengths, torch.Tensor):
+        lengths_t = lengths.to(device=device, dtype=torch.int64).contiguous()
+    else:
+        length = int(lengths)
+    physical = torch.empty(B, K, dtype=torch.int64, device=device)
+    miss_host = torch.empty_like(physical)
+    miss_device = torch.empty_like(physical)
+    counts = torch.empty(B, 3, dtype=torch.int64, device=device)
+    lib = _hip.load()
+    status = lib.nhs_resolve_rows(
+        B, K, _ptr(positions), int(positions.dtype == torch.int64), positions.stride(0), _ptr(source),
+        _ptr(resident), source.stride(0), source.shape[1], _ptr(hot), hot.stride(0), _ptr(tags), tags.stride(0),
+        _ptr(lru), lru.stride(0), H, _ptr(lengths_t), length, page_size, _ptr(physical), _ptr(miss_host),
+        _ptr(miss_device), K, _ptr(counts), _ptr(counts_total), _stream(device),
+    )
+    _hip.check(status, "nhs_resolve_rows")
+    return physical, miss_host, miss_device, counts
+
+
+def expand_columns(shared_rows, columns):
+    """out[h, c] = shared_rows[columns[h, c]] for 0 <= column < n, else -1."""
+    device = _require_gpu("expand_columns", shared_rows, columns)
+    shared_rows, columns = shared_rows.contiguous(), columns.contiguous()
+    out = torch.empty(columns.shape, dtype=torch.int64, device=device)
+    lib = _hip.load()
+    status = lib.nhs_expand_columns(
+        _ptr(shared_rows), shared_rows.numel(), _ptr(columns), columns.shape[0], columns.shape[1], _ptr(out),
+        _stream(device),
+    )
+    _hip.check(status, "nhs_expand_columns")
+    return out
+
+
+# ---- selectors ---------------------------------------------------------------------
+
+
+def _lengths_arg(lengths, device):
+    if isinstance(lengths, torch.Tensor):
+        return lengths.to(device=device, dtype=torch.int64).contiguous(), 0
+    return None, int(lengths)
+
+
+def quest_batched(query, minimum, maximum, lengths, page_size, top_pages, keep_sink=True):
+    """Quest selection for B requests: query [B, Hq, D]; minimum/maximum
+    [B, n_pages, Hkv, D] (the per-page bounds of each request). Returns
+    (pages [B, top_pages] int32 ascending with -1 padding, positions
+    [B, top_pages*P] int32 ascending with -1 padding, scores [B, n_pages])."""
+    device = _require_gpu("quest_selection", query, minimum, maximum)
+    B, Hq, D = query.shape
+    if minimum.shape != maximum.shape or minimum.ndim != 4 or minimum.shape[0] != B or minimum.shape[3] != D:
+        raise ValueError("quest bounds must be [B, n_pages, Hkv, D]")
+    if minimum.dtype != maximum.dtype or minimum.stride() != maximum.stride():
+        raise ValueError("minimum and maximum must share dtype and layout")
+    if not minimum[0].is_contiguous() or query.stride(2) != 1:
+        raise ValueError("quest bounds of a request and query rows must be contiguous")
+    n_pages, kv_heads = minimum.shape[1], minimum.shape[2]
+    lengths_t, length = _lengths_arg(lengths, device)
+    scores = torch.empty(B, n_pages, dtype=torch.float32, device=device)
+    pages = torch.empty(B, top_pages, dtype=torch.int32, device=device)
+    positions = torch.empty(B, top_pages * page_size, dtype=torch.int32, device=device)
+    lib = _hip.load()
+    status = lib.nhs_quest_select(
+        B, _ptr(query), dtype_code(query.dtype), query.stride(0), query.stride(1), _ptr(minimum), _ptr(maximum),
+        dtype_code(minimum.dtype), minimum.stride(0), Hq, kv_heads, D, _ptr(lengths_t), length, page_size,
+        n_pages, top_pages, int(bool(keep_sink)), _ptr(scores), _ptr(pages), _ptr(positions), _stream(device),
+    )
+    _hip.check(status, "nhs_quest_select")
+    return pages, positions, scores
+
+
+def mean_batched(query, summaries, lengths, page_size, top_pages):
+    """Page-mean selection for B requests; summaries [B, n_pages, Hkv, D] fp32."""
+    device = _require_gpu("select_pages", query, summaries)
+    B, Hq, D = query.shape
+    if summaries.ndim != 4 or summaries.dtype != torch.float32 or summaries.shape[0] != B:
+        raise ValueError("summaries must be [B, n_pages, Hkv, D] float32")
+    if not summaries[0].is_contiguous() or query.stride(2) != 1:
+        raise ValueError("summaries of a request and query rows must be contiguous")
+    n_pages, kv_heads = summaries.shape[1], summaries.shape[2]
+    lengths_t, length = _lengths_arg(lengths, device)
+    scores = torch.empty(B, n_pages, dtype=torch.float32, device=device)
+    pages = torch.empty(B, top_pages, dtype=torch.int32, device=device)
+    positions = torch.empty(B, top_pages * page_size, dtype=torch.int32, device=device)
+    lib = _hip.load()
+    status = lib.nhs_mean_select(
+        B, _ptr(query), dtype_code(query.dtype), query.stride(0), query.stride(1), _ptr(summaries),
+        summaries.stride(0), Hq, kv_heads, D, _ptr(lengths_t), length, page_size, n_pages, top_pages,
+        _ptr(scores), _ptr(pages), _ptr(positions), _stream(device),
+    )
+    _hip.check(status, "nhs_mean_select")
+    return pages, positions, scores

@@ -1,0 +1,296 @@
+"""Parity of the HIP kernels (through the C ABI) with the CPU oracle.
+
+Integer and byte outputs (selected pages, positions, resolved rows, miss
+plans, tags, LRU order, gathered bytes) must be bit-exact; Quest scores are
+bit-exact because the oracle restates the kernels' fixed fp32 summation
+order; attention must be within max-abs 2e-2 (bf16/fp16) or 1e-4 (fp32) of
+the oracle's float64 masked softmax.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from nano_hisparse import row_kernels as rk
+
+pytestmark = pytest.mark.gpu
+
+ATOL = {torch.bfloat16: 2e-2, torch.float16: 2e-2, torch.float32: 1e-4}
+
+
+def log_case(**kw):
+    print("case:", kw, flush=True)
+
+
+# ---- gather ----------------------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    "dtype,page,kv_heads,head_dim",
+    [(torch.bfloat16, 64, 8, 128), (torch.float32, 4, 1, 8), (torch.float16, 7, 2, 24), (torch.float32, 3, 1, 1)],
+)
+def test_gather_rows_bit_exact(gpu, dtype, page, kv_heads, head_dim):
+    log_case(test="gather", dtype=dtype, page=page, kv_heads=kv_heads, head_dim=head_dim)
+    g = torch.Generator().manual_seed(1)
+    host_pages, pool_blocks = 48, 20
+    host = torch.randn(host_pages, 2, page, kv_heads, head_dim, generator=g).to(dtype).pin_memory()
+    pool_cpu = torch.randn(pool_blocks, 2, page, kv_heads, head_dim, generator=g).to(dtype)
+    n = 3 * page + 5
+    rows = torch.randperm(pool_blocks * page, generator=g)[:n]
+    srcs = torch.randint(0, host_pages * page, (n,), generator=g)
+    mh, md = srcs.clone(), rows.clone()
+    mh[n // 2 :] = -1  # compact prefix, then padding
+    md[n // 2 :] = -1
+    mh[3] = -1  # a hole inside the prefix is skipped too
+    expected = pool_cpu.clone()
+    oracle.gather_rows(host, expected, mh, md, page)
+    pool = pool_cpu.to(gpu)
+    alias = rk.MappedHost(host)
+    rk.gather_plan(alias, pool, mh.to(gpu), md.to(gpu), page)
+    torch.cuda.synchronize()
+    assert torch.equal(pool.cpu().view(torch.uint8), expected.view(torch.uint8))
+
+
+# ---- attention ------------------------------------------------------------------
+
+
+def _attention_case(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, N, per_head, seed):
+    g = torch.Generator().manual_seed(seed)
+    blocks = max(4, (N * 2) // P + 2)
+    pool = torch.randn(blocks, 2, P, Hkv, D, generator=g).to(dtype)
+    q = torch.randn(B, Hq, D, generator=g).to(q_dtype)
+    shape = (B, Hq, N) if per_head else (B, N)
+    rows = torch.randint(0, blocks * P, shape, generator=g)
+    rows[torch.rand(shape, generator=g) < 0.2] = -1
+    return pool, q, rows
+
+
+@pytest.mark.parametrize(
+    "dtype,q_dtype,B,Hq,Hkv,D,P,N,per_head",
+    [
+        (torch.bfloat16, torch.bfloat16, 3, 32, 8, 128, 64, 700, False),  # Llama-3-8B heads, GQA 4
+        (torch.bfloat16, torch.bfloat16, 2, 28, 4, 128, 32, 300, False),  # Qwen2-7B heads, GQA 7
+        (torch.float32, torch.float32, 2, 4, 2, 64, 16, 129, False),  # toy fp32 decoder, GQA 2
+        (torch.float32, torch.float32, 1, 2, 1, 8, 4, 6, False),
+        (torch.float16, torch.float16, 1, 6, 2, 24, 7, 9, False),  # head_dim*2 bytes = 48
+        (torch.float16, torch.float16, 2, 4, 2, 24, 3, 11, True),  # per-head (legacy) rows
+        (torch.bfloat16, torch.float32, 2, 16, 2, 128, 64, 257, False),  # fp32 query, bf16 KV, GQA 8
+        (torch.bfloat16, torch.bfloat16, 1, 48, 4, 64, 16, 100, False),  # GQA 12 (two workgroups per KV head)
+        (torch.float32, torch.float32, 1, 3, 3, 256, 8, 40, False),  # 1 KiB rows
+    ],
+)
+def test_attend_rows_matches_oracle(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, N, per_head):
+    log_case(test="attend", dtype=dtype, B=B, Hq=Hq, Hkv=Hkv, D=D, P=P, N=N, per_head=per_head)
+    pool, q, rows = _attention_case(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, N, per_head, seed=B * 100 + Hq)
+    expected = oracle.attend_rows(q, pool, rows, P)
+    out = rk.attend_batched(q.to(gpu), pool.to(gpu), rows.to(gpu), P)
+    torch.cuda.synchronize()
+    assert out.dtype == q_dtype
+    err = (out.cpu().float() - expected).abs().max().item()
+    assert err <= ATOL[dtype if dtype != torch.float32 else q_dtype], err
+
+
+def test_attend_rows_masking_edge_cases(gpu):
+    log_case(test="attend-edges")
+    P, Hkv, D = 16, 2, 64
+    g = torch.Generator().manual_seed(7)
+    pool = torch.randn(8, 2, P, Hkv, D, generator=g)
+    q = torch.randn(3, 4, D, generator=g)
+    rows = torch.full((3, 50), -1, dtype=torch.int64)
+    rows[1, 37] = 21  # a single valid row: output is exactly that V row
+    rows[2, :] = 5  # the same row repeated: still that V row
+    out = rk.attend_batched(q.to(gpu), pool.to(gpu), rows.to(gpu), P).cpu()
+    assert torch.equal(out[0], torch.zeros(4, D))  # no valid row -> zeros
+    v21 = pool[21 // P, 1, 21 % P]
+    v5 = pool[5 // P, 1, 5 % P]
+    for h in range(4):
+        torch.testing.assert_close(out[1, h], v21[h // 2], atol=1e-6, rtol=1e-6)
+        torch.testing.assert_close(out[2, h], v5[h // 2], atol=1e-5, rtol=1e-5)
+
+
+# ---- resolver -----------------------------------------------------------------------
+
+
+def test_resolver_known_answer(gpu):
+    """tests/test_selection.py:36-50 of the reference, plus the LRU post-state."""
+    log_case(test="resolve-kat")
+    t32 = lambda v: torch.tensor([v], dtype=torch.int32, device=gpu)  # noqa: E731
+    source, resident, hot = t32([5, 2, 9, 4]), t32([-1, 7, -1, 3]), t32([6, 1])
+    tags = t32([-1, -1, -1, -1, -1, 22, -1, -1])
+    lru = torch.tensor([[0, 1, 2, 3, 4, 6, 7, 5]], dtype=torch.int64, device=gpu)
+    positions = torch.tensor([[9, 2, 6, 9, 14, -1]], dtype=torch.int64, device=gpu)
+    phys, mh, md, counts = rk.resolve_batched(positions, source, resident, hot, tags, lru, 16, 4)
+    assert phys[0].tolist() == [24, 5, 30, -1, 14, -1]
+    assert counts[0].tolist() == [2, 1, 1]
+    assert mh[0].tolist() == [37, -1, -1, -1, -1, -1]
+    assert md[0].tolist() == [24, -1, -1, -1, -1, -1]
+    assert tags[0].tolist() == [37, -1, -1, -1, -1, 22, -1, -1]
+    assert lru[0].tolist() == [1, 2, 3, 4, 6, 7, 0, 5]
+
+
+def make_resolver_state(rng, B, H, P, n_pages, host_pages, pool_blocks, resident_frac, tag_frac):
+    """Random but consistent tables: distinct host slots per page, distinct
+    resident blocks, hot blocks disjoint from resident blocks, unique tags."""
+    source = np.full((B, n_pages), -1, np.int32)
+    resident = np.full((B, n_pages), -1, np.int32)
+    hot_blocks = -(-H // P)
+    hot = np.zeros((B, hot_blocks), np.int32)
+    tags = np.full((B, H), -1, np.int32)
+    lru = np.zeros((B, H), np.int64)
+    for b in range(B):
+        source[b] = rng.permutation(host_pages)[:n_pages]
+        blocks = rng.permutation(pool_blocks)
+        hot[b] = blocks[:hot_blocks]
+        res_pages = rng.random(n_pages) < resident_frac
+        res_ids = blocks[hot_blocks : hot_blocks + res_pages.sum()]
+        resident[b, res_pages] = res_ids
+        n_tags = int(H * tag_frac)
+        cand = (source[b][:, None].astype(np.int64) * P + np.arange(P)).ravel()
+        cand = cand[np.repeat(resident[b] < 0, P)]
+        chosen = rng.choice(cand, size=min(n_tags, cand.size), replace=False)
+        slots = rng.permutation(H)[: chosen.size]
+        tags[b, slots] = chosen
+        lru[b] = rng.permutation(H)
+    return source, resident, hot, tags, lru
+
+
+def random_positions(rng, B, K, length, P, mode):
+    pos = np.full((B, K), -1, np.int64)
+    for b in range(B):
+        if mode == "pages":  # whole pages, sorted, tail clipped, -1 padded
+            count = -(-int(length[b]) // P)
+            k_pages = K // P
+            pages = np.sort(rng.choice(count, size=min(k_pages, count), replace=False))
+            toks = (pages[:, None] * P + np.arange(P)).ravel()
+            toks = toks[toks < length[b]]
+            pos[b, : toks.size] = toks
+        else:  # arbitrary order, duplicates, out-of-range and negative values
+            pos[b] = rng.integers(-3, int(length[b]) + 5, size=K)
+            dup = rng.integers(0, K, size=K // 8)
+            pos[b, dup] = pos[b, rng.integers(0, K, size=dup.size)]
+    return pos
+
+
+@pytest.mark.parametrize(
+    "B,K,H,P,n_pages,mode,steps",
+    [
+        (4, 2048, 4096, 64, 512, "pages", 3),  # Llama-3-8B shape at 32K context, 2048-row budget
+        (8, 1024, 2048, 32, 2048, "pages", 3),  # Qwen2-7B stress shape, H = 2U
+        (3, 1024, 1024, 32, 256, "pages", 4),  # H = U: every miss replaces a row
+        (2, 777, 1500, 7, 300, "random", 4),  # unsorted, duplicates, invalid entries, odd sizes
+        (2, 4096, 8192, 64, 2048, "pages", 2),  # 128K context, 4096-row budget
+        (1, 4096, 32768, 16, 4096, "random", 2),  # maximum sizes
+    ],
+)
+def test_resolver_matches_oracle_over_steps(gpu, B, K, H, P, n_pages, mode, steps):
+    log_case(test="resolve", B=B, K=K, H=H, P=P, n_pages=n_pages, mode=mode)
+    rng = np.random.default_rng(B * 1000 + K)
+    host_pages = n_pages * 2
+    pool_blocks = n_pages + -(-H // P) + 8
+    source, resident, hot, tags, lru = make_resolver_state(rng, B, H, P, n_pages, host_pages, pool_blocks, 0.4, 0.6)
+    lengths = rng.integers(n_pages * P // 2, n_pages * P + 1, size=B)
+    g_src, g_res, g_hot = (torch.from_numpy(x).to(gpu) for x in (source, resident, hot))
+    g_tags, g_lru = torch.from_numpy(tags).to(gpu), torch.from_numpy(lru).to(gpu)
+    o_tags, o_lru = tags.astype(np.int64), lru.copy()
+    total = torch.zeros(3, dtype=torch.int64, device=gpu)
+    expected_total = np.zeros(3, np.int64)
+    for step in range(steps):
+        pos = random_positions(rng, B, K, lengths, P, mode)
+        dtype = torch.int32 if step % 2 else torch.int64
+        phys, mh, md, counts = rk.resolve_batched(
+            torch.from_numpy(pos).to(gpu, dtype), g_src, g_res, g_hot, g_tags, g_lru,
+            torch.from_numpy(lengths).to(gpu), P, counts_total=total,
+        )
+        phys, mh, md, counts = (t.cpu().numpy() for t in (phys, mh, md, counts))
+        for b in range(B):
+            e_phys, e_mh, e_md, e_counts = oracle.resolve_rows(
+                pos[b], source[b], resident[b], hot[b], o_tags[b], o_lru[b], lengths[b], P
+            )
+            np.testing.assert_array_equal(phys[b], e_phys)
+            np.testing.assert_array_equal(mh[b], e_mh)
+            np.testing.assert_array_equal(md[b], e_md)
+            np.testing.assert_array_equal(counts[b], e_counts)
+            expected_total += e_counts
+        np.testing.assert_array_equal(g_tags.cpu().numpy(), o_tags)
+        np.testing.assert_array_equal(g_lru.cpu().numpy(), o_lru)
+    np.testing.assert_array_equal(total.cpu().numpy(), expected_total)
+    for b in range(B):  # invariants: lru is a permutation, non-negative tags are unique
+        assert sorted(o_lru[b].tolist()) == list(range(H))
+        t = o_tags[b][o_tags[b] >= 0]
+        assert t.size == np.unique(t).size
+
+
+# ---- selectors -----------------------------------------------------------------------
+
+
+def _bounds(g, B, n_pages, Hkv, D, dtype, offsets=False):
+    a = torch.randn(B, n_pages, Hkv, D, generator=g)
+    c = torch.randn(B, n_pages, Hkv, D, generator=g)
+    if offsets:
+        mu = 0.5 * torch.randn(B, n_pages, 1, 1, generator=g)
+        a, c = a + mu, c + mu
+    return torch.minimum(a, c).to(dtype), torch.maximum(a, c).to(dtype)
+
+
+@pytest.mark.parametrize(
+    "dtype,q_dtype,B,Hq,Hkv,D,P,n_pages,top,keep_sink",
+    [
+        (torch.bfloat16, torch.bfloat16, 16, 32, 8, 128, 64, 512, 32, True),  # 32K context, 32 pages
+        (torch.bfloat16, torch.bfloat16, 4, 32, 8, 128, 64, 2048, 64, True),  # 128K context, 64 pages
+        (torch.bfloat16, torch.bfloat16, 8, 28, 4, 128, 32, 2048, 32, True),
+        (torch.float32, torch.float32, 3, 4, 2, 64, 16, 40, 8, True),
+        (torch.float32, torch.float32, 2, 4, 2, 64, 16, 40, 8, False),
+        (torch.float16, torch.float32, 2, 6, 2, 24, 7, 30, 5, True),
+        (torch.float32, torch.float32, 2, 2, 1, 2, 2, 3, 2, False),  # head_dim 2 (element lanes)
+        (torch.bfloat16, torch.bfloat16, 2, 8, 2, 64, 16, 9000, 300, True),
+    ],
+)
+def test_quest_select_bit_exact(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, n_pages, top, keep_sink):
+    log_case(test="quest", dtype=dtype, B=B, Hq=Hq, Hkv=Hkv, D=D, P=P, n_pages=n_pages, top=top)
+    g = torch.Generator().manual_seed(n_pages + B)
+    q = torch.randn(B, Hq, D, generator=g).to(q_dtype)
+    mn, mx = _bounds(g, B, n_pages, Hkv, D, dtype, offsets=True)
+    lengths = torch.randint(1, n_pages * P + 1, (B,), generator=g)
+    lengths[0] = n_pages * P  # full
+    if B > 1:
+        lengths[1] = min(int(lengths[1]), top * P - 3)  # fewer pages than the budget
+    e_scores, e_pages, e_pos = oracle.quest_select(q, mn, mx, lengths, P, top, keep_sink)
+    pages, pos, scores = rk.quest_batched(q.to(gpu), mn.to(gpu), mx.to(gpu), lengths.to(gpu), P, top, keep_sink)
+    pages, pos, scores = pages.cpu(), pos.cpu(), scores.cpu()
+    assert torch.equal(pages, e_pages)
+    assert torch.equal(pos, e_pos)
+    for b in range(B):
+        count = -(-int(lengths[b]) // P)
+        if top < count:
+            assert torch.equal(scores[b, :count].view(torch.int32), e_scores[b, :count].view(torch.int32))
+
+
+def test_quest_known_answers(gpu):
+    """tests/test_selection.py:18-33 of the reference."""
+    log_case(test="quest-kat")
+    low = torch.tensor([[[-10.0, 0.0]], [[1.0, 0.0]], [[0.0, 0.0]]])
+    high = torch.tensor([[[10.0, 0.0]], [[1.0, 0.0]], [[0.0, 0.0]]])
+    pages, pos, _ = rk.quest_batched(
+        torch.tensor([[[1.0, 0.0]]], device=gpu), low[None].to(gpu), high[None].to(gpu), 5, 2, 2, keep_sink=False
+    )
+    assert pages[0].tolist() == [0, 2]
+    assert pos[0].tolist() == [0, 1, 4, -1]
+    bounds = torch.tensor([[[9.0, 0.0]], [[0.0, 10.0]], [[-1.0, -1.0]]])[None].to(gpu)
+    pages, pos, _ = rk.quest_batched(torch.eye(2, device=gpu)[None], bounds, bounds, 5, 2, 2, keep_sink=False)
+    assert pages[0].tolist() == [1, 2]
+    assert pos[0].tolist() == [2, 3, 4, -1]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,D,P,n_pages,top", [(4, 32, 8, 128, 64, 512, 32), (3, 4, 2, 8, 4, 20, 1),
+                                                      (2, 4, 2, 8, 4, 20, 2), (2, 6, 3, 24, 5, 33, 7)])
+def test_mean_select_bit_exact(gpu, B, Hq, Hkv, D, P, n_pages, top):
+    log_case(test="mean", B=B, Hq=Hq, D=D, n_pages=n_pages, top=top)
+    g = torch.Generator().manual_seed(5 + n_pages)
+    q = torch.randn(B, Hq, D, generator=g)
+    summ = torch.randn(B, n_pages, Hkv, D, generator=g)
+    lengths = torch.randint(1, n_pages * P + 1, (B,), generator=g)
+    e_scores, e_pages, e_pos = oracle.mean_select(q, summ, lengths, P, top)
+    pages, pos, scores = rk.mean_batched(q.to(gpu), summ.to(gpu), lengths.to(gpu), P, top)
+    assert torch.equal(pages.cpu(), e_pages)
+    assert torch.equal(pos.cpu(), e_pos)

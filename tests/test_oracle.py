@@ -1,0 +1,195 @@
+"""The CPU oracle pinned against the reference's known answers, independent
+formulations and closed forms (no GPU needed), plus the C ABI export check.
+
+Known answers come from the reference's own tests (paths relative to the
+reference repository): tests/test_selection.py:18-50.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+
+def test_library_exports_every_header_symbol():
+    from nano_hisparse import _hip
+
+    lib = ctypes.CDLL(_hip.LIB_PATH)  # loads without a GPU; nothing is called
+    symbols = _hip.header_symbols()
+    assert len(symbols) >= 10
+    missing = [s for s in symbols if not hasattr(lib, s)]
+    assert not missing, missing
+    assert set(symbols) == set(_hip.SIGNATURES)
+
+
+# ---- resolver ----------------------------------------------------------------------
+
+KAT = dict(
+    source=[5, 2, 9, 4], resident=[-1, 7, -1, 3], hot=[6, 1], tags=[-1, -1, -1, -1, -1, 22, -1, -1],
+    lru=[0, 1, 2, 3, 4, 6, 7, 5], positions=[9, 2, 6, 9, 14, -1], length=16, page=4,
+)
+
+
+def test_resolver_known_answer_and_lru_post_state():
+    tags = np.array(KAT["tags"], np.int64)
+    lru = np.array(KAT["lru"], np.int64)
+    phys, mh, md, counts = oracle.resolve_rows(
+        KAT["positions"], KAT["source"], KAT["resident"], KAT["hot"], tags, lru, KAT["length"], KAT["page"]
+    )
+    assert phys.tolist() == [24, 5, 30, -1, 14, -1]
+    assert counts.tolist() == [2, 1, 1]
+    assert mh.tolist() == [37, -1, -1, -1, -1, -1]
+    assert md.tolist() == [24, -1, -1, -1, -1, -1]
+    assert tags[0] == 37 and tags[5] == 22
+    # slot 0 was inserted (category 1), slot 5 was a protected hit (category 2)
+    assert lru.tolist() == [1, 2, 3, 4, 6, 7, 0, 5]
+
+
+def _random_item(rng, n_pages, P, H):
+    host_pages = 2 * n_pages + 3
+    source = rng.permutation(host_pages)[:n_pages].astype(np.int64)
+    source[rng.random(n_pages) < 0.1] = -1  # pages without host backing
+    resident = np.where(rng.random(n_pages) < 0.3, rng.permutation(n_pages) + 50, -1).astype(np.int64)
+    hot = rng.permutation(40)[: -(-H // P)].astype(np.int64)
+    rows = (np.arange(host_pages)[:, None] * P + np.arange(P)).ravel()
+    tags = np.full(H, -1, np.int64)
+    k = int(rng.integers(0, min(H, rows.size) + 1))
+    tags[rng.permutation(H)[:k]] = rng.choice(rows, size=k, replace=False)
+    return source, resident, hot, tags, rng.permutation(H).astype(np.int64)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_resolver_c_restatement_equals_bruteforce_simulation(seed):
+    rng = np.random.default_rng(seed)
+    P = int(rng.integers(1, 6))
+    n_pages = int(rng.integers(1, 12))
+    H = int(rng.integers(1, 24))
+    source, resident, hot, tags, lru = _random_item(rng, n_pages, P, H)
+    t_list, l_list = tags.tolist(), lru.tolist()
+    for _ in range(4):
+        length = int(rng.integers(0, n_pages * P + 1))
+        n = int(rng.integers(1, H + 1))  # the cache admits at most H distinct rows
+        raw = rng.integers(-2, n_pages * P + 3, size=n)
+        got = oracle.resolve_rows(raw, source, resident, hot, tags, lru, length, P)
+        want = oracle.resolve_rows_bruteforce(raw, source, resident, hot, t_list, l_list, length, P)
+        for g, w in zip(got, want):
+            assert g.tolist() == list(w)
+        assert tags.tolist() == t_list and lru.tolist() == l_list
+        assert sorted(lru.tolist()) == list(range(H))
+        assert int(got[3].sum()) == len({int(t) for t in raw if 0 <= t < length and source[min(t // P, n_pages - 1)] >= 0})
+
+
+# ---- Quest ---------------------------------------------------------------------------
+
+
+def test_quest_known_answers():
+    low = torch.tensor([[[-10.0, 0.0]], [[1.0, 0.0]], [[0.0, 0.0]]])[None]
+    high = torch.tensor([[[10.0, 0.0]], [[1.0, 0.0]], [[0.0, 0.0]]])[None]
+    _, pages, pos = oracle.quest_select(torch.tensor([[[1.0, 0.0]]]), low, high, [5], 2, 2, keep_sink=False)
+    assert pages[0].tolist() == [0, 2] and pos[0].tolist() == [0, 1, 4, -1]
+    bounds = torch.tensor([[[9.0, 0.0]], [[0.0, 10.0]], [[-1.0, -1.0]]])[None]
+    _, pages, pos = oracle.quest_select(torch.eye(2)[None], bounds, bounds, [5], 2, 2, keep_sink=False)
+    assert pages[0].tolist() == [1, 2] and pos[0].tolist() == [2, 3, 4, -1]
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.bfloat16, 128), (torch.float16, 24), (torch.float32, 3)])
+def test_quest_scores_closed_form_on_small_integers(dtype, D):
+    """Small-integer queries and bounds make every product and partial sum
+    exact in fp32, so any summation order gives the float64 value."""
+    g = torch.Generator().manual_seed(D)
+    B, Hq, Hkv, n_pages, P = 2, 8, 2, 30, 4
+    q = torch.randint(-8, 9, (B, Hq, D), generator=g).float()
+    a = torch.randint(-8, 9, (B, n_pages, Hkv, D), generator=g).float()
+    c = torch.randint(-8, 9, (B, n_pages, Hkv, D), generator=g).float()
+    mn, mx = torch.minimum(a, c).to(dtype), torch.maximum(a, c).to(dtype)
+    scores, pages, _ = oracle.quest_select(q.to(dtype), mn, mx, [n_pages * P] * B, P, 5)
+    qe = q.double().repeat_interleave(1, 1)
+    kmin = mn.double().repeat_interleave(Hq // Hkv, 2)
+    kmax = mx.double().repeat_interleave(Hq // Hkv, 2)
+    exact = torch.maximum(qe[:, None] * kmin, qe[:, None] * kmax).sum(-1).mean(-1)
+    assert torch.equal(scores.double(), exact)
+    for b in range(B):  # top-5 with page 0 and the last page forced, ties to the lower page
+        rest = sorted(range(1, n_pages - 1), key=lambda p: (-exact[b, p].item(), p))[:3]
+        assert pages[b].tolist() == sorted([0, n_pages - 1, *rest])
+
+
+def test_quest_pages_agree_with_float64_scores_outside_ties():
+    g = torch.Generator().manual_seed(3)
+    B, Hq, Hkv, D, n_pages, P, top = 4, 32, 8, 128, 256, 64, 32
+    q = torch.randn(B, Hq, D, generator=g).bfloat16()
+    a, c = torch.randn(2, B, n_pages, Hkv, D, generator=g)
+    mn, mx = torch.minimum(a, c).bfloat16(), torch.maximum(a, c).bfloat16()
+    scores, pages, _ = oracle.quest_select(q, mn, mx, [n_pages * P] * B, P, top)
+    qe = q.double()
+    kmin, kmax = mn.double().repeat_interleave(4, 2), mx.double().repeat_interleave(4, 2)
+    exact = torch.maximum(qe[:, None] * kmin, qe[:, None] * kmax).sum(-1).mean(-1)
+    assert (scores.double() - exact).abs().max() < 1e-4
+    for b in range(B):
+        ex = exact[b].clone()
+        ex[0] = ex[-1] = float("inf")
+        want = set(ex.topk(top).indices.tolist())
+        got = set(pages[b].tolist())
+        kth = ex.topk(top).values[-1].item()
+        for p in got ^ want:  # any disagreement must be a near-tie at the k-th score
+            assert abs(ex[p].item() - kth) < 1e-4
+
+
+def test_mean_select_forces_first_and_last_page():
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(1, 4, 8, generator=g)
+    summ = torch.randn(1, 10, 2, 8, generator=g)
+    for top in (1, 2, 3, 6):
+        scores, pages, _ = oracle.mean_select(q, summ, [40], 4, top)
+        gq = q[0].view(2, 2, 8).double().mean(1)
+        exact = torch.einsum("hd,phd->p", gq, summ[0].double())
+        required = [9] if top == 1 else [0, 9]
+        rest = sorted((p for p in range(10) if p not in required), key=lambda p: (-exact[p].item(), p))
+        want = sorted(required + rest[: top - len(required)])
+        assert pages[0].tolist() == want
+
+
+# ---- attention and gather ---------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_attention_c_restatement_matches_float64_numpy(dtype):
+    g = torch.Generator().manual_seed(1)
+    P, Hkv, D = 8, 2, 32
+    pool = torch.randn(6, 2, P, Hkv, D, generator=g).to(dtype)
+    q = torch.randn(3, 4, D, generator=g).to(dtype)
+    rows = torch.randint(-1, 6 * P, (3, 20), generator=g)
+    rows[2] = -1
+    a = oracle.attend_rows(q, pool, rows, P)
+    b = oracle.attend_rows_float64(q, pool, rows, P)
+    assert np.abs(a.numpy() - b).max() < 1e-6
+    assert not a[2].any()
+
+
+def test_attention_single_row_and_uniform_keys_closed_forms():
+    P, Hkv, D = 4, 1, 8
+    pool = torch.randn(3, 2, P, Hkv, D)
+    pool[:, 0] = 1.0  # identical keys: uniform weights -> mean of the values
+    q = torch.randn(1, 2, D)
+    rows = torch.tensor([[0, 5, 9, -1]])
+    out = oracle.attend_rows(q, pool, rows, P)
+    mean_v = torch.stack([pool[r // P, 1, r % P, 0] for r in (0, 5, 9)]).mean(0)
+    torch.testing.assert_close(out[0, 0], mean_v, atol=1e-6, rtol=1e-6)
+    out = oracle.attend_rows(q, pool, torch.tensor([[-1, 6, -1]]), P)
+    torch.testing.assert_close(out[0, 1], pool[1, 1, 2, 0], atol=1e-6, rtol=1e-6)
+
+
+def test_gather_closed_form_matches_fancy_indexing():
+    g = torch.Generator().manual_seed(2)
+    P = 5
+    host = torch.randn(9, 2, P, 2, 4, generator=g)
+    pool = torch.zeros(4, 2, P, 2, 4)
+    mh = torch.tensor([3, 44, 17, -1, -1])
+    md = torch.tensor([0, 19, 7, -1, 2])
+    oracle.gather_rows(host, pool, mh, md, P)
+    expected = torch.zeros_like(pool)
+    for h, d in ((3, 0), (44, 19), (17, 7)):
+        expected[d // P, :, d % P] = host[h // P, :, h % P]
+    assert torch.equal(pool, expected)
