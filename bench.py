@@ -239,7 +239,7 @@ def main():
     torch.cuda.set_device(device)
     print(f"[bench] building workload batch={args.batch} context={args.context}", file=sys.stderr, flush=True)
     w = Workload(args.batch, args.context, args.seed, device)
-    w.workspace = torch.empty(
+    w.workspace = torch.zeros(  # split-arrival counters start at zero; the kernel leaves them at zero
         _hip.load().nhs_attend_workspace_bytes(w.batch, w.q_heads, w.head_dim, w.K), dtype=torch.uint8, device=device
     )
     compute = torch.cuda.current_stream(device)

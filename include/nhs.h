@@ -81,7 +81,12 @@ int nhs_gather_rows(const void* host_alias, void* pool,
  * query head of a request shares one row list (the default shared
  * selection); otherwise each head has its own list. Accumulation is fp32;
  * out has the query's dtype. head_dim*kv element size must be a multiple of
- * 16 bytes and at most 1024 bytes.
+ * 16 bytes and at most 2048 bytes; pool rows must be below 2^31. The splits
+ * are merged in the same launch by the last workgroup of each head group,
+ * found with arrival counters in the first 256 KiB of the workspace: that
+ * region must be zero before the first call on a workspace, every call
+ * leaves it at zero, and calls that share a workspace must not overlap.
+ * batch * q_heads <= 65536.
  * Replaces _attend / attend_rows, nano_hisparse/row_kernels.py:73-135 (torch
  * twin nano_hisparse/attention.py:26-35).
  */

@@ -119,6 +119,26 @@ def gather_rows(host, pool, plan, config):
 
 # ---- attention ------------------------------------------------------------------
 
+_workspaces: dict = {}
+
+
+def attend_workspace(device, nbytes):
+    """Zero-initialised attention workspace for the current stream of `device`.
+
+    The kernel's split-arrival counters live at the front of the workspace;
+    they must be zero before a launch and every launch leaves them at zero,
+    so one buffer serves every call on a stream (calls on one stream never
+    overlap). A larger request replaces the buffer.
+    """
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
 
 def attend_batched(query, pool, rows, page_size, out=None, workspace=None):
     """GQA attention of query [B, Hq, D] over rows [B, N] (shared by all heads
@@ -145,11 +165,13 @@ def attend_batched(query, pool, rows, page_size, out=None, workspace=None):
     lib = _hip.load()
     if out is None:
         out = torch.empty(B, Hq, D, dtype=query.dtype, device=device)
-    need = lib.nhs_attend_workspace_bytes(B, Hq, D, max(n_rows, 1))
-    if workspace is None or workspace.numel() * workspace.element_size() < need:
-        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=device)
     if n_rows == 0:
         return out.zero_()
+    need = lib.nhs_attend_workspace_bytes(B, Hq, D, n_rows)
+    if workspace is None:
+        workspace = attend_workspace(device, need)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"attend_rows: workspace holds {workspace.numel() * workspace.element_size()} < {need} bytes")
     status = lib.nhs_attend_rows(
         _ptr(query), dtype_code(query.dtype), query.stride(0), query.stride(1), _ptr(pool), dtype_code(pool.dtype),
         _ptr(rows), r_bs, r_hs, r_cs, B, n_rows, Hq, kv_heads, D, page_size, _ptr(out), out.stride(0),
