@@ -83,9 +83,10 @@ int nhs_gather_rows(const void* host_alias, void* pool,
  * out has the query's dtype. head_dim*kv element size must be a multiple of
  * 16 bytes and at most 2048 bytes; pool rows must be below 2^31. The splits
  * are merged in the same launch by the last workgroup of each head group,
- * found with arrival counters in the first 256 KiB of the workspace: that
- * region must be zero before the first call on a workspace, every call
- * leaves it at zero, and calls that share a workspace must not overlap.
+ * found with arrival counters at the front of the workspace: its first
+ * 260 KiB (the counters and a zero block read in place of masked rows) must
+ * be zero before the first call on a workspace, every call leaves them zero,
+ * and calls that share a workspace must not overlap.
  * batch * q_heads <= 65536.
  * Replaces _attend / attend_rows, nano_hisparse/row_kernels.py:73-135 (torch
  * twin nano_hisparse/attention.py:26-35).

@@ -1,6 +1,6 @@
 // Physical-row GQA decode attention over selected pool rows, one launch.
 //
-// A workgroup of 4 waves owns one request, up to G query heads that share a
+// A workgroup of 8 waves owns one request, up to G query heads that share a
 // row list (the GQA group of one KV head, or one head for per-head lists)
 // and one contiguous split of the row list. A row's K (and V) for a KV head
 // is head_dim contiguous elements = `row_chunks` 16-byte chunks; lane `sub`
@@ -17,11 +17,9 @@
 // The last workgroup of a head group to finish (an arrival counter in the
 // workspace, reset to zero by that workgroup) merges the splits, divides by
 // the softmax denominator (0 when no row was valid) and stores the output in
-// the query's dtype. The workspace's counter region (its first 256 KiB) must
-// be zero before the first call; every call leaves it at zero.
+// the query's dtype. The workspace's first 260 KiB (arrival counters and a
+// zero block) must be zero before the first call; every call leaves them so.
 #include <math.h>
-
-#include <stdlib.h>
 
 #include <mutex>
 #include <vector>
@@ -30,15 +28,19 @@
 
 namespace nhs {
 
-constexpr int kAttendThreads = 256;
+constexpr int kAttendThreads = 512;
 constexpr int kAttendWaves = kAttendThreads / kWave;
-constexpr int kMaxSplits = 64;
+constexpr int kMaxSplits = 32;
 constexpr int kMinRowsPerSplit = 32;
 constexpr int kStage = 1024;  // row indices staged in LDS per pass
 // Arrival counters occupy a fixed region at the front of the workspace, so a
 // call never finds another call's partials where it expects a counter.
 constexpr int kCounterSlots = 65536;
 constexpr int64_t kCounterBytes = kCounterSlots * (int64_t)sizeof(int);
+// A zero block follows the counters; the kernel never writes it and reads it
+// in place of masked rows (it must cover the widest row, 2 KiB).
+constexpr int64_t kZeroBytes = 4096;
+constexpr int64_t kHeaderBytes = kCounterBytes + kZeroBytes;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -55,6 +57,7 @@ struct AttendArgs {
   int lpr_log2, lanes_used, chunks_per_kv;
   FastDiv page_div;
   float qscale;
+  const char* zeros;  // kZeroBytes of zeros
   float* ws;          // partials [B, q_heads, n_splits, 2 + head_dim]
   int* counters;      // [B, gridDim.y]
   void* out;
@@ -69,6 +72,30 @@ __device__ __forceinline__ float packed_dot(uint32_t k, uint32_t q, float acc) {
                                            false);
   else
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, k), __builtin_bit_cast(f16x2_t, q), acc, false);
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int w) {
+  return w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w;
+}
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// two fp32 weights packed as a pair of the KV dtype (bf16: round to nearest
+// even; f16: round toward zero), and back
+template <typename T>
+__device__ __forceinline__ uint32_t pack_pair(float a, float b) {
+  if constexpr (T::dtype == NHS_BF16)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+  else
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+}
+template <typename T>
+__device__ __forceinline__ float pair_lo(uint32_t v) {
+  return T::dtype == NHS_BF16 ? __uint_as_float(v << 16) : f16_bits_to_f32(v & 0xffffu);
+}
+template <typename T>
+__device__ __forceinline__ float pair_hi(uint32_t v) {
+  return T::dtype == NHS_BF16 ? __uint_as_float(v & 0xffff0000u) : f16_bits_to_f32(v >> 16);
 }
 
 // element e (0..E-1) of a 16-byte chunk, as fp32
@@ -170,27 +197,34 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
       krow[i - s0] = kr_idx;
     }
     __syncthreads();
-    for (int base = s0; base < s1; base += per_iter) {
-      uint4 kr[U][C], vr[U][C];
-      bool ok[U];
+    // Software pipeline: the K/V chunks of the next iteration are requested
+    // before the current one is consumed, so every wave keeps two iterations
+    // of loads in flight.
+    uint4 kr[U][C], vr[U][C], kn[U][C], vn[U][C];
+    bool ok[U], okn[U];
+    // Loads are unconditional: masked rows, padding lanes and rows past the
+    // end read the workspace's zero block instead, so no branch separates a
+    // load from its use and the compiler can keep the prefetch in flight.
+    auto issue = [&](int base, uint4 (&kd)[U][C], uint4 (&vd)[U][C], bool (&okd)[U]) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c_idx = base + (u * kAttendWaves + wave) * slots + slot;
         const uint32_t ki = c_idx < s1 ? krow[c_idx - s0] : 0xffffffffu;
-        ok[u] = ki != 0xffffffffu;
-        if (ok[u] && data_lane) {
-          const char* kp = pool + (int64_t)ki * row_bytes;
+        okd[u] = ki != 0xffffffffu;
+        const bool live = okd[u] && data_lane;
+        const char* kp = live ? pool + (int64_t)ki * row_bytes : a.zeros;
+        const int64_t vo = live ? plane_bytes : 0;
 #pragma unroll
-          for (int c = 0; c < C; ++c) {
-            const int64_t cb = (int64_t)(c * a.lanes_used + sub) * 16;
-            kr[u][c] = *reinterpret_cast<const uint4*>(kp + cb);
-            vr[u][c] = *reinterpret_cast<const uint4*>(kp + plane_bytes + cb);
-          }
-        } else {
-#pragma unroll
-          for (int c = 0; c < C; ++c) kr[u][c] = vr[u][c] = make_uint4(0u, 0u, 0u, 0u);
+        for (int c = 0; c < C; ++c) {
+          const int64_t cb = (int64_t)(c * a.lanes_used + sub) * 16;
+          kd[u][c] = *reinterpret_cast<const uint4*>(kp + cb);
+          vd[u][c] = *reinterpret_cast<const uint4*>(kp + vo + cb);
         }
       }
+    };
+    issue(s0, kr, vr, ok);
+    for (int base = s0; base < s1; base += per_iter) {
+      issue(base + per_iter, kn, vn, okn);  // past the end: zero-block reads
       float p[G][U], alpha[G];
 #pragma unroll
       for (int g = 0; g < G; ++g)
@@ -257,31 +291,82 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
           mx = fmaxf(mx, p[g][u]);
         }
         const float ref = mx == -INFINITY ? 0.f : mx;  // keeps exp2 arguments finite
-        alpha[g] = exp2f(m[g] - ref);
-        float psum = 0.f;
+        // arguments are <= 0: v_exp_f32 without range reduction (a weight below
+        // 2^-126 flushes to 0)
+        alpha[g] = __builtin_amdgcn_exp2f(m[g] - ref);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          p[g][u] = exp2f(p[g][u] - ref);
-          psum += p[g][u];
-        }
-        l[g] = l[g] * alpha[g] + psum;
+        for (int u = 0; u < U; ++u) p[g][u] = __builtin_amdgcn_exp2f(p[g][u] - ref);
         m[g] = mx;
       }
 #pragma unroll
-      for (int c = 0; c < C; ++c)
+      for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-          float v[U];
+        for (int c = 0; c < C; ++c)
 #pragma unroll
-          for (int u = 0; u < U; ++u) v[u] = chunk_elem<T>(vr[u][c], e);
+          for (int e = 0; e < E; ++e) acc[g][c][e] *= alpha[g];
+      if constexpr (PK) {
+        // P.V with v_dot2 over pairs of rows: the weights are rounded to the
+        // KV dtype and the denominator sums the same rounded weights, so the
+        // output stays an exact convex combination of the V rows.
+        uint32_t pp[G][U / 2];
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            float x = acc[g][c][e] * alpha[g];
+        for (int g = 0; g < G; ++g) {
+          float psum = 0.f;
 #pragma unroll
-            for (int u = 0; u < U; ++u) x += p[g][u] * v[u];
-            acc[g][c][e] = x;
+          for (int j = 0; j < U / 2; ++j) {
+            pp[g][j] = pack_pair<T>(p[g][2 * j], p[g][2 * j + 1]);
+            psum += pair_lo<T>(pp[g][j]) + pair_hi<T>(pp[g][j]);
           }
+          l[g] = l[g] * alpha[g] + psum;
         }
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+#pragma unroll
+            for (int j = 0; j < U / 2; ++j) {
+              const uint32_t x = word_of(vr[2 * j][c], w), y = word_of(vr[2 * j + 1][c], w);
+              const uint32_t lo = __builtin_amdgcn_perm(y, x, 0x05040100u);  // (x.lo, y.lo)
+              const uint32_t hi = __builtin_amdgcn_perm(y, x, 0x07060302u);  // (x.hi, y.hi)
+#pragma unroll
+              for (int g = 0; g < G; ++g) {
+                acc[g][c][2 * w] = packed_dot<T>(lo, pp[g][j], acc[g][c][2 * w]);
+                acc[g][c][2 * w + 1] = packed_dot<T>(hi, pp[g][j], acc[g][c][2 * w + 1]);
+              }
+            }
+      } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float psum = 0.f;
+#pragma unroll
+          for (int u = 0; u < U; ++u) psum += p[g][u];
+          l[g] = l[g] * alpha[g] + psum;
+        }
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            float v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = chunk_elem<T>(vr[u][c], e);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              float x = acc[g][c][e];
+#pragma unroll
+              for (int u = 0; u < U; ++u) x += p[g][u] * v[u];
+              acc[g][c][e] = x;
+            }
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        ok[u] = okn[u];
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          kr[u][c] = kn[u][c];
+          vr[u][c] = vn[u][c];
+        }
+      }
     }
   }
 
@@ -349,8 +434,6 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
   }
 
   // the last workgroup of this head group merges the splits
-  __shared__ float split_m[8 * kMaxSplits];
-  __shared__ float split_w[8 * kMaxSplits];
   // The partials were written with agent-coherent stores; waiting for them to
   // complete before the arrival orders them without an L2 writeback (an
   // agent-scope fence would write back and invalidate this XCD's whole L2).
@@ -363,33 +446,28 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
   if (!last_arrival) return;
   const float* base_part = a.ws + ((int64_t)b * a.q_heads + h0) * a.n_splits * stride;
   const int ns = a.n_splits;
-  for (int idx = threadIdx.x; idx < nh * ns; idx += kAttendThreads) {
-    const int g = idx / ns, s = idx - g * ns;
-    const float* hp = base_part + ((int64_t)g * ns + s) * stride;
-    split_m[idx] = ld_coherent(hp);
-    split_w[idx] = ld_coherent(hp + 1);
-  }
-  __syncthreads();
-  if (threadIdx.x < nh) {
-    const int g = threadIdx.x;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, split_m[g * ns + s]);
-    float L = 0.f;
-    if (M != -INFINITY)
-      for (int s = 0; s < ns; ++s) L += split_w[g * ns + s] * exp2f(split_m[g * ns + s] - M);
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    for (int s = 0; s < ns; ++s)  // weight of split s in the output
-      split_w[g * ns + s] = inv > 0.f ? exp2f(split_m[g * ns + s] - M) * inv : 0.f;
-  }
-  __syncthreads();
+  // Each thread loads, in one batch, the split statistics of its head and
+  // its element of every split, then merges them.
   for (int idx = threadIdx.x; idx < nh * a.head_dim; idx += kAttendThreads) {
     const int g = idx / a.head_dim;
     const int d = idx - g * a.head_dim;
-    const float* hp = base_part + (int64_t)g * ns * stride + 2 + d;
-    const float* wg = split_w + g * ns;
-    float v = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < ns; ++s) v += ld_coherent(hp + (int64_t)s * stride) * wg[s];
+    const float* hp = base_part + (int64_t)g * ns * stride;
+    float ms[kMaxSplits], ls[kMaxSplits], vs[kMaxSplits];
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) {
+      ms[s] = ld_coherent(hp + (int64_t)s * stride);
+      ls[s] = ld_coherent(hp + (int64_t)s * stride + 1);
+      vs[s] = ld_coherent(hp + (int64_t)s * stride + 2 + d);
+    }
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, ms[s]);
+    float L = 0.f, v = 0.f;
+    if (M != -INFINITY)
+      for (int s = 0; s < ns; ++s) {
+        const float w = exp2f(ms[s] - M);
+        L += ls[s] * w;
+        v += vs[s] * w;
+      }
+    v = L > 0.f ? v / L : 0.f;
     store_elem(a.out, a.out_dtype, (int64_t)b * a.out_bs + (int64_t)(h0 + g) * a.out_hs + d, v);
   }
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -430,32 +508,19 @@ static int max_splits_for(int n_rows) {
   return s < 1 ? 1 : s > kMaxSplits ? kMaxSplits : s;
 }
 
-// Workgroups of `kernel` resident on the whole current device at once,
-// cached per (device, kernel, LDS size).
-static int device_capacity(AttendKernel kernel, size_t lds) {
-  struct Entry {
-    int dev;
-    AttendKernel kernel;
-    size_t lds;
-    int capacity;
-  };
+// Compute units of the current device (cached per device).
+static int device_cus() {
   static std::mutex mu;
-  static std::vector<Entry> cache;
+  static std::vector<std::pair<int, int>> cache;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    for (const Entry& e : cache)
-      if (e.dev == dev && e.kernel == kernel && e.lds == lds) return e.capacity;
-  }
-  int cus = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), kAttendThreads,
-                                                   lds) != hipSuccess)
-    return 0;
   std::lock_guard<std::mutex> lock(mu);
-  cache.push_back({dev, kernel, lds, per_cu * cus});
-  return per_cu * cus;
+  for (const auto& e : cache)
+    if (e.first == dev) return e.second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  cache.emplace_back(dev, cus);
+  return cus;
 }
 
 }  // namespace nhs
@@ -463,7 +528,7 @@ static int device_capacity(AttendKernel kernel, size_t lds) {
 extern "C" int64_t nhs_attend_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_dim, int32_t n_rows) {
   if (batch < 1 || q_heads < 1 || head_dim < 1 || n_rows < 1) return 0;
   int64_t partials = (int64_t)batch * q_heads * nhs::max_splits_for(n_rows) * (head_dim + 2) * (int64_t)sizeof(float);
-  return nhs::kCounterBytes + partials;
+  return nhs::kHeaderBytes + partials;
 }
 
 extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_batch_stride, int64_t q_head_stride,
@@ -508,8 +573,7 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
   a.head_dim = head_dim;
   a.page_size = page_size;
   a.page_div = FastDiv((uint32_t)page_size);
-  int C = row_chunks > 64 ? 2 : 1;
-  if (const char* env = getenv("NHS_ATTEND_C")) C = atoi(env) == 2 && row_chunks % 2 == 0 ? 2 : 1;  // TEMP tuning
+  const int C = row_chunks > 64 ? 2 : 1;
   if (row_chunks / C > 64) return fail(NHS_ERR_UNSUPPORTED, "nhs_attend_rows: rows too wide");
   a.lanes_used = row_chunks / C;
   a.lpr_log2 = ilog2(a.lanes_used);
@@ -529,14 +593,17 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
   const size_t lds = (size_t)kAttendWaves * G * (2 + head_dim) * sizeof(float);
   const int groups = kv_heads * a.chunks_per_kv;
   const int items = batch * groups;
-  const int capacity = device_capacity(kernel, lds);
-  int splits = capacity > 0 ? capacity / items : 1;
+  // One balanced round: about one 8-wave workgroup per CU. (Partial rounds
+  // leave some CUs with twice the work; extra workgroups add merges.)
+  const int cus = device_cus();
+  int splits = cus > 0 ? (cus + items / 2) / items : 1;
   if (splits < 1) splits = 1;
   if (splits > max_splits_for(n_rows)) splits = max_splits_for(n_rows);
   a.n_splits = splits;
   a.rows_per_split = (n_rows + splits - 1) / splits;
   a.counters = static_cast<int*>(workspace);
-  a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  a.zeros = static_cast<const char*>(workspace) + kCounterBytes;
+  a.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kHeaderBytes);
   a.out = out;
   a.out_dtype = q_dtype;
   a.out_bs = out_batch_stride;
