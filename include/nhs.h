@@ -129,9 +129,11 @@ int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t po
  * Quest page selection for `batch` requests. Request b scores each of its
  * count = ceil(lengths[b]/page_size) pages (count is clamped to max_pages):
  *   score[p] = (sum_h sum_d max(q[h,d]*min[p,h/g,d], q[h,d]*max[p,h/g,d])) / q_heads
- * in fp32 with a fixed summation order (per lane: sequential over its 16
- * bytes of bound elements; across lanes: pairwise tree; across heads:
- * sequential h = 0..q_heads-1). Page count-1, and page 0 when keep_sink and
+ * in fp32 with a fixed summation order (per lane: from 0.0, sequential over
+ * its 16 bytes of bound elements, each term added as
+ * fma(min(q,0), min, fma(max(q,0), max, t)); across lanes: pairwise tree;
+ * across heads: sequential h = 0..q_heads-1). q_heads/kv_heads <= 8.
+ * Page count-1, and page 0 when keep_sink and
  * top_pages > 1 and count > 1, score +inf. The top_pages pages by (score
  * descending, page ascending) are written ascending to pages[b, :top_pages]
  * (-1 padded when count < top_pages) and expanded to causal token positions

@@ -5,9 +5,9 @@
 // The semantics are those of resolve_rows (nano_hisparse/row_index.py:62-140),
 // restated as LDS passes instead of sorts over the hot rows:
 //  1. keys (norm << 32 | input index), norm = raw if 0 <= raw < length else
-//     length, bitonic-sorted in LDS: sorted order = ascending logical, and
-//     the first entry of each run of equal positions is its first occurrence
-//     in the input.
+//     length, bitonic-sorted in LDS unless already in order: sorted order =
+//     ascending logical, and the first entry of each run of equal positions
+//     is its first occurrence in the input.
 //  2. per sorted entry: page/offset, source and resident tables, host row,
 //     valid / resident_hit / needs_hot.
 //  3. an LDS hash of the host rows that need the hot buffer.
@@ -142,7 +142,12 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     sh.u.keys[i] = key;
   }
   __syncthreads();
-  for (int k = 2; k <= kp; k <<= 1) {
+  // Selector output is already in order (ascending positions, -1 padding at
+  // the end maps to `length`); the sort is skipped when no pair is inverted.
+  int inverted = 0;
+  for (int i = tid; i + 1 < n; i += kResolveThreads) inverted |= sh.u.keys[i] > sh.u.keys[i + 1];
+  const bool sorted = !__syncthreads_or(inverted);
+  for (int k = 2; !sorted && k <= kp; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int i = tid; i < kp; i += kResolveThreads) {
         int ixj = i ^ j;

@@ -26,7 +26,8 @@ namespace nhs {
 
 constexpr int kScoreThreads = 256;
 constexpr int kScoreWaves = kScoreThreads / kWave;
-constexpr int kPagesPerBlock = 32;
+constexpr int kPagesPerBlock = 8;
+constexpr int kQuestThreads = 512;
 constexpr int kSelectThreads = 1024;
 constexpr int kMaxSelectPerThread = NHS_MAX_SELECT_PAGES / kSelectThreads;  // 16
 
@@ -39,8 +40,9 @@ struct ScoreArgs {
   const void* lo;   // quest: minimum; mean: summaries (fp32)
   const void* hi;   // quest: maximum
   int64_t b_bs;     // elements between requests' bound tensors
-  int q_heads, kv_heads, head_dim;
+  int q_heads, kv_heads, head_dim, group;
   int lanes_used, lpr_log2;
+  int pages_per_step, pages_per_block;
   const int64_t* lengths;
   int64_t length;
   int page_size, max_pages;
@@ -61,59 +63,90 @@ __device__ __forceinline__ int page_count(const int64_t* lengths, int64_t length
 }
 
 // Quest bounds score: (sum_h sum_d max(q*min, q*max)) / q_heads.
-template <typename T, int E>
-__global__ __launch_bounds__(kScoreThreads) void quest_score_kernel(ScoreArgs a) {
+//
+// The term max(q*kmin, q*kmax) is evaluated as fma(q-, kmin, fma(q+, kmax, t))
+// with q+ = max(q, 0) and q- = min(q, 0) (kmax >= kmin): for 16-bit queries
+// and bounds both products are exact, so this adds the reference's term to t
+// (up to the sign of a zero). Lanes are laid out as (page of the step, kv
+// head, 16-byte chunk), so a lane keeps one kv head's query slices in
+// registers for the whole kernel; the next step's bounds are requested
+// before the current step is summed.
+template <typename T, int E, int G>
+__global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ float smem[];
-  float* qs = smem;                                   // [q_heads * head_dim]
-  float* hs = smem + a.q_heads * a.head_dim;          // [waves][q_heads]
+  const int pages_per_step = a.pages_per_step;
+  float* qs = smem;                              // [q_heads * head_dim]
+  float* hs = smem + a.q_heads * a.head_dim;     // [pages_per_step][q_heads]
   const int b = blockIdx.y;
   const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
-  const int p_begin = blockIdx.x * kPagesPerBlock;
+  const int p_begin = blockIdx.x * a.pages_per_block;
   if (p_begin >= count) return;
-  for (int i = threadIdx.x; i < a.q_heads * a.head_dim; i += kScoreThreads) {
-    int h = i / a.head_dim, d = i - h * a.head_dim;
+  const int p_end = min(count, p_begin + a.pages_per_block);
+  for (int i = threadIdx.x; i < a.q_heads * a.head_dim; i += blockDim.x) {
+    const int h = i / a.head_dim, d = i - h * a.head_dim;
     qs[i] = load_elem(a.q, a.q_dtype, (int64_t)b * a.q_bs + (int64_t)h * a.q_hs + d);
   }
   __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lpr = 1 << a.lpr_log2;
-  const int heads_per_pass = kWave >> a.lpr_log2;
-  const int sub = lane & (lpr - 1);
-  const int group = a.q_heads / a.kv_heads;
-  const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
-  for (int it = 0; it < kPagesPerBlock / kScoreWaves; ++it) {
-    const int p = p_begin + it * kScoreWaves + wave;
-    const bool live = p < count;
-    for (int kh0 = 0; kh0 < a.kv_heads; kh0 += heads_per_pass) {
-      const int kh = kh0 + (lane >> a.lpr_log2);
-      const bool data = live && kh < a.kv_heads && sub < a.lanes_used;
-      float mn[E], mx[E];
-      if (data) {
-        int64_t idx = (int64_t)b * a.b_bs + (int64_t)p * page_elems + (int64_t)kh * a.head_dim + sub * E;
-        load_vec<T, E>(a.lo, idx, mn);
-        load_vec<T, E>(a.hi, idx, mx);
-      }
-      for (int g = 0; g < group; ++g) {
-        const int h = (kh < a.kv_heads ? kh : 0) * group + g;
-        float t = 0.f;
-        if (data) {
-          const float* qh = qs + h * a.head_dim + sub * E;
-          t = torch_maximum(qh[0] * mn[0], qh[0] * mx[0]);
+  const int lanes_per_page = a.kv_heads << a.lpr_log2;
+  const int page_local = threadIdx.x / lanes_per_page;
+  const int within = threadIdx.x - page_local * lanes_per_page;
+  const int kh = within >> a.lpr_log2;
+  const int sub = within & (lpr - 1);
+  const bool active = page_local < pages_per_step;
+  const bool data = active && sub < a.lanes_used;
+  float qp[G][E], qn[G][E];
 #pragma unroll
-          for (int e = 1; e < E; ++e) t = t + torch_maximum(qh[e] * mn[e], qh[e] * mx[e]);
-        }
-        t = group_sum(t, lpr);
-        if (live && kh < a.kv_heads && sub == 0) hs[wave * a.q_heads + h] = t;
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float q = data && g < a.group ? qs[(kh * a.group + g) * a.head_dim + sub * E + e] : 0.f;
+      qp[g][e] = q > 0.f ? q : 0.f;
+      qn[g][e] = q < 0.f ? q : 0.f;
+    }
+  const char* lo = static_cast<const char*>(a.lo) + (int64_t)b * a.b_bs * T::bytes;
+  const char* hi = static_cast<const char*>(a.hi) + (int64_t)b * a.b_bs * T::bytes;
+  const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
+  const int64_t lane_off = data ? (int64_t)kh * a.head_dim + sub * E : 0;
+  auto load = [&](int p, float (&mn)[E], float (&mx)[E]) {
+    const int pc = (active && p < p_end) ? p : p_begin;  // idle lanes reread a live page
+    load_vec<T, E>(lo, (int64_t)pc * page_elems + lane_off, mn);
+    load_vec<T, E>(hi, (int64_t)pc * page_elems + lane_off, mx);
+  };
+  float mn[E], mx[E], mn2[E], mx2[E];
+  load(p_begin + page_local, mn, mx);
+  for (int base = p_begin; base < p_end; base += pages_per_step) {
+    const int p = base + page_local;
+    load(p + pages_per_step, mn2, mx2);
+    float t[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float x = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        x = __builtin_fmaf(qp[g][e], mx[e], x);
+        x = __builtin_fmaf(qn[g][e], mn[e], x);
       }
+      t[g] = group_sum(x, lpr);
+    }
+    if (active && sub == 0 && p < p_end)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (g < a.group) hs[page_local * a.q_heads + kh * a.group + g] = t[g];
+    __syncthreads();
+    if ((int)threadIdx.x < pages_per_step && base + (int)threadIdx.x < p_end) {
+      const float* row = hs + threadIdx.x * a.q_heads;
+      float total = row[0];
+      for (int h = 1; h < a.q_heads; ++h) total = total + row[h];
+      a.scores[(int64_t)b * a.max_pages + base + threadIdx.x] = total / (float)a.q_heads;
     }
     __syncthreads();
-    if (live && lane == 0) {
-      float total = hs[wave * a.q_heads];
-      for (int h = 1; h < a.q_heads; ++h) total = total + hs[wave * a.q_heads + h];
-      a.scores[(int64_t)b * a.max_pages + p] = total / (float)a.q_heads;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      mn[e] = mn2[e];
+      mx[e] = mx2[e];
     }
-    __syncthreads();
   }
 }
 
@@ -349,7 +382,7 @@ extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtyp
   if (st != NHS_OK) return st;
   if (!minimum || !maximum) return fail(NHS_ERR_INVALID, "%s: null bounds", who);
   if (!valid_dtype(bounds_dtype)) return fail(NHS_ERR_INVALID, "%s: bad bounds dtype", who);
-  if ((int64_t)q_heads * head_dim + 4 * q_heads > 16384)
+  if ((int64_t)q_heads * head_dim + 8 * q_heads > 16384)
     return fail(NHS_ERR_UNSUPPORTED, "%s: q_heads * head_dim too large", who);
   const int esize = elem_size(bounds_dtype);
   const int E = chunk_elems(head_dim, esize);
@@ -376,17 +409,35 @@ extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtyp
   a.page_size = page_size;
   a.max_pages = max_pages;
   a.scores = scores;
-  dim3 grid((unsigned)((max_pages + kPagesPerBlock - 1) / kPagesPerBlock), (unsigned)batch);
-  size_t lds = ((size_t)q_heads * head_dim + (size_t)kScoreWaves * q_heads) * sizeof(float);
+  a.group = q_heads / kv_heads;
+  const int lanes_per_page = kv_heads << a.lpr_log2;
+  if (a.group > 8 || lanes_per_page > kQuestThreads)
+    return fail(NHS_ERR_UNSUPPORTED, "%s: needs q_heads/kv_heads <= 8 and kv_heads * lanes per head <= %d", who,
+                kQuestThreads);
+  const int threads = lanes_per_page >= 256 ? ((lanes_per_page + 63) / 64) * 64 : 256;
+  a.pages_per_step = threads / lanes_per_page;
+  a.pages_per_block = a.pages_per_step * ((kPagesPerBlock + a.pages_per_step - 1) / a.pages_per_step);
+  dim3 grid((unsigned)((max_pages + a.pages_per_block - 1) / a.pages_per_block), (unsigned)batch);
+  size_t lds = ((size_t)q_heads * head_dim + (size_t)a.pages_per_step * q_heads) * sizeof(float);
   if (top_pages < max_pages) {  // scores are not needed when every page is kept
-    switch (bounds_dtype * 16 + E) {
-      case NHS_F32 * 16 + 4: hipLaunchKernelGGL((quest_score_kernel<F32, 4>), grid, dim3(kScoreThreads), lds, s, a); break;
-      case NHS_F32 * 16 + 1: hipLaunchKernelGGL((quest_score_kernel<F32, 1>), grid, dim3(kScoreThreads), lds, s, a); break;
-      case NHS_F16 * 16 + 8: hipLaunchKernelGGL((quest_score_kernel<F16, 8>), grid, dim3(kScoreThreads), lds, s, a); break;
-      case NHS_F16 * 16 + 1: hipLaunchKernelGGL((quest_score_kernel<F16, 1>), grid, dim3(kScoreThreads), lds, s, a); break;
-      case NHS_BF16 * 16 + 8: hipLaunchKernelGGL((quest_score_kernel<BF16, 8>), grid, dim3(kScoreThreads), lds, s, a); break;
-      default: hipLaunchKernelGGL((quest_score_kernel<BF16, 1>), grid, dim3(kScoreThreads), lds, s, a); break;
+    const int G = a.group == 1 ? 1 : a.group == 2 ? 2 : a.group <= 4 ? 4 : 8;
+    void (*kernel)(ScoreArgs) = nullptr;
+    switch (bounds_dtype * 64 + E * 8 + G) {
+#define NHS_QUEST_CASE(DT, TY, EE, GG) \
+  case DT * 64 + EE * 8 + GG: kernel = quest_score_kernel<TY, EE, GG>; break;
+#define NHS_QUEST_GS(DT, TY, EE) \
+  NHS_QUEST_CASE(DT, TY, EE, 1) NHS_QUEST_CASE(DT, TY, EE, 2) NHS_QUEST_CASE(DT, TY, EE, 4) NHS_QUEST_CASE(DT, TY, EE, 8)
+      NHS_QUEST_GS(NHS_F32, F32, 4)
+      NHS_QUEST_GS(NHS_F32, F32, 1)
+      NHS_QUEST_GS(NHS_F16, F16, 8)
+      NHS_QUEST_GS(NHS_F16, F16, 1)
+      NHS_QUEST_GS(NHS_BF16, BF16, 8)
+      NHS_QUEST_GS(NHS_BF16, BF16, 1)
+#undef NHS_QUEST_GS
+#undef NHS_QUEST_CASE
     }
+    if (!kernel) return fail(NHS_ERR_UNSUPPORTED, "%s: no scoring kernel", who);
+    hipLaunchKernelGGL(kernel, grid, dim3(threads), lds, s, a);
     st = launch_status(who);
     if (st != NHS_OK) return st;
   }

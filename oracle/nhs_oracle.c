@@ -17,10 +17,16 @@
  * follow exactly (the reference sums in torch's CPU reduction order, which
  * no other implementation reproduces): a bound row of head_dim elements is
  * cut into E-element chunks (E = 16 bytes / element size when the row is a
- * multiple of 16 bytes, else 1); each chunk is summed sequentially; the
- * chunk sums, padded with +0.0 to a power of two, are added as a pairwise
- * tree in chunk order; the per-head sums are added sequentially. Build with
- * -ffp-contract=off so products are rounded before they are added.
+ * multiple of 16 bytes, else 1); each chunk is summed sequentially from
+ * 0.0; the chunk sums, padded with +0.0 to a power of two, are added as a
+ * pairwise tree in chunk order; the per-head sums are added sequentially.
+ * The Quest term max(q*kmin, q*kmax) (selection.py:84) is accumulated as
+ * fma(q-, kmin, fma(q+, kmax, t)) with q+ = max(q, 0), q- = min(q, 0): for
+ * 16-bit queries and bounds the products are exact, so each step adds the
+ * reference's term (up to the sign of a zero); for fp32 inputs the products
+ * are not rounded before the addition. The mean selector rounds each
+ * product before adding it. Build with -ffp-contract=off so no other
+ * product is fused.
  */
 #include <math.h>
 #include <stdint.h>
@@ -151,11 +157,6 @@ static float tree_sum(float* t, int L) {
   return t[0];
 }
 
-static float torch_maximum(float a, float b) {
-  if (a != a || b != b) return a + b;
-  return a > b ? a : b;
-}
-
 static int page_count(int64_t len, int page_size, int max_pages) {
   if (len <= 0) return 0;
   int64_t c = (len + page_size - 1) / page_size;
@@ -178,10 +179,13 @@ static void quest_scores_one(const void* q, int q_dtype, int64_t q_hs, const voi
         t[l] = 0.0f;
         if (l >= used) continue;
         for (int e = 0; e < E; ++e) {
+          /* max(q*kmin, q*kmax) added to t as fma(q-, kmin, fma(q+, kmax, t)):
+             exact for 16-bit inputs, whose products fit in fp32 */
           int d = l * E + e;
           float qd = load_elem(q, q_dtype, (int64_t)h * q_hs + d);
-          float x = torch_maximum(qd * load_elem(lo, bdt, base + d), qd * load_elem(hi, bdt, base + d));
-          t[l] = e == 0 ? x : t[l] + x;
+          float qpos = qd > 0.0f ? qd : 0.0f, qneg = qd < 0.0f ? qd : 0.0f;
+          t[l] = fmaf(qpos, load_elem(hi, bdt, base + d), t[l]);
+          t[l] = fmaf(qneg, load_elem(lo, bdt, base + d), t[l]);
         }
       }
       hs[h] = tree_sum(t, L);
