@@ -1,0 +1,95 @@
+"""Device blocks of the KV pool: ownership, reference counts and reuse.
+
+Reference: nano_hisparse/allocator.py:9-83. One pool tensor of
+[gpu_pages, 2, page_size, kv_heads, head_dim] holds resident pages and hot
+blocks alike. A block bound to an owner carries one allocation reference;
+readers add temporary references. A block whose allocation reference was
+given up (unpinned) stays readable until it is reclaimed, which runs the
+owner's callback; `fence` is the event that must complete before the block's
+bytes may be overwritten.
+"""
+
+from __future__ import annotations
+
+from collections import Counter, OrderedDict
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass
+class DeviceSlot:
+    owner: tuple | None = None
+    ref_cnt: int = 0
+    fence: object = None
+
+
+class DeviceAllocator:
+    def __init__(self, config):
+        self.storage = torch.empty(
+            (config.gpu_pages, 2, config.page_size, config.kv_heads, config.head_dim),
+            device=config.device,
+            dtype=config.dtype,
+        )
+        self.budget = config.gpu_pages
+        self.slots = [DeviceSlot() for _ in range(config.gpu_pages)]
+        self.free: set[int] = set(range(config.gpu_pages))
+        # slot -> callback run when an unpinned (still readable) block is taken
+        self.reclaimable: OrderedDict[int, object] = OrderedDict()
+        # owner key -> slot, in binding order
+        self.lru: OrderedDict[tuple, int] = OrderedDict()
+        self.occupancy: Counter = Counter()
+
+    def _allocation_refs(self, slot) -> int:
+        return 0 if slot in self.reclaimable else 1
+
+    def bind(self, slot, key):
+        frame = self.slots[slot]
+        assert slot in self.free and slot < self.budget
+        assert frame.owner is None and frame.ref_cnt == 0
+        self.free.discard(slot)
+        frame.owner, frame.ref_cnt = key, 1
+        self.lru[key] = slot
+        self.occupancy[key[0]] += 1
+
+    def release(self, slot, fence):
+        frame = self.slots[slot]
+        assert frame.owner is not None
+        if frame.ref_cnt != self._allocation_refs(slot):
+            raise RuntimeError("cannot release a block with active references")
+        owner = frame.owner
+        self.reclaimable.pop(slot, None)
+        del self.lru[owner]
+        self.occupancy[owner[0]] -= 1
+        frame.owner, frame.ref_cnt, frame.fence = None, 0, fence
+        self.free.add(slot)
+
+    def unpin(self, slot, on_reuse):
+        """Give up the allocation reference; contents stay readable."""
+        frame = self.slots[slot]
+        assert frame.owner is not None and slot not in self.free
+        if slot in self.reclaimable:
+            return
+        assert frame.ref_cnt > 0
+        frame.ref_cnt -= 1
+        self.reclaimable[slot] = on_reuse
+
+    def reclaim(self, slot):
+        """Take an unpinned block: its owner callback detaches the old mapping."""
+        if self.slots[slot].ref_cnt:
+            raise RuntimeError("cannot reclaim a block with active references")
+        callback = self.reclaimable[slot]
+        callback(slot)
+        assert slot in self.free and slot not in self.reclaimable
+
+    def incref(self, slot):
+        frame = self.slots[slot]
+        if frame.owner is None:
+            raise RuntimeError("cannot reference an unbound block")
+        frame.ref_cnt += 1
+
+    def decref(self, slot):
+        frame = self.slots[slot]
+        if frame.owner is None or frame.ref_cnt <= self._allocation_refs(slot):
+            raise RuntimeError("no reader reference to release")
+        frame.ref_cnt -= 1

@@ -1,0 +1,206 @@
+"""A small Qwen2-shaped decoder that drives the sparse decode path.
+
+Reference: nano_hisparse/model.py:19-221. Dense layers (projections, RoPE,
+RMSNorm, SwiGLU, the prefill's causal attention) are torch operations; each
+decode step appends K/V through the cache, selects pages with Quest on the
+GPU and attends over the selected rows with the HIP kernels. The module tree
+(names and construction order) is the reference's, which is HF Qwen2's, so
+state dicts load either way and a seeded random init draws the same weights.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from .selection import Selection, quest_selection, select_pages
+
+
+@dataclass
+class ModelConfig:
+    vocab_size: int = 256
+    hidden_size: int = 128
+    intermediate_size: int = 256
+    num_hidden_layers: int = 2
+    num_attention_heads: int = 4
+    num_key_value_heads: int = 2
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 10000.0
+
+    @property
+    def head_dim(self):
+        return self.hidden_size // self.num_attention_heads
+
+    def __post_init__(self):
+        if (
+            self.hidden_size % self.num_attention_heads
+            or self.num_attention_heads % self.num_key_value_heads
+            or self.head_dim % 2
+        ):
+            raise ValueError("model dimensions must support grouped-query attention and RoPE")
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, width, eps):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(width))
+        self.eps = eps
+
+    def forward(self, x):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + self.eps)).to(x.dtype) * self.weight
+
+
+class Projections(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        kv_width = cfg.num_key_value_heads * cfg.head_dim
+        self.q_proj = nn.Linear(cfg.hidden_size, cfg.hidden_size, bias=True)
+        self.k_proj = nn.Linear(cfg.hidden_size, kv_width, bias=True)
+        self.v_proj = nn.Linear(cfg.hidden_size, kv_width, bias=True)
+        self.o_proj = nn.Linear(cfg.hidden_size, cfg.hidden_size, bias=False)
+
+
+class MLP(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.gate_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False)
+        self.up_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class Block(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.self_attn = Projections(cfg)
+        self.mlp = MLP(cfg)
+
+
+class Decoder(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
+        self.layers = nn.ModuleList(Block(cfg) for _ in range(cfg.num_hidden_layers))
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+
+
+class Model(nn.Module):
+    def __init__(self, config: ModelConfig | None = None):
+        super().__init__()
+        self.config = config or ModelConfig()
+        self.model = Decoder(self.config)
+        self.lm_head = nn.Linear(self.config.hidden_size, self.config.vocab_size, bias=False)
+
+    @classmethod
+    def from_pretrained(cls, name: str, device="cuda", dtype=torch.bfloat16):
+        """Qwen2/Qwen2.5 weights with standard RoPE from a local directory or
+        an already-cached hub name (no network is assumed)."""
+        from transformers import AutoConfig, AutoModelForCausalLM
+
+        hf_cfg = AutoConfig.from_pretrained(name)
+        rope = getattr(hf_cfg, "rope_parameters", None) or getattr(hf_cfg, "rope_scaling", None) or {}
+        if hf_cfg.model_type != "qwen2" or rope.get("rope_type", rope.get("type", "default")) != "default":
+            raise ValueError("only Qwen2/Qwen2.5 with standard RoPE are supported")
+        if getattr(hf_cfg, "use_sliding_window", False) or hf_cfg.hidden_act != "silu":
+            raise ValueError("sliding window / non-SiLU models are unsupported")
+        hf = AutoModelForCausalLM.from_pretrained(name, torch_dtype=dtype).eval().to(device)
+        model = cls.__new__(cls)
+        nn.Module.__init__(model)
+        fields = {f: getattr(hf_cfg, f) for f in ModelConfig.__dataclass_fields__ if f != "rope_theta"}
+        fields["rope_theta"] = rope.get("rope_theta", getattr(hf_cfg, "rope_theta", 10000.0))
+        model.config = ModelConfig(**fields)
+        model.model, model.lm_head = hf.model, hf.lm_head
+        return model.eval()
+
+    @property
+    def device(self):
+        return self.model.embed_tokens.weight.device
+
+    @property
+    def dtype(self):
+        return self.model.embed_tokens.weight.dtype
+
+    def _project(self, layer, x, start):
+        """RMSNorm, q/k/v projections and rotary embedding for tokens at
+        positions start .. start + len(x) - 1."""
+        cfg, n = self.config, len(x)
+        h = layer.input_layernorm(x)
+        attn = layer.self_attn
+        q = attn.q_proj(h).view(n, cfg.num_attention_heads, cfg.head_dim)
+        k = attn.k_proj(h).view(n, cfg.num_key_value_heads, cfg.head_dim)
+        v = attn.v_proj(h).view(n, cfg.num_key_value_heads, cfg.head_dim)
+        inv_freq = cfg.rope_theta ** (-torch.arange(0, cfg.head_dim, 2, device=x.device).float() / cfg.head_dim)
+        angle = torch.arange(start, start + n, device=x.device).float()[:, None] * inv_freq[None, :]
+        angle = torch.cat((angle, angle), -1)[:, None, :]
+        cos, sin = angle.cos().to(x.dtype), angle.sin().to(x.dtype)
+
+        def rope(t):
+            lo, hi = t.chunk(2, -1)
+            return t * cos + torch.cat((-hi, lo), -1) * sin
+
+        return rope(q), rope(k), v
+
+    @staticmethod
+    def _finish(layer, residual, attention):
+        x = residual + layer.self_attn.o_proj(attention.reshape(len(residual), -1))
+        return x + layer.mlp(layer.post_attention_layernorm(x))
+
+    @torch.inference_mode()
+    def prefill(self, tokens: list[int], cache=None, request_id=None):
+        """Dense causal forward over the prompt, writing K/V to the cache;
+        returns the last position's logits (fp32)."""
+        if not tokens:
+            raise ValueError("prompt cannot be empty")
+        if cache is not None and any(cache.storage.requests[request_id].lengths):
+            raise ValueError("prefill is allowed exactly once per request")
+        cfg = self.config
+        groups = cfg.num_attention_heads // cfg.num_key_value_heads
+        x = self.model.embed_tokens(torch.tensor(tokens, device=self.device))
+        for index, layer in enumerate(self.model.layers):
+            q, k, v = self._project(layer, x, 0)
+            if cache is not None:
+                cache.write(request_id, index, k, v)
+            attention = F.scaled_dot_product_attention(
+                q.transpose(0, 1),
+                k.repeat_interleave(groups, 1).transpose(0, 1),
+                v.repeat_interleave(groups, 1).transpose(0, 1),
+                is_causal=True,
+            ).transpose(0, 1)
+            x = self._finish(layer, x, attention)
+        return self.lm_head(self.model.norm(x[-1])).float()
+
+    @torch.inference_mode()
+    def decode(self, token: int, request_id, cache, top_k=None, backend="auto", selector="quest"):
+        """One decode step: per layer append K/V, select (Quest top_k pages,
+        or the page-mean selector, or everything for top_k=None) and attend
+        over the selected rows. Returns fp32 logits."""
+        lengths = cache.storage.requests[request_id].lengths
+        if len(set(lengths)) != 1 or lengths[0] == 0:
+            raise ValueError("all layers must have the same nonempty history")
+        position = lengths[0]
+        P = cache.config.page_size
+        x = self.model.embed_tokens(torch.tensor([token], device=self.device))
+        for index, layer in enumerate(self.model.layers):
+            q, k, v = self._project(layer, x, position)
+            cache.write(request_id, index, k, v)
+            request = cache.storage.requests[request_id]
+            if selector == "quest" and top_k is not None:
+                selection = quest_selection(
+                    q[0], request.minimum[index], request.maximum[index], request.lengths[index], P, top_k
+                )
+            elif selector in ("quest", "mean"):
+                pages = select_pages(cache, request_id, index, q[0], top_k)
+                selection = Selection.from_pages(pages, request.lengths[index], P, q.shape[1])
+            else:
+                raise ValueError("selector must be quest or mean")
+            attention = cache.attention(q[0], request_id, index, selection, backend)
+            x = self._finish(layer, x, attention.unsqueeze(0))
+        return self.lm_head(self.model.norm(x[0])).float()

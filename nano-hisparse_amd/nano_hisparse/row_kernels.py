@@ -26,8 +26,11 @@ def set_cpu_provider(provider):
     """Install (or clear, with None) the object that computes for CPU tensors.
 
     Only test harnesses use this, to run the host control plane without a GPU.
-    It must offer resolve_rows, gather_rows, attend_rows, quest_positions and
-    mean_positions with the signatures of the functions below.
+    It must offer resolve_rows(topk, source, resident, hot, tags, lru, length,
+    page_size) -> RowPlan, gather_rows(host, pool, plan, config),
+    attend_rows(query, pool, rows, config), quest_positions(query, minimum,
+    maximum, length, page_size, top_pages, keep_sink) -> position tensor and
+    mean_pages(query, summaries, length, page_size, top_pages) -> page list.
     """
     global _cpu_provider
     _cpu_provider = provider

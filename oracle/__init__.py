@@ -116,6 +116,8 @@ def attend_rows(query, pool, rows, page_size):
     rows = torch.as_tensor(rows, dtype=torch.int64)
     if rows.ndim == 2:
         rows = rows[:, None, :].expand(B, Hq, rows.shape[-1])
+    if tuple(rows.shape[:2]) != (B, Hq) or tuple(pool.shape[3:]) != (kv_heads, D) or Hq % kv_heads:
+        raise ValueError("oracle attend_rows: query, rows and pool shapes disagree")
     rows = rows.contiguous()
     out = torch.empty(B, Hq, D, dtype=torch.float32)
     query = query.contiguous()
