@@ -10,11 +10,19 @@ buffer, 8 missing (their rows come from pinned host memory). The hot buffer
 holds H = 4096 rows per request, fully occupied, in a random LRU order. Q/K/V
 are N(0,1) from a seeded generator.
 
-One step = Quest score + top-k (nhs_quest_select) -> row resolution
-(nhs_resolve_rows) -> host-row gather on a side stream (nhs_gather_rows)
--> attention (nhs_attend_rows). The resolver's tags/LRU are restored from a
-saved copy at the start of every step (a 0.8 MB device copy, inside the timed
-region) so every step has the same 25% misses. Prints one JSON line.
+One step = the layer's batched sparse decode (nano_hisparse.batch_step):
+per chunk of requests, Quest score + top-k (nhs_quest_select) and row
+resolution (nhs_resolve_rows) on the compute stream, the host-row gather on
+a side stream (nhs_gather_rows), then attention (nhs_attend_rows) once that
+chunk's gather event has fired; the next chunk's selection and resolution
+are enqueued before the previous chunk's attention, so both overlap the
+gather. The resolver's tags/LRU are restored from a saved copy at the start
+of every step (a 0.8 MB device copy, inside the timed region) so every step
+has the same 25% misses. Prints one JSON line.
+
+`--copy-calibration` instead runs a plain 256 MiB device-to-device copy three
+times: the known-size kernel that scales the FETCH_SIZE / WRITE_SIZE
+counters of a rocprofv3 --pmc run to bytes.
 """
 
 from __future__ import annotations
@@ -22,7 +30,6 @@ from __future__ import annotations
 import argparse
 import json
 import os
-import subprocess
 import sys
 import time
 
@@ -45,6 +52,8 @@ def parse_args():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--seed", type=int, default=42)
+    ap.add_argument("--chunks", type=int, default=1, help="request chunks pipelined against the gather")
+    ap.add_argument("--copy-calibration", action="store_true", help="run the PMC calibration copy and exit")
     return ap.parse_args()
 
 
@@ -57,6 +66,7 @@ class Workload:
         import torch
 
         from nano_hisparse import row_kernels as rk
+        from nano_hisparse.batch_step import BatchTables
 
         self.batch, self.context, self.device = batch, context, device
         B, Hq, Hkv, D, P = batch, self.q_heads, self.kv_heads, self.head_dim, self.page
@@ -131,56 +141,48 @@ class Workload:
         self.resident = resident.to(device)
         self.hot = hot.to(device)
         self.tags0, self.lru0 = tags.to(device), lru.to(device)
-        self.tags, self.lru = self.tags0.clone(), self.lru0.clone()
-        self.alias = rk.MappedHost(self.host)
+        self.tables = BatchTables(self.source, self.resident, self.hot, self.tags0.clone(), self.lru0.clone(),
+                                  mn, mx, self.lengths)
         self.out = torch.empty(B, Hq, D, dtype=dtype, device=device)
-        self.workspace = None
         self.row_bytes = 2 * Hkv * D * 2
         self.selected_pages = pages
 
-    # algorithmic bytes per launch (one decode step of one layer for the batch)
-    def attention_bytes(self, valid_rows):
-        return valid_rows * self.row_bytes + self.batch * (2 * self.q_heads * self.head_dim * 2 + 8 * self.K)
+    # algorithmic bytes of one attention launch over `requests` requests
+    def attention_bytes(self, valid_rows, requests):
+        return valid_rows * self.row_bytes + requests * (2 * self.q_heads * self.head_dim * 2 + 8 * self.K)
 
     def quest_bytes(self):
         return self.batch * (self.n_pages * self.kv_heads * self.head_dim * 2 * 2 + self.q_heads * self.head_dim * 2)
 
 
-def run_step(w, rk, compute, transfer, events=None):
-    """One sparse decode step; `events` (dict of name -> (start, end)) are
-    recorded on the stream each kernel runs on."""
+def run_step(w, step, events=None):
+    """One sparse decode step of the layer for the whole batch."""
+    w.tables.tags.copy_(w.tags0)
+    w.tables.lru.copy_(w.lru0)
+    return step.step(w.q, out=w.out, events=events)[1]
+
+
+def copy_calibration():
+    """A plain 256 MiB device copy, three times: reads and writes 256 MiB each."""
     import torch
 
-    def ev(name, stream, which):
-        if events is not None:
-            events[name][which].record(stream)
+    src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("copy calibration: 3 x 268435456-byte device copies", flush=True)
 
-    w.tags.copy_(w.tags0)
-    w.lru.copy_(w.lru0)
-    ev("quest", compute, 0)
-    _, positions, _ = rk.quest_batched(w.q, w.minimum, w.maximum, w.lengths, w.page, w.top_pages)
-    ev("quest", compute, 1)
-    ev("resolve", compute, 0)
-    physical, miss_host, miss_dev, counts = rk.resolve_batched(
-        positions, w.source, w.resident, w.hot, w.tags, w.lru, w.lengths, w.page
-    )
-    ev("resolve", compute, 1)
-    resolved = torch.cuda.Event()
-    resolved.record(compute)
-    transfer.wait_event(resolved)
-    with torch.cuda.stream(transfer):
-        ev("gather", transfer, 0)
-        rk.gather_plan(w.alias, w.pool, miss_host, miss_dev, w.page)
-        ev("gather", transfer, 1)
-    gathered = torch.cuda.Event()
-    gathered.record(transfer)
-    compute.wait_event(gathered)
-    miss_host.record_stream(transfer)
-    miss_dev.record_stream(transfer)
-    ev("attention", compute, 0)
-    rk.attend_batched(w.q, w.pool, physical, w.page, out=w.out, workspace=w.workspace)
-    ev("attention", compute, 1)
-    return physical, counts
+
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
 
 
 def cpu_baseline(w, steps):
@@ -220,6 +222,22 @@ def cpu_baseline(w, steps):
     return float(np.median(times)), physical
 
 
+def traffic_from_profile(kernel_tag):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE scaled by a plain copy of known
+    size), or None when no summary is present."""
+    path = os.path.join(ROOT, "profiles", "sparse_decode_b16_ctx32k_pmc_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                fields = line.split()
+                if len(fields) >= 3 and fields[0] == "traffic_bytes" and fields[1] == kernel_tag:
+                    return int(fields[2])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -229,45 +247,53 @@ def main():
             file=sys.stderr,
         )
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     import torch
 
     from nano_hisparse import _hip
-    from nano_hisparse import row_kernels as rk
+    from nano_hisparse.batch_step import SparseDecodeBatch, gather_results
 
     _hip.load()
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
     print(f"[bench] building workload batch={args.batch} context={args.context}", file=sys.stderr, flush=True)
     w = Workload(args.batch, args.context, args.seed, device)
-    w.workspace = torch.zeros(  # split-arrival counters start at zero; the kernel leaves them at zero
-        _hip.load().nhs_attend_workspace_bytes(w.batch, w.q_heads, w.head_dim, w.K), dtype=torch.uint8, device=device
-    )
-    compute = torch.cuda.current_stream(device)
-    transfer = torch.cuda.Stream(device=device)
+    step = SparseDecodeBatch(w.pool, w.host, w.tables, w.page, w.top_pages, chunks=args.chunks)
+    compute = step.compute
 
     names = ("quest", "resolve", "gather", "attention")
     for _ in range(args.warmup):
-        physical, counts = run_step(w, rk, compute, transfer)
+        results = run_step(w, step)
     torch.cuda.synchronize()
+    _, physical, counts = gather_results(results)
     counts_sum = counts.sum(0).tolist()
     valid_rows = int((physical >= 0).sum())
-    print(f"[bench] counts resident/hot/miss = {counts_sum}, valid rows {valid_rows}", file=sys.stderr, flush=True)
+    chunk_valid = [int((r.physical >= 0).sum()) for r in results]
+    chunk_requests = [r.requests.stop - r.requests.start for r in results]
+    print(f"[bench] counts resident/hot/miss = {counts_sum}, valid rows {valid_rows}, chunks {chunk_requests}",
+          file=sys.stderr, flush=True)
 
     # timed region: K steps, synchronized on both sides
-    per_step = [{n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for n in names}
-                for _ in range(args.steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    step_events = [step.timing_events() for _ in range(args.steps)]
+    timed = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record(compute)
     for i in range(args.steps):
-        run_step(w, rk, compute, transfer, per_step[i])
+        timed.append(run_step(w, step, step_events[i]))
     end.record(compute)
+    enqueue_s = time.perf_counter() - t0
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    total_ms = start.elapsed_time(end)
-    ms_per_step = total_ms / args.steps
-    kernel_us = {n: 1e3 * sum(e[n][0].elapsed_time(e[n][1]) for e in per_step) / args.steps for n in names}
+    ms_per_step = start.elapsed_time(end) / args.steps
+    # per kernel: summed over the chunks of a step, then averaged over steps
+    kernel_us = {n: 1e3 * sum(c.events[n][0].elapsed_time(c.events[n][1]) for r in timed for c in r) / args.steps
+                 for n in names}
+    launches = args.steps * len(results)
+    attn_launch_us = kernel_us["attention"] * args.steps / launches
 
     # measured pinned H2D copy ceiling (copy engine), for reference
     probe = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
@@ -284,9 +310,16 @@ def main():
         h2d.append(probe.numel() / (a.elapsed_time(b) * 1e-3))
     del probe, dst
 
-    attn_bytes = w.attention_bytes(valid_rows)
+    attn_bytes = sum(w.attention_bytes(v, r) for v, r in zip(chunk_valid, chunk_requests))
+    attn_launch_bytes = attn_bytes / len(results)
     gather_bytes = counts_sum[2] * w.row_bytes
+    quest_bytes = w.quest_bytes()
     tokens_per_s = w.batch / (ms_per_step * 1e-3)
+    # ideal step: every HBM byte at the HBM peak, or every host byte at the PCIe peak
+    ideal_us = 1e6 * max((attn_bytes + quest_bytes + gather_bytes) / HBM_PEAK, gather_bytes / PCIE_PEAK)
+    # the committed PMC summary covers the default workload only
+    default = (args.batch, args.context, args.seed, len(results)) == (16, 32768, 42, 1)
+    traffic = traffic_from_profile("attend_kernel") if default else None
     result = {
         "metric": METRIC,
         "value": round(tokens_per_s, 1),
@@ -306,19 +339,21 @@ def main():
             "selected pages 50% resident / 25% hot / 25% host misses, hot rows 4096 per request",
             "batch": w.batch,
             "context": w.context,
+            "chunks": len(results),
             "parallelism": "single GPU",
         },
         "step_us": round(ms_per_step * 1e3, 2),
         "kernel_us": {n: round(v, 2) for n, v in kernel_us.items()},
         "roofline": {
-            "kernel": "nhs_attend_rows (attend_split_kernel + attend_combine_kernel)",
+            "kernel": "nhs_attend_rows (attend_kernel)",
             "bound": "hbm",
-            "achieved": round(attn_bytes / (kernel_us["attention"] * 1e-6) / 1e9, 1),
+            "achieved": round(attn_launch_bytes / (attn_launch_us * 1e-6) / 1e9, 1),
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
-            "frac": round(attn_bytes / (kernel_us["attention"] * 1e-6) / HBM_PEAK, 4),
-            "traffic": None,
-            "algorithmic_bytes": attn_bytes,
+            "frac": round(attn_launch_bytes / (attn_launch_us * 1e-6) / HBM_PEAK, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": round(attn_launch_bytes),
+            "launch_us": round(attn_launch_us, 2),
         },
         "gather_roofline": {
             "kernel": "nhs_gather_rows (gather_rows_kernel)",
@@ -330,8 +365,10 @@ def main():
             "measured_h2d_copy_gbs": round(max(h2d) / 1e9, 2),
             "algorithmic_bytes": gather_bytes,
         },
-        "quest_gbs": round(w.quest_bytes() / (kernel_us["quest"] * 1e-6) / 1e9, 1),
+        "step_roofline": {"ideal_us": round(ideal_us, 1), "frac": round(ideal_us / (ms_per_step * 1e3), 4)},
+        "quest_gbs": round(quest_bytes / (kernel_us["quest"] * 1e-6) / 1e9, 1),
         "wall_s_timed": round(wall, 3),
+        "host_enqueue_us_per_step": round(enqueue_s * 1e6 / args.steps, 1),
     }
     if args.cpu_steps > 0:
         print(f"[bench] CPU oracle baseline, {args.cpu_steps} steps", file=sys.stderr, flush=True)
@@ -344,13 +381,8 @@ def main():
             "cores": 1,
             "kind": "port",
             "sample": f"{args.cpu_steps} full steps of the same workload (median step {cpu_s:.3f} s)",
+            "host": f"{cpu_model_name()} ({os.cpu_count()} CPUs visible)",
         }
-        try:
-            model = subprocess.run(["bash", "-c", "lscpu | grep 'Model name' | head -1"], capture_output=True,
-                                   text=True).stdout.split(":")[-1].strip()
-        except OSError:
-            model = ""
-        result["cpu_baseline"]["host"] = f"{model} ({os.cpu_count()} CPUs visible)"
     print(json.dumps(result), flush=True)
 
 

@@ -48,6 +48,18 @@ int nhs_abi_version(void);
 const char* nhs_last_error(void);
 
 /*
+ * Per-kernel timing hook: the next nhs_* entry point called on this thread
+ * stamps `start_event` with the begin of its first kernel and `stop_event`
+ * with the end of its last kernel (either may be NULL), taken from the
+ * dispatches themselves through hipExtLaunchKernel, then forgets both.
+ * The events must be created timing hipEvent_t of the launch's device.
+ * No counterpart in the reference, which times its Triton launches with
+ * torch.cuda.Event pairs; marker packets around a kernel add several us of
+ * queue latency that a dispatch's own timestamps do not have.
+ */
+int nhs_set_launch_events(void* start_event, void* stop_event);
+
+/*
  * Device alias of pinned host memory allocated by hipHostMalloc (torch's
  * pin_memory=True). The library never registers or unregisters memory.
  * Replaces MappedHost, nano_hisparse/row_kernels.py:10-32 (a libcuda

@@ -538,6 +538,7 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
                                int64_t out_batch_stride, int64_t out_head_stride, void* workspace,
                                int64_t workspace_bytes, void* stream) {
   using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
   if (!query || !pool || !rows || !out || !workspace) return fail(NHS_ERR_INVALID, "nhs_attend_rows: null pointer");
   if (!valid_dtype(q_dtype) || !valid_dtype(kv_dtype)) return fail(NHS_ERR_INVALID, "nhs_attend_rows: bad dtype");
   if (batch < 1 || n_rows < 1 || q_heads < 1 || kv_heads < 1 || head_dim < 1 || page_size < 1 ||
@@ -609,6 +610,6 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
   a.out_bs = out_batch_stride;
   a.out_hs = out_head_stride;
   dim3 grid((unsigned)splits, (unsigned)groups, (unsigned)batch);
-  hipLaunchKernelGGL(kernel, grid, dim3(kAttendThreads), lds, (hipStream_t)stream, a);
+  launch(kernel, grid, dim3(kAttendThreads), lds, (hipStream_t)stream, ev.start, ev.stop, a);
   return launch_status("nhs_attend_rows");
 }

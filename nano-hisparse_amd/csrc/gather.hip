@@ -76,6 +76,7 @@ extern "C" int nhs_gather_rows(const void* host_alias, void* pool, const int64_t
                                const int64_t* miss_device_rows, int64_t n_entries, int32_t page_size,
                                int64_t plane_bytes, void* stream) {
   using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
   if (!host_alias || !pool || !miss_host_rows || !miss_device_rows)
     return fail(NHS_ERR_INVALID, "nhs_gather_rows: null pointer");
   if (n_entries < 0 || page_size < 1 || plane_bytes < 4 || plane_bytes % 4)
@@ -87,18 +88,15 @@ extern "C" int nhs_gather_rows(const void* host_alias, void* pool, const int64_t
   if (blocks > 0x7fffffff) return fail(NHS_ERR_UNSUPPORTED, "nhs_gather_rows: too many plan entries");
   hipStream_t s = (hipStream_t)stream;
   if (plane_bytes % 16 == 0 && align % 16 == 0) {
-    hipLaunchKernelGGL(gather_rows_kernel<uint4>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s,
-                       (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size,
-                       plane_bytes);
+    launch(gather_rows_kernel<uint4>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s, ev.start, ev.stop,
+           (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes);
   } else if (plane_bytes % 8 == 0 && align % 8 == 0) {
-    hipLaunchKernelGGL(gather_rows_kernel<uint2>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s,
-                       (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size,
-                       plane_bytes);
+    launch(gather_rows_kernel<uint2>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s, ev.start, ev.stop,
+           (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes);
   } else {
     if (align % 4) return fail(NHS_ERR_INVALID, "nhs_gather_rows: host and pool must be 4-byte aligned");
-    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s,
-                       (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size,
-                       plane_bytes);
+    launch(gather_rows_kernel<uint32_t>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s, ev.start, ev.stop,
+           (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes);
   }
   return launch_status("nhs_gather_rows");
 }

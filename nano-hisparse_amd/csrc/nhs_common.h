@@ -2,6 +2,7 @@
 // conversion, wave64 cross-lane sums and block-wide scans.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -13,6 +14,25 @@ namespace nhs {
 int fail(int code, const char* fmt, ...);
 // Converts the launch status of the kernels just enqueued into an nhs status.
 int launch_status(const char* what);
+
+// Timing events set by nhs_set_launch_events for the next entry point called
+// on this thread; take_launch_events() returns and clears them.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents take_launch_events();
+
+// Enqueues `kernel`. With a start and/or stop event the launch goes through
+// hipExtLaunchKernel, which stamps the events with the dispatch's own begin
+// and end times (no marker packets between them and the kernel).
+template <typename K, typename... Args>
+inline void launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, hipEvent_t start,
+                   hipEvent_t stop, Args... args) {
+  if (start || stop)
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, start, stop, 0u, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+}
 
 constexpr int kWave = 64;
 

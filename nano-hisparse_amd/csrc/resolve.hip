@@ -403,6 +403,7 @@ extern "C" int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions,
                                 int64_t* physical, int64_t* miss_host, int64_t* miss_device, int64_t plan_stride,
                                 int64_t* counts, int64_t* counts_total, void* stream) {
   using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
   if (!positions || !source || !resident || !hot || !tags || !lru || !physical || !miss_host || !miss_device ||
       !counts)
     return fail(NHS_ERR_INVALID, "nhs_resolve_rows: null pointer");
@@ -439,6 +440,7 @@ extern "C" int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions,
   a.plan_stride = plan_stride;
   a.counts = counts;
   a.counts_total = counts_total;
-  hipLaunchKernelGGL(resolve_rows_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0, (hipStream_t)stream, a);
+  launch(resolve_rows_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0, (hipStream_t)stream, ev.start, ev.stop,
+         a);
   return launch_status("nhs_resolve_rows");
 }

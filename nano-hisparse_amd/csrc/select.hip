@@ -362,8 +362,9 @@ static int chunk_elems(int head_dim, int esize) {
   return 0;
 }
 
-static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, const char* who) {
-  hipLaunchKernelGGL(select_topk_kernel, dim3((unsigned)batch), dim3(kSelectThreads), 0, stream, s);
+static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, const char* who, hipEvent_t start,
+                         hipEvent_t stop) {
+  launch(select_topk_kernel, dim3((unsigned)batch), dim3(kSelectThreads), 0, stream, start, stop, s);
   return launch_status(who);
 }
 
@@ -376,6 +377,7 @@ extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtyp
                                 int32_t max_pages, int32_t top_pages, int32_t keep_sink, float* scores,
                                 int32_t* pages, int32_t* positions, void* stream) {
   using namespace nhs;
+  LaunchEvents ev = take_launch_events();
   const char* who = "nhs_quest_select";
   int st = check_select_common(who, batch, query, q_dtype, q_heads, kv_heads, head_dim, lengths, length, page_size,
                                max_pages, top_pages, scores, pages, positions);
@@ -437,7 +439,8 @@ extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtyp
 #undef NHS_QUEST_CASE
     }
     if (!kernel) return fail(NHS_ERR_UNSUPPORTED, "%s: no scoring kernel", who);
-    hipLaunchKernelGGL(kernel, grid, dim3(threads), lds, s, a);
+    launch(kernel, grid, dim3(threads), lds, s, ev.start, nullptr, a);
+    ev.start = nullptr;  // the start event belongs to the first kernel
     st = launch_status(who);
     if (st != NHS_OK) return st;
   }
@@ -453,7 +456,7 @@ extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtyp
   sa.page_div = FastDiv((uint32_t)page_size);
   sa.pages = pages;
   sa.positions = positions;
-  return launch_select(sa, batch, s, who);
+  return launch_select(sa, batch, s, who, ev.start, ev.stop);
 }
 
 extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
@@ -462,6 +465,7 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
                                int64_t length, int32_t page_size, int32_t max_pages, int32_t top_pages, float* scores,
                                int32_t* pages, int32_t* positions, void* stream) {
   using namespace nhs;
+  LaunchEvents ev = take_launch_events();
   const char* who = "nhs_mean_select";
   int st = check_select_common(who, batch, query, q_dtype, q_heads, kv_heads, head_dim, lengths, length, page_size,
                                max_pages, top_pages, scores, pages, positions);
@@ -496,9 +500,10 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
   size_t lds = ((size_t)kv_heads * head_dim + (size_t)kScoreWaves * kv_heads) * sizeof(float);
   if (top_pages < max_pages) {
     if (E == 4)
-      hipLaunchKernelGGL((mean_score_kernel<4>), grid, dim3(kScoreThreads), lds, s, a);
+      launch(mean_score_kernel<4>, grid, dim3(kScoreThreads), lds, s, ev.start, nullptr, a);
     else
-      hipLaunchKernelGGL((mean_score_kernel<1>), grid, dim3(kScoreThreads), lds, s, a);
+      launch(mean_score_kernel<1>, grid, dim3(kScoreThreads), lds, s, ev.start, nullptr, a);
+    ev.start = nullptr;
     st = launch_status(who);
     if (st != NHS_OK) return st;
   }
@@ -514,5 +519,5 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
   sa.page_div = FastDiv((uint32_t)page_size);
   sa.pages = pages;
   sa.positions = positions;
-  return launch_select(sa, batch, s, who);
+  return launch_select(sa, batch, s, who, ev.start, ev.stop);
 }

@@ -70,6 +70,25 @@ def _require_gpu(what, *tensors):
     return device
 
 
+def timing_events():
+    """A (start, stop) pair of timing events usable with set_launch_events."""
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()  # creates the underlying hipEvent_t now
+    stop.record()
+    return start, stop
+
+
+def set_launch_events(start, stop):
+    """The next launcher called on this thread stamps `start` with the begin
+    of its first kernel and `stop` with the end of its last kernel (events
+    from timing_events(); either may be None)."""
+    lib = _hip.load()
+    lib.nhs_set_launch_events(
+        ctypes.c_void_p(start.cuda_event if start is not None else 0),
+        ctypes.c_void_p(stop.cuda_event if stop is not None else 0),
+    )
+
+
 class MappedHost:
     """Device alias of pinned host memory that torch allocated.
 

@@ -193,3 +193,27 @@ def test_gather_closed_form_matches_fancy_indexing():
     for h, d in ((3, 0), (44, 19), (17, 7)):
         expected[d // P, :, d % P] = host[h // P, :, h % P]
     assert torch.equal(pool, expected)
+
+
+# ---- bounds producer -------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_append_bounds_are_exact_min_max_and_rounded_mean(dtype):
+    """storage.py:302-309: the page summary is the fp32 mean of the valid
+    keys; minimum/maximum fold the new keys into the old bounds exactly."""
+    g = torch.Generator().manual_seed(12)
+    P, Hkv, D = 16, 2, 8
+    keys = torch.randn(P, Hkv, D, generator=g).to(dtype)
+    summary = torch.zeros(Hkv, D)
+    lo = torch.full((Hkv, D), float("inf"))
+    hi = torch.full((Hkv, D), float("-inf"))
+    valid = 0
+    for count in (5, 1, 7):  # appends of 5, 1 and 7 tokens into one page
+        oracle.append_bounds(keys, valid, count, summary, lo, hi)
+        valid += count
+        seen = keys[:valid].double()
+        assert torch.equal(lo, keys[:valid].float().amin(0))
+        assert torch.equal(hi, keys[:valid].float().amax(0))
+        mean = seen.mean(0)
+        assert torch.allclose(summary.double(), mean, rtol=2 ** -23, atol=1e-12)
