@@ -11,14 +11,15 @@ holds H = 4096 rows per request, fully occupied, in a random LRU order. Q/K/V
 are N(0,1) from a seeded generator.
 
 One step = the layer's batched sparse decode (nano_hisparse.batch_step):
-per chunk of requests, Quest score + top-k (nhs_quest_select) and row
-resolution (nhs_resolve_rows) on the compute stream, the host-row gather on
-a side stream (nhs_gather_rows), then attention (nhs_attend_rows) once that
-chunk's gather event has fired; the next chunk's selection and resolution
-are enqueued before the previous chunk's attention, so both overlap the
-gather. The resolver's tags/LRU are restored from a saved copy at the start
-of every step (a 0.8 MB device copy, inside the timed region) so every step
-has the same 25% misses. Prints one JSON line.
+Quest score + top-k (nhs_quest_select), row resolution (nhs_resolve_rows),
+the host-row gather (nhs_gather_rows) and attention (nhs_attend_rows). With
+the default single chunk all four run in order on one stream; --side-stream
+puts the gather on a second stream ordered by HIP events, and --chunks n
+pipelines n groups of requests (selection and resolution of the next group
+and attention of the previous one are enqueued around each gather). The
+resolver's tags/LRU are restored from a saved copy at the start of every
+step (a 0.8 MB device copy, inside the timed region) so every step has the
+same 25% misses. Prints one JSON line.
 
 `--copy-calibration` instead runs a plain 256 MiB device-to-device copy three
 times: the known-size kernel that scales the FETCH_SIZE / WRITE_SIZE
@@ -53,6 +54,8 @@ def parse_args():
     ap.add_argument("--context", type=int, default=32768)
     ap.add_argument("--seed", type=int, default=42)
     ap.add_argument("--chunks", type=int, default=1, help="request chunks pipelined against the gather")
+    ap.add_argument("--side-stream", action="store_true",
+                    help="run the gather on a side stream ordered by events (the default with --chunks > 1)")
     ap.add_argument("--copy-calibration", action="store_true", help="run the PMC calibration copy and exit")
     return ap.parse_args()
 
@@ -260,7 +263,9 @@ def main():
     torch.cuda.set_device(device)
     print(f"[bench] building workload batch={args.batch} context={args.context}", file=sys.stderr, flush=True)
     w = Workload(args.batch, args.context, args.seed, device)
-    step = SparseDecodeBatch(w.pool, w.host, w.tables, w.page, w.top_pages, chunks=args.chunks)
+    compute = torch.cuda.current_stream(device)
+    step = SparseDecodeBatch(w.pool, w.host, w.tables, w.page, w.top_pages, chunks=args.chunks, compute=compute,
+                             transfer=torch.cuda.Stream(device=device) if args.side_stream else None)
     compute = step.compute
 
     names = ("quest", "resolve", "gather", "attention")
@@ -340,6 +345,7 @@ def main():
             "batch": w.batch,
             "context": w.context,
             "chunks": len(results),
+            "gather_stream": "side" if step.transfer is not step.compute else "compute",
             "parallelism": "single GPU",
         },
         "step_us": round(ms_per_step * 1e3, 2),

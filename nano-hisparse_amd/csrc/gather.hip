@@ -14,7 +14,7 @@
 namespace nhs {
 
 constexpr int kGatherThreads = 256;
-constexpr int kRowsPerBlock = 8;
+constexpr int kRowsPerBlock = 16;  // 16 reads in flight per lane reach the copy engine's PCIe rate
 
 template <typename V>
 __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char* __restrict__ host,

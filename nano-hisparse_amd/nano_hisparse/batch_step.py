@@ -17,7 +17,10 @@ streams host rows over PCIe slow down 2-7x, even on CUs the gather does not
 use (a CU-masked transfer stream of 16 CUs still saturates the link), so the
 overlap costs more than it hides at the Llama-3-8B decode shape: 778 us per
 step unchunked against 805-2073 us with 2-8 chunks. The chunked schedule
-stays for shapes with little gather traffic per chunk.
+stays for shapes with little gather traffic per chunk. With one chunk there
+is nothing to overlap, and each event hop between two queues costs ~10 us,
+so the gather then runs on the compute stream unless a transfer stream is
+passed (740 us against 760 us per step).
 """
 
 from __future__ import annotations
@@ -68,7 +71,9 @@ class SparseDecodeBatch:
     pipelined groups of requests.
 
     pool: the device KV pool [blocks, 2, P, Hkv, D]; host: the pinned host
-    store of the same page shape. Tensors live on one GPU.
+    store of the same page shape. Tensors live on one GPU. transfer: the
+    stream of the gathers (default: the compute stream for one chunk, a new
+    side stream for several).
     """
 
     def __init__(self, pool, host, tables: BatchTables, page_size, top_pages, keep_sink=True, chunks=1,
@@ -82,10 +87,12 @@ class SparseDecodeBatch:
         self.alias = rk.MappedHost(host)
         device = pool.device
         self.compute = compute or torch.cuda.current_stream(device)
-        self.transfer = transfer or torch.cuda.Stream(device=device)
         B = tables.batch
         bounds = [round(i * B / chunks) for i in range(chunks + 1)]
         self.slices = [slice(a, b) for a, b in zip(bounds, bounds[1:]) if b > a]
+        if transfer is None:
+            transfer = self.compute if len(self.slices) == 1 else torch.cuda.Stream(device=device)
+        self.transfer = transfer
         self._workspace = None
 
     def _attend(self, query, physical, out):
