@@ -11,10 +11,14 @@
 // chunk serves all G query heads, so the pool is read once per KV head.
 // Scores are reduced across a row's lanes with DPP; an online softmax in
 // base 2 (scale * log2 e applied after the dot) accumulates (m, l, acc) per
-// row slot; slots are merged by shuffles, waves through LDS, and the
-// workgroup writes (m, l, acc) of its split to the workspace.
+// row slot; slots are merged by shuffles and waves through LDS.
 //
-// The last workgroup of a head group to finish (an arrival counter in the
+// The grid is one balanced round of about one workgroup per CU. A (request,
+// KV head) that gets two CUs is split by query heads (two workgroups of G
+// heads read the same rows on one XCD, the second read mostly from L2) and
+// its workgroups store the normalised output directly; beyond that the row
+// list is split, each split writes (m, l, acc) to the workspace, and the
+// last workgroup of a head group to finish (an arrival counter in the
 // workspace, reset to zero by that workgroup) merges the splits, divides by
 // the softmax denominator (0 when no row was valid) and stores the output in
 // the query's dtype. The workspace's first 260 KiB (arrival counters and a
@@ -32,7 +36,10 @@ constexpr int kAttendThreads = 512;
 constexpr int kAttendWaves = kAttendThreads / kWave;
 constexpr int kMaxSplits = 32;
 constexpr int kMinRowsPerSplit = 32;
-constexpr int kStage = 1024;  // row indices staged in LDS per pass
+constexpr int kStage = 4096;  // row indices staged in LDS per pass (16 KiB)
+constexpr int kStagePerThread = kStage / kAttendThreads;
+constexpr int kIssueGroups = 2;  // row groups whose loads a wave issues together
+constexpr int kMaxHeadChunks = 2;  // query-head chunks that re-read one KV head's rows
 // Arrival counters occupy a fixed region at the front of the workspace, so a
 // call never finds another call's partials where it expects a counter.
 constexpr int kCounterSlots = 65536;
@@ -55,11 +62,12 @@ struct AttendArgs {
   int n_rows, rows_per_split, n_splits;
   int q_heads, kv_heads, group, head_dim, page_size;
   int lpr_log2, lanes_used, chunks_per_kv;
+  int kv_items;  // batch * kv_heads
   FastDiv page_div;
   float qscale;
   const char* zeros;  // kZeroBytes of zeros
   float* ws;          // partials [B, q_heads, n_splits, 2 + head_dim]
-  int* counters;      // [B, gridDim.y]
+  int* counters;      // [B, kv_heads * chunks_per_kv]
   void* out;
   int out_dtype;
   int64_t out_bs, out_hs;
@@ -133,10 +141,18 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
   const int sub = lane & (lpr - 1);
   const bool data_lane = sub < a.lanes_used;
 
-  const int split = blockIdx.x;
-  const int kv = blockIdx.y / a.chunks_per_kv;
-  const int chunk = blockIdx.y - kv * a.chunks_per_kv;
-  const int b = blockIdx.z;
+  // 1-D grid, id = kv_item + kv_items * (chunk * n_splits + split): the
+  // workgroups of one (request, KV head) are kv_items apart, so they land on
+  // the same XCD (workgroups go to the 8 XCDs round robin) whenever kv_items
+  // is a multiple of 8, and the head chunks that read the same rows share
+  // that XCD's L2.
+  const int kv_item = (int)(blockIdx.x % (unsigned)a.kv_items);
+  const int rest = (int)(blockIdx.x / (unsigned)a.kv_items);
+  const int split = rest % a.n_splits;
+  const int chunk = rest / a.n_splits;
+  const int b = kv_item / a.kv_heads;
+  const int kv = kv_item - b * a.kv_heads;
+  const int head_group = kv * a.chunks_per_kv + chunk;
   const int h0 = kv * a.group + chunk * G;
   const int nh = min(G, a.group - chunk * G);
   const int64_t* rows = a.rows + (int64_t)b * a.r_bs + (int64_t)h0 * a.r_hs;
@@ -177,42 +193,66 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
   const int64_t row_bytes = (int64_t)a.kv_heads * a.head_dim * T::bytes;  // one plane row, all KV heads
   const int64_t plane_bytes = (int64_t)a.page_size * row_bytes;
   const char* pool = static_cast<const char*>(a.pool) + (int64_t)kv * a.head_dim * T::bytes;
-  const int per_iter = kAttendWaves * slots * U;
+  const int per_iter = kAttendWaves * slots * U;  // rows of one group (all waves)
 
   // The split's rows are staged in LDS as K-plane row indices of the pool
   // (block * 2P + offset; 0xffffffff for masked rows), kStage at a time, so
   // the loop below issues its K/V loads back to back without waiting on
   // index loads. Pool rows are < 2^31, checked on the host.
-  __shared__ uint32_t krow[kStage];
+  __shared__ __attribute__((aligned(16))) uint32_t krow[kStage];
+  __shared__ int progress[kAttendWaves];  // passes each wave has issued
   for (int s0 = row_begin; s0 < row_end; s0 += kStage) {
     const int s1 = min(row_end, s0 + kStage);
-    __syncthreads();
-    for (int i = s0 + (int)threadIdx.x; i < s1; i += kAttendThreads) {
-      const int64_t r = rows[(int64_t)i * a.r_cs];
-      uint32_t kr_idx = 0xffffffffu;
-      if (r >= 0) {
-        const uint32_t blk = a.page_div.div((uint32_t)r);
-        kr_idx = blk * (uint32_t)a.page_size + (uint32_t)r;  // blk*2P + (r - blk*P)
-      }
-      krow[i - s0] = kr_idx;
+    // every index load of the stage is issued before the first is used
+    int64_t rv[kStagePerThread];
+#pragma unroll
+    for (int j = 0; j < kStagePerThread; ++j) {
+      const int i = s0 + j * kAttendThreads + (int)threadIdx.x;
+      rv[j] = i < s1 ? rows[(int64_t)i * a.r_cs] : -1;
     }
+#pragma unroll
+    for (int j = 0; j < kStagePerThread; ++j) {
+      const int i = s0 + j * kAttendThreads + (int)threadIdx.x;
+      uint32_t kr_idx = 0xffffffffu;
+      if (rv[j] >= 0) {
+        const uint32_t blk = a.page_div.div((uint32_t)rv[j]);
+        kr_idx = blk * (uint32_t)a.page_size + (uint32_t)rv[j];  // blk*2P + (r - blk*P)
+      }
+      if (i < s1) krow[i - s0] = kr_idx;
+    }
+    if (threadIdx.x < kAttendWaves) progress[threadIdx.x] = 0;
     __syncthreads();
-    // Software pipeline: the K/V chunks of the next iteration are requested
-    // before the current one is consumed, so every wave keeps two iterations
-    // of loads in flight.
-    uint4 kr[U][C], vr[U][C], kn[U][C], vn[U][C];
-    bool ok[U], okn[U];
+    // Each pass issues the loads of kIssueGroups row groups back to back and
+    // then consumes the groups in order, so a wave keeps up to
+    // kIssueGroups * U rows per lane in flight. No loaded register is carried
+    // across passes: a carried prefetch makes the compiler copy registers at
+    // the loop edge, and the copy waits for every outstanding load.
     // Loads are unconditional: masked rows, padding lanes and rows past the
     // end read the workspace's zero block instead, so no branch separates a
-    // load from its use and the compiler can keep the prefetch in flight.
+    // load from its use.
+    // A lane's U rows are consecutive entries of the staged list, read from
+    // LDS with one vector read.
     auto issue = [&](int base, uint4 (&kd)[U][C], uint4 (&vd)[U][C], bool (&okd)[U]) {
+      const int first = base + (wave * slots + slot) * U;
+      // the read address is clamped into the array (U-aligned); entries at or
+      // past s1 are masked by position, so the read needs no branch
+      const int at = min(first - s0, kStage - U);
+      uint32_t w[U];
+      if constexpr (U == 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(&krow[at]);
+        w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2*>(&krow[at]);
+        w[0] = v.x, w[1] = v.y;
+      }
+      uint32_t ki[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) ki[u] = first + u < s1 ? w[u] : 0xffffffffu;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int c_idx = base + (u * kAttendWaves + wave) * slots + slot;
-        const uint32_t ki = c_idx < s1 ? krow[c_idx - s0] : 0xffffffffu;
-        okd[u] = ki != 0xffffffffu;
+        okd[u] = ki[u] != 0xffffffffu;
         const bool live = okd[u] && data_lane;
-        const char* kp = live ? pool + (int64_t)ki * row_bytes : a.zeros;
+        const char* kp = live ? pool + (int64_t)ki[u] * row_bytes : a.zeros;
         const int64_t vo = live ? plane_bytes : 0;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
@@ -222,9 +262,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
         }
       }
     };
-    issue(s0, kr, vr, ok);
-    for (int base = s0; base < s1; base += per_iter) {
-      issue(base + per_iter, kn, vn, okn);  // past the end: zero-block reads
+    auto consume = [&](const uint4 (&kr)[U][C], const uint4 (&vr)[U][C], const bool (&ok)[U]) {
       float p[G][U], alpha[G];
 #pragma unroll
       for (int g = 0; g < G; ++g)
@@ -358,16 +396,35 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
             }
           }
       }
+    };
+    // The waves of a workgroup share every pass (a static split of the rows,
+    // so the summation order and the result do not depend on timing). Waves
+    // that win issue arbitration would run microseconds ahead of the others
+    // and leave the CU with too few loads in flight at the end, so each wave
+    // publishes its pass count in LDS and sets its issue priority by its lag
+    // behind the slowest wave (3 when level, 1 one pass ahead, 0 beyond).
+    int pass = 0;
+    for (int base = s0; base < s1; base += kIssueGroups * per_iter, ++pass) {
+      uint4 kk[kIssueGroups][U][C], vv[kIssueGroups][U][C];
+      bool okk[kIssueGroups][U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        ok[u] = okn[u];
+      for (int gi = 0; gi < kIssueGroups; ++gi) issue(base + gi * per_iter, kk[gi], vv[gi], okk[gi]);
+      if (lane == 0) progress[wave] = pass;
+      int slowest = pass;
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
-          kr[u][c] = kn[u][c];
-          vr[u][c] = vn[u][c];
-        }
-      }
+      for (int w = 0; w < kAttendWaves; ++w) slowest = min(slowest, progress[w]);
+      if (pass > slowest + 1)
+        __builtin_amdgcn_s_setprio(0);
+      else if (pass > slowest)
+        __builtin_amdgcn_s_setprio(1);
+      else
+        __builtin_amdgcn_s_setprio(3);
+#pragma unroll
+      for (int gi = 0; gi < kIssueGroups; ++gi)
+        if (base + gi * per_iter < s1) consume(kk[gi], vv[gi], okk[gi]);
     }
+    __builtin_amdgcn_s_setprio(0);
+    if (s1 < row_end) __syncthreads();  // the next stage rewrites krow
   }
 
   // merge the row slots of this wave (lanes that differ in the slot bits)
@@ -411,6 +468,27 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
     }
   }
   __syncthreads();
+  if (a.n_splits == 1) {  // the workgroup saw every row: normalise and store
+    for (int idx = threadIdx.x; idx < nh * a.head_dim; idx += kAttendThreads) {
+      const int g = idx / a.head_dim;
+      const int d = idx - g * a.head_dim;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kAttendWaves; ++w) M = fmaxf(M, lds[(w * G + g) * stride]);
+      float L = 0.f, v = 0.f;
+      if (M != -INFINITY)
+#pragma unroll
+        for (int w = 0; w < kAttendWaves; ++w) {
+          const float* src = lds + (w * G + g) * stride;
+          const float f = exp2f(src[0] - M);
+          L += src[1] * f;
+          v += src[2 + d] * f;
+        }
+      v = L > 0.f ? v / L : 0.f;
+      store_elem(a.out, a.out_dtype, (int64_t)b * a.out_bs + (int64_t)(h0 + g) * a.out_hs + d, v);
+    }
+    return;
+  }
   float* part = a.ws + (((int64_t)b * a.q_heads + h0) * a.n_splits + split) * stride;
   for (int idx = threadIdx.x; idx < nh * stride; idx += kAttendThreads) {
     const int g = idx / stride;
@@ -439,7 +517,7 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
   // agent-scope fence would write back and invalidate this XCD's whole L2).
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  int* counter = a.counters + (int64_t)b * gridDim.y + blockIdx.y;
+  int* counter = a.counters + (int64_t)b * a.kv_heads * a.chunks_per_kv + head_group;
   if (threadIdx.x == 0)
     last_arrival = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.n_splits - 1;
   __syncthreads();
@@ -580,26 +658,34 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
   a.lpr_log2 = ilog2(a.lanes_used);
   a.qscale = (float)(1.4426950408889634 / sqrt((double)head_dim));
   a.group = q_heads / kv_heads;
+  // Grid: one balanced round, about one 8-wave workgroup per CU. A (request,
+  // KV head) whose share is several CUs is first divided by query heads
+  // (chunks of G heads that each read every row: the repeated reads hit the
+  // XCD's L2, and no split merge is needed), then by row splits (merged by
+  // the last workgroup to finish).
+  const int cus = device_cus();
+  const int kv_items = batch * kv_heads;
+  const int share = cus > 0 ? (cus + kv_items / 2) / kv_items : 1;  // workgroups per (request, KV head)
   int G;
   if (rows_head_stride != 0) {
     G = 1;  // one head per workgroup; its own row list
     a.chunks_per_kv = a.group;
   } else {
-    const int group = a.group;
-    G = group >= 8 ? 8 : group >= 4 ? (group == 4 ? 4 : 8) : group == 3 ? 4 : group;
-    a.chunks_per_kv = (group + G - 1) / G;
+    int chunks = 1;
+    while (chunks * 2 <= share && chunks * 2 <= a.group && chunks * 2 <= kMaxHeadChunks) chunks *= 2;
+    const int per_chunk = (a.group + chunks - 1) / chunks;
+    G = per_chunk <= 1 ? 1 : per_chunk <= 2 ? 2 : per_chunk <= 4 ? 4 : 8;
+    a.chunks_per_kv = (a.group + G - 1) / G;
   }
   AttendKernel kernel = pick_kernel(kv_dtype, packed, G, C);
   if (!kernel) return fail(NHS_ERR_UNSUPPORTED, "nhs_attend_rows: no kernel for G=%d C=%d", G, C);
   const size_t lds = (size_t)kAttendWaves * G * (2 + head_dim) * sizeof(float);
-  const int groups = kv_heads * a.chunks_per_kv;
-  const int items = batch * groups;
-  // One balanced round: about one 8-wave workgroup per CU. (Partial rounds
-  // leave some CUs with twice the work; extra workgroups add merges.)
-  const int cus = device_cus();
-  int splits = cus > 0 ? (cus + items / 2) / items : 1;
+  const int units = kv_items * a.chunks_per_kv;
+  int splits = cus > 0 ? (cus + units / 2) / units : 1;
   if (splits < 1) splits = 1;
   if (splits > max_splits_for(n_rows)) splits = max_splits_for(n_rows);
+  if ((int64_t)units * splits > 0x7fffffff) return fail(NHS_ERR_UNSUPPORTED, "nhs_attend_rows: grid too large");
+  a.kv_items = kv_items;
   a.n_splits = splits;
   a.rows_per_split = (n_rows + splits - 1) / splits;
   a.counters = static_cast<int*>(workspace);
@@ -609,7 +695,7 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
   a.out_dtype = q_dtype;
   a.out_bs = out_batch_stride;
   a.out_hs = out_head_stride;
-  dim3 grid((unsigned)splits, (unsigned)groups, (unsigned)batch);
-  launch(kernel, grid, dim3(kAttendThreads), lds, (hipStream_t)stream, ev.start, ev.stop, a);
+  launch(kernel, dim3((unsigned)(units * splits)), dim3(kAttendThreads), lds, (hipStream_t)stream, ev.start, ev.stop,
+         a);
   return launch_status("nhs_attend_rows");
 }
