@@ -11,15 +11,16 @@ holds H = 4096 rows per request, fully occupied, in a random LRU order. Q/K/V
 are N(0,1) from a seeded generator.
 
 One step = the layer's batched sparse decode (nano_hisparse.batch_step):
-Quest score + top-k (nhs_quest_select), row resolution (nhs_resolve_rows),
-the host-row gather (nhs_gather_rows) and attention (nhs_attend_rows). With
-the default single chunk all four run in order on one stream; --side-stream
-puts the gather on a second stream ordered by HIP events, and --chunks n
-pipelines n groups of requests (selection and resolution of the next group
-and attention of the previous one are enqueued around each gather). The
-resolver's tags/LRU are restored from a saved copy at the start of every
-step (a 0.8 MB device copy, inside the timed region) so every step has the
-same 25% misses. Prints one JSON line.
+Quest score + top-k (nhs_quest_select) and row resolution
+(nhs_resolve_rows) for the whole batch, then the host-row gather
+(nhs_gather_rows) and attention (nhs_attend_rows). With --chunks n the
+gathers run on a side stream in n groups of requests and each group's
+attention starts when its gather event fires, overlapping the next group's
+gather; with one chunk everything runs in order on one stream (--side-stream
+moves the gather to a second stream ordered by events). The resolver's
+tags/LRU are restored from a saved copy at the start of every step (a 0.8 MB
+device copy, inside the timed region) so every step has the same 25% misses.
+Prints one JSON line.
 
 `--copy-calibration` instead runs a plain 256 MiB device-to-device copy three
 times: the known-size kernel that scales the FETCH_SIZE / WRITE_SIZE
@@ -256,7 +257,7 @@ def main():
     import torch
 
     from nano_hisparse import _hip
-    from nano_hisparse.batch_step import SparseDecodeBatch, gather_results
+    from nano_hisparse.batch_step import SparseDecodeBatch
 
     _hip.load()
     device = torch.device("cuda:0")
@@ -270,35 +271,34 @@ def main():
 
     names = ("quest", "resolve", "gather", "attention")
     for _ in range(args.warmup):
-        results = run_step(w, step)
+        result = run_step(w, step)
     torch.cuda.synchronize()
-    _, physical, counts = gather_results(results)
+    physical, counts = result.physical, result.counts
     counts_sum = counts.sum(0).tolist()
     valid_rows = int((physical >= 0).sum())
-    chunk_valid = [int((r.physical >= 0).sum()) for r in results]
-    chunk_requests = [r.requests.stop - r.requests.start for r in results]
+    chunk_valid = [int((physical[c] >= 0).sum()) for c in result.chunks]
+    chunk_requests = [c.stop - c.start for c in result.chunks]
     print(f"[bench] counts resident/hot/miss = {counts_sum}, valid rows {valid_rows}, chunks {chunk_requests}",
           file=sys.stderr, flush=True)
 
     # timed region: K steps, synchronized on both sides
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     step_events = [step.timing_events() for _ in range(args.steps)]
-    timed = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start.record(compute)
     for i in range(args.steps):
-        timed.append(run_step(w, step, step_events[i]))
+        run_step(w, step, step_events[i])
     end.record(compute)
     enqueue_s = time.perf_counter() - t0
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = start.elapsed_time(end) / args.steps
     # per kernel: summed over the chunks of a step, then averaged over steps
-    kernel_us = {n: 1e3 * sum(c.events[n][0].elapsed_time(c.events[n][1]) for r in timed for c in r) / args.steps
+    # per stage: summed over the launches of a step, then averaged over steps
+    kernel_us = {n: 1e3 * sum(a.elapsed_time(b) for ev in step_events for a, b in ev[n]) / args.steps
                  for n in names}
-    launches = args.steps * len(results)
-    attn_launch_us = kernel_us["attention"] * args.steps / launches
+    attn_launch_us = kernel_us["attention"] / len(result.chunks)
 
     # measured pinned H2D copy ceiling (copy engine), for reference
     probe = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
@@ -316,14 +316,14 @@ def main():
     del probe, dst
 
     attn_bytes = sum(w.attention_bytes(v, r) for v, r in zip(chunk_valid, chunk_requests))
-    attn_launch_bytes = attn_bytes / len(results)
+    attn_launch_bytes = attn_bytes / len(result.chunks)
     gather_bytes = counts_sum[2] * w.row_bytes
     quest_bytes = w.quest_bytes()
     tokens_per_s = w.batch / (ms_per_step * 1e-3)
     # ideal step: every HBM byte at the HBM peak, or every host byte at the PCIe peak
     ideal_us = 1e6 * max((attn_bytes + quest_bytes + gather_bytes) / HBM_PEAK, gather_bytes / PCIE_PEAK)
     # the committed PMC summary covers the default workload only
-    default = (args.batch, args.context, args.seed, len(results)) == (16, 32768, 42, 1)
+    default = (args.batch, args.context, args.seed, len(result.chunks)) == (16, 32768, 42, 1)
     traffic = traffic_from_profile("attend_kernel") if default else None
     result = {
         "metric": METRIC,
@@ -344,7 +344,7 @@ def main():
             "selected pages 50% resident / 25% hot / 25% host misses, hot rows 4096 per request",
             "batch": w.batch,
             "context": w.context,
-            "chunks": len(results),
+            "chunks": len(result.chunks),
             "gather_stream": "side" if step.transfer is not step.compute else "compute",
             "parallelism": "single GPU",
         },

@@ -109,7 +109,12 @@ __device__ __forceinline__ void load_vec(const void* base, int64_t elem_index, f
   constexpr int nbytes = E * T::bytes;
   const char* p = static_cast<const char*>(base) + elem_index * T::bytes;
   uint32_t w[(nbytes + 3) / 4];
-  if constexpr (nbytes == 16) {
+  if constexpr (nbytes == 32) {
+    const uint4 v0 = *reinterpret_cast<const uint4*>(p);
+    const uint4 v1 = *reinterpret_cast<const uint4*>(p + 16);
+    w[0] = v0.x; w[1] = v0.y; w[2] = v0.z; w[3] = v0.w;
+    w[4] = v1.x; w[5] = v1.y; w[6] = v1.z; w[7] = v1.w;
+  } else if constexpr (nbytes == 16) {
     uint4 v = *reinterpret_cast<const uint4*>(p);
     w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
   } else if constexpr (nbytes == 8) {

@@ -36,6 +36,7 @@ enum { kModeQuest = 0, kModeMean = 1 };
 struct ScoreArgs {
   const void* q;
   int q_dtype;
+  int q_vec;  // query rows may be read with 16-byte loads
   int64_t q_bs, q_hs;
   const void* lo;   // quest: minimum; mean: summaries (fp32)
   const void* hi;   // quest: maximum
@@ -64,12 +65,13 @@ __device__ __forceinline__ int page_count(const int64_t* lengths, int64_t length
 
 // Quest bounds score: (sum_h sum_d max(q*min, q*max)) / q_heads.
 //
-// The term max(q*kmin, q*kmax) is evaluated as fma(q-, kmin, fma(q+, kmax, t))
-// with q+ = max(q, 0) and q- = min(q, 0) (kmax >= kmin): for 16-bit queries
-// and bounds both products are exact, so this adds the reference's term to t
-// (up to the sign of a zero). Lanes are laid out as (page of the step, kv
-// head, 16-byte chunk), so a lane keeps one kv head's query slices in
-// registers for the whole kernel; the next step's bounds are requested
+// The term max(q*kmin, q*kmax) is q * (q > 0 ? kmax : kmin) (kmax >= kmin),
+// added to t with one fma: for 16-bit queries and bounds the product is
+// exact, so this adds the reference's term to t (up to the sign of a zero).
+//
+// General kernel, for pages wider than one wave: lanes are laid out as (page
+// of the step, kv head, chunk), so a lane keeps one kv head's query slices
+// in registers for the whole kernel; the next step's bounds are requested
 // before the current step is summed.
 template <typename T, int E, int G>
 __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a) {
@@ -96,15 +98,11 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
   const int sub = within & (lpr - 1);
   const bool active = page_local < pages_per_step;
   const bool data = active && sub < a.lanes_used;
-  float qp[G][E], qn[G][E];
+  float qv[G][E];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float q = data && g < a.group ? qs[(kh * a.group + g) * a.head_dim + sub * E + e] : 0.f;
-      qp[g][e] = q > 0.f ? q : 0.f;
-      qn[g][e] = q < 0.f ? q : 0.f;
-    }
+    for (int e = 0; e < E; ++e) qv[g][e] = data && g < a.group ? qs[(kh * a.group + g) * a.head_dim + sub * E + e] : 0.f;
   const char* lo = static_cast<const char*>(a.lo) + (int64_t)b * a.b_bs * T::bytes;
   const char* hi = static_cast<const char*>(a.hi) + (int64_t)b * a.b_bs * T::bytes;
   const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
@@ -124,10 +122,7 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
     for (int g = 0; g < G; ++g) {
       float x = 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        x = __builtin_fmaf(qp[g][e], mx[e], x);
-        x = __builtin_fmaf(qn[g][e], mn[e], x);
-      }
+      for (int e = 0; e < E; ++e) x = __builtin_fmaf(qv[g][e], qv[g][e] > 0.f ? mx[e] : mn[e], x);
       t[g] = group_sum(x, lpr);
     }
     if (active && sub == 0 && p < p_end)
@@ -147,6 +142,114 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
       mn[e] = mn2[e];
       mx[e] = mx2[e];
     }
+  }
+}
+
+// Page kernel, for pages that fit one wave (kv_heads * lanes per head <=
+// 64, 32-byte chunks): lane = (page of the wave, kv head, chunk). A wave
+// loads its query slices straight into registers, issues the bounds of all
+// its kPageSlots page slots, then scores them one by one: per-lane chunk sum,
+// DPP tree over a head's lanes, and the sequential head sum through the
+// wave's own LDS rows, so no workgroup barrier is involved.
+constexpr int kPageThreads = 256;
+constexpr int kPageWaves = kPageThreads / kWave;
+constexpr int kPageSlots = 4;
+constexpr int kMaxHeadsPerWave = 512;  // pages per wave * q_heads rounded up to 4 (+ 16 read past the end)
+
+template <typename T, int E, int G>
+__global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float hsum[kPageWaves][kMaxHeadsPerWave + 16];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int b = blockIdx.y;
+  const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
+  const int ppw = a.pages_per_step;  // pages per wave slot
+  const int wave_first = (blockIdx.x * kPageWaves + wave) * kPageSlots * ppw;
+  if (wave_first >= count) return;
+  const int lanes_per_page = a.kv_heads << a.lpr_log2;
+  const int page_local = lane / lanes_per_page;
+  const int within = lane - page_local * lanes_per_page;
+  const int kh = within >> a.lpr_log2;
+  const int sub = within & ((1 << a.lpr_log2) - 1);
+  const bool data = page_local < ppw && sub < a.lanes_used;
+
+  // query slices: with the bounds' dtype and 16-byte rows, every head's
+  // vector loads are issued before the first is used
+  float qv[G][E];
+  int64_t qi[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    qi[g] = (int64_t)b * a.q_bs + (data && g < a.group ? (int64_t)(kh * a.group + g) * a.q_hs + sub * E : 0);
+  if (a.q_vec && a.q_dtype == T::dtype) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) load_vec<T, E>(a.q, qi[g], qv[g]);
+  } else {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < E; ++e) qv[g][e] = load_elem(a.q, a.q_dtype, qi[g] + (data ? e : 0));
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    if (!(data && g < a.group))
+#pragma unroll
+      for (int e = 0; e < E; ++e) qv[g][e] = 0.f;
+  const char* lo = static_cast<const char*>(a.lo) + (int64_t)b * a.b_bs * T::bytes;
+  const char* hi = static_cast<const char*>(a.hi) + (int64_t)b * a.b_bs * T::bytes;
+  const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
+  const int64_t lane_off = data ? (int64_t)kh * a.head_dim + sub * E : 0;
+  float mn[kPageSlots][E], mx[kPageSlots][E];
+#pragma unroll
+  for (int s = 0; s < kPageSlots; ++s) {
+    const int p = wave_first + s * ppw + page_local;
+    const int pc = p < count ? p : wave_first;  // lanes past the end reread a live page
+    load_vec<T, E>(lo, (int64_t)pc * page_elems + lane_off, mn[s]);
+    load_vec<T, E>(hi, (int64_t)pc * page_elems + lane_off, mx[s]);
+  }
+  float* hs = hsum[wave];
+  const int lpr = 1 << a.lpr_log2;
+#pragma unroll
+  for (int s = 0; s < kPageSlots; ++s) {
+    const int p0 = wave_first + s * ppw;
+    if (p0 >= count) break;
+    float t[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float x = 0.f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) x = __builtin_fmaf(qv[g][e], qv[g][e] > 0.f ? mx[s][e] : mn[s][e], x);
+      t[g] = group_sum(x, lpr);
+    }
+    const int row_stride = (a.q_heads + 3) & ~3;  // 16-byte aligned rows
+    if (data && sub == 0)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (g < a.group) hs[page_local * row_stride + kh * a.group + g] = t[g];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < ppw && p0 + lane < count) {
+      // sequential sum over the heads; 16 values are read per batch so the
+      // adds do not wait on one LDS round trip each
+      const float* row = hs + lane * row_stride;
+      float total = 0.f;
+      for (int h0 = 0; h0 < a.q_heads; h0 += 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float4 w = *reinterpret_cast<const float4*>(row + h0 + 4 * j);
+          v[4 * j] = w.x, v[4 * j + 1] = w.y, v[4 * j + 2] = w.z, v[4 * j + 3] = w.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (h0 + j < a.q_heads) total = h0 + j == 0 ? v[j] : total + v[j];
+      }
+      a.scores[(int64_t)b * a.max_pages + p0 + lane] = total / (float)a.q_heads;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 
@@ -362,6 +465,13 @@ static int chunk_elems(int head_dim, int esize) {
   return 0;
 }
 
+// Quest cuts a bound row into 32-byte chunks when it is a multiple of 32
+// bytes of at most 64 chunks, else as chunk_elems() does.
+static int quest_chunk_elems(int head_dim, int esize) {
+  if ((head_dim * esize) % 32 == 0 && head_dim * esize / 32 <= 64) return 32 / esize;
+  return chunk_elems(head_dim, esize);
+}
+
 static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, const char* who, hipEvent_t start,
                          hipEvent_t stop) {
   launch(select_topk_kernel, dim3((unsigned)batch), dim3(kSelectThreads), 0, stream, start, stop, s);
@@ -387,15 +497,20 @@ extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtyp
   if ((int64_t)q_heads * head_dim + 8 * q_heads > 16384)
     return fail(NHS_ERR_UNSUPPORTED, "%s: q_heads * head_dim too large", who);
   const int esize = elem_size(bounds_dtype);
-  const int E = chunk_elems(head_dim, esize);
+  const int E = quest_chunk_elems(head_dim, esize);
   if (E == 0) return fail(NHS_ERR_UNSUPPORTED, "%s: head_dim %d unsupported", who, head_dim);
-  if (E > 1 && ((uintptr_t)minimum | (uintptr_t)maximum) % 16)
+  if (E > 1 && (((uintptr_t)minimum | (uintptr_t)maximum) % 16 || (bounds_batch_stride * esize) % 16))
     return fail(NHS_ERR_INVALID, "%s: bounds must be 16-byte aligned", who);
   if (batch == 0) return NHS_OK;
   hipStream_t s = (hipStream_t)stream;
   ScoreArgs a;
   a.q = query;
   a.q_dtype = q_dtype;
+  {
+    const int qes = elem_size(q_dtype);
+    a.q_vec = (E * qes) % 16 == 0 && (uintptr_t)query % 16 == 0 && (q_head_stride * qes) % 16 == 0 &&
+              (q_batch_stride * qes) % 16 == 0;
+  }
   a.q_bs = q_batch_stride;
   a.q_hs = q_head_stride;
   a.lo = minimum;
@@ -416,30 +531,56 @@ extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtyp
   if (a.group > 8 || lanes_per_page > kQuestThreads)
     return fail(NHS_ERR_UNSUPPORTED, "%s: needs q_heads/kv_heads <= 8 and kv_heads * lanes per head <= %d", who,
                 kQuestThreads);
-  const int threads = lanes_per_page >= 256 ? ((lanes_per_page + 63) / 64) * 64 : 256;
-  a.pages_per_step = threads / lanes_per_page;
-  a.pages_per_block = a.pages_per_step * ((kPagesPerBlock + a.pages_per_step - 1) / a.pages_per_step);
-  dim3 grid((unsigned)((max_pages + a.pages_per_block - 1) / a.pages_per_block), (unsigned)batch);
-  size_t lds = ((size_t)q_heads * head_dim + (size_t)a.pages_per_step * q_heads) * sizeof(float);
-  if (top_pages < max_pages) {  // scores are not needed when every page is kept
-    const int G = a.group == 1 ? 1 : a.group == 2 ? 2 : a.group <= 4 ? 4 : 8;
-    void (*kernel)(ScoreArgs) = nullptr;
-    switch (bounds_dtype * 64 + E * 8 + G) {
+  const int G = a.group == 1 ? 1 : a.group == 2 ? 2 : a.group <= 4 ? 4 : 8;
+  void (*kernel)(ScoreArgs) = nullptr;
+  dim3 grid, block;
+  size_t lds = 0;
+  const int ppw = lanes_per_page <= kWave ? kWave / lanes_per_page : 0;
+  if (E * esize == 32 && ppw > 0 && ppw * ((q_heads + 3) & ~3) <= kMaxHeadsPerWave) {
+    // a page fits one wave: the page kernel
+    a.pages_per_step = ppw;
+    a.pages_per_block = kPageWaves * kPageSlots * ppw;
+    grid = dim3((unsigned)((max_pages + a.pages_per_block - 1) / a.pages_per_block), (unsigned)batch);
+    block = dim3(kPageThreads);
+    switch (bounds_dtype * 8 + G) {
+#define NHS_PAGE_CASE(DT, TY, EE, GG) \
+  case DT * 8 + GG: kernel = quest_page_kernel<TY, EE, GG>; break;
+#define NHS_PAGE_GS(DT, TY, EE) \
+  NHS_PAGE_CASE(DT, TY, EE, 1) NHS_PAGE_CASE(DT, TY, EE, 2) NHS_PAGE_CASE(DT, TY, EE, 4) NHS_PAGE_CASE(DT, TY, EE, 8)
+      NHS_PAGE_GS(NHS_F32, F32, 8)
+      NHS_PAGE_GS(NHS_F16, F16, 16)
+      NHS_PAGE_GS(NHS_BF16, BF16, 16)
+#undef NHS_PAGE_GS
+#undef NHS_PAGE_CASE
+    }
+  } else {
+    const int threads = lanes_per_page >= 256 ? ((lanes_per_page + 63) / 64) * 64 : 256;
+    a.pages_per_step = threads / lanes_per_page;
+    a.pages_per_block = a.pages_per_step * ((kPagesPerBlock + a.pages_per_step - 1) / a.pages_per_step);
+    grid = dim3((unsigned)((max_pages + a.pages_per_block - 1) / a.pages_per_block), (unsigned)batch);
+    block = dim3(threads);
+    lds = ((size_t)q_heads * head_dim + (size_t)a.pages_per_step * q_heads) * sizeof(float);
+    switch (bounds_dtype * 1024 + E * 16 + G) {
 #define NHS_QUEST_CASE(DT, TY, EE, GG) \
-  case DT * 64 + EE * 8 + GG: kernel = quest_score_kernel<TY, EE, GG>; break;
+  case DT * 1024 + EE * 16 + GG: kernel = quest_score_kernel<TY, EE, GG>; break;
 #define NHS_QUEST_GS(DT, TY, EE) \
   NHS_QUEST_CASE(DT, TY, EE, 1) NHS_QUEST_CASE(DT, TY, EE, 2) NHS_QUEST_CASE(DT, TY, EE, 4) NHS_QUEST_CASE(DT, TY, EE, 8)
+      NHS_QUEST_GS(NHS_F32, F32, 8)
       NHS_QUEST_GS(NHS_F32, F32, 4)
       NHS_QUEST_GS(NHS_F32, F32, 1)
+      NHS_QUEST_GS(NHS_F16, F16, 16)
       NHS_QUEST_GS(NHS_F16, F16, 8)
       NHS_QUEST_GS(NHS_F16, F16, 1)
+      NHS_QUEST_GS(NHS_BF16, BF16, 16)
       NHS_QUEST_GS(NHS_BF16, BF16, 8)
       NHS_QUEST_GS(NHS_BF16, BF16, 1)
 #undef NHS_QUEST_GS
 #undef NHS_QUEST_CASE
     }
+  }
+  if (top_pages < max_pages) {  // scores are not needed when every page is kept
     if (!kernel) return fail(NHS_ERR_UNSUPPORTED, "%s: no scoring kernel", who);
-    launch(kernel, grid, dim3(threads), lds, s, ev.start, nullptr, a);
+    launch(kernel, grid, block, lds, s, ev.start, nullptr, a);
     ev.start = nullptr;  // the start event belongs to the first kernel
     st = launch_status(who);
     if (st != NHS_OK) return st;

@@ -1,26 +1,23 @@
-"""Batched sparse decode step for one layer, pipelined across two streams.
+"""Batched sparse decode step for one layer, with the host-row gather
+double-buffered against attention on a side stream.
 
 The reference resolves, gathers and attends one (request, layer) at a time
 (hybrid.py:412-469, attention.py:18-35). Here B requests whose layer tables
-are stacked ([B, ...] tensors with a common stride) run as chunks of
-requests: for every chunk the compute stream selects pages (Quest) and
-resolves rows, the transfer stream gathers that chunk's missed rows from
-pinned host memory, and the compute stream attends over the chunk once its
-gather event has fired. The compute stream enqueues chunk c+1's selection
-and resolution before chunk c's attention, so while the transfer stream is
-busy with one chunk's host rows the compute stream works on its neighbours
-(double buffering); HIP events order the two streams, and nothing is read
-back to the host.
+are stacked ([B, ...] tensors with a common stride) take one Quest launch
+and one resolver launch; their host-row gathers then run on the transfer
+stream in `chunks` groups of requests, and the compute stream attends over
+each group as soon as that group's gather event has fired, while the
+transfer stream already copies the next group's rows. HIP events order the
+two streams; nothing is read back to the host.
 
-On MI355X the default is one chunk. Kernels that run while the gather
-streams host rows over PCIe slow down 2-7x, even on CUs the gather does not
-use (a CU-masked transfer stream of 16 CUs still saturates the link), so the
-overlap costs more than it hides at the Llama-3-8B decode shape: 778 us per
-step unchunked against 805-2073 us with 2-8 chunks. The chunked schedule
-stays for shapes with little gather traffic per chunk. With one chunk there
-is nothing to overlap, and each event hop between two queues costs ~10 us,
-so the gather then runs on the compute stream unless a transfer stream is
-passed (740 us against 760 us per step).
+Measured on MI355X at the Llama-3-8B decode shape (16 requests, 2048 rows,
+25% of them gathered): kernels that run beside the PCIe gather slow down
+2-7x (the contention is in the shared L2/fabric path: it stays when the
+gather is confined to 16 CUs, which alone still saturate the link), so only
+the attention, not the selection or resolution, is overlapped with it. With
+one chunk there is nothing to overlap and each event hop between two queues
+costs ~10 us, so the gather then runs on the compute stream unless a
+transfer stream is passed.
 """
 
 from __future__ import annotations
@@ -57,23 +54,22 @@ class BatchTables:
 
 
 @dataclass
-class ChunkResult:
-    requests: slice
-    positions: torch.Tensor  # [b, top_pages * P] int32 selected token positions
-    physical: torch.Tensor  # [b, top_pages * P] int64 pool rows (-1 padding)
-    counts: torch.Tensor  # [b, 3] int64 resident / hot / miss
-    events: dict | None = None
+class StepResult:
+    positions: torch.Tensor  # [B, top_pages * P] int32 selected token positions (-1 padding)
+    physical: torch.Tensor  # [B, top_pages * P] int64 pool rows (-1 padding)
+    counts: torch.Tensor  # [B, 3] int64 resident / hot / miss
+    chunks: list  # slices of the batch gathered and attended together
 
 
 class SparseDecodeBatch:
     """One layer's sparse decode for B requests: Quest top-k -> resolve ->
-    host-row gather (transfer stream) -> GQA row attention, in `chunks`
-    pipelined groups of requests.
+    host-row gather -> GQA row attention.
 
     pool: the device KV pool [blocks, 2, P, Hkv, D]; host: the pinned host
-    store of the same page shape. Tensors live on one GPU. transfer: the
-    stream of the gathers (default: the compute stream for one chunk, a new
-    side stream for several).
+    store of the same page shape. Tensors live on one GPU. chunks: request
+    groups whose gathers and attentions are pipelined. transfer: the stream
+    of the gathers (default: the compute stream for one chunk, a new side
+    stream for several).
     """
 
     def __init__(self, pool, host, tables: BatchTables, page_size, top_pages, keep_sink=True, chunks=1,
@@ -95,6 +91,17 @@ class SparseDecodeBatch:
         self.transfer = transfer
         self._workspace = None
 
+    def timing_events(self):
+        """Events for one timed step: a (start, stop) pair for the Quest and
+        resolver launches and, per chunk, for its gather and its attention
+        (create them before a timed region)."""
+        return {
+            "quest": [rk.timing_events()],
+            "resolve": [rk.timing_events()],
+            "gather": [rk.timing_events() for _ in self.slices],
+            "attention": [rk.timing_events() for _ in self.slices],
+        }
+
     def _attend(self, query, physical, out):
         lib = rk._hip.load()
         B, Hq, D = query.shape
@@ -103,78 +110,53 @@ class SparseDecodeBatch:
             self._workspace = torch.zeros(max(need, 1 << 16), dtype=torch.uint8, device=query.device)
         rk.attend_batched(query, self.pool, physical, self.page_size, out=out, workspace=self._workspace)
 
-    def timing_events(self):
-        """Events for one timed step: per chunk, a (start, stop) pair for
-        each of its four launchers (create them before a timed region)."""
-        names = ("quest", "resolve", "gather", "attention")
-        return [{n: rk.timing_events() for n in names} for _ in self.slices]
-
     def step(self, query, out=None, events=None):
         """Attend query [B, Hq, D] over each request's Quest selection.
 
-        Returns (out [B, Hq, D] in the query dtype, [ChunkResult]). With
-        `events` from timing_events(), each launcher's events are stamped by
-        its dispatches themselves (begin of its first kernel, end of its
-        last).
+        Returns (out [B, Hq, D] in the query dtype, StepResult). With
+        `events` from timing_events(), every launch stamps its pair with its
+        kernels' own begin and end.
         """
         t = self.tables
-        B = t.batch
-        if query.shape[0] != B:
+        if query.shape[0] != t.batch:
             raise ValueError("query batch differs from the tables")
         if out is None:
             out = torch.empty_like(query)
         compute, transfer = self.compute, self.transfer
+        side = transfer is not compute
 
-        def mark(events, name):
+        def mark(name, i=0):
             if events is not None:
-                rk.set_launch_events(*events[name])
+                rk.set_launch_events(*events[name][i])
 
-        results, waiting = [], []
         with torch.cuda.stream(compute):
-            for i, s in enumerate(self.slices):
-                chunk_events = events[i] if events is not None else None
-                mark(chunk_events, "quest")
-                _, positions, _ = rk.quest_batched(
-                    query[s], t.minimum[s], t.maximum[s], t.lengths[s], self.page_size, self.top_pages,
-                    self.keep_sink,
-                )
-                mark(chunk_events, "resolve")
-                physical, miss_host, miss_device, counts = rk.resolve_batched(
-                    positions, t.source[s], t.resident[s], t.hot[s], t.tags[s], t.lru[s], t.lengths[s],
-                    self.page_size,
-                )
+            mark("quest")
+            _, positions, _ = rk.quest_batched(
+                query, t.minimum, t.maximum, t.lengths, self.page_size, self.top_pages, self.keep_sink
+            )
+            mark("resolve")
+            physical, miss_host, miss_device, counts = rk.resolve_batched(
+                positions, t.source, t.resident, t.hot, t.tags, t.lru, t.lengths, self.page_size
+            )
+            if side:
                 resolved = torch.cuda.Event()
                 resolved.record(compute)
                 transfer.wait_event(resolved)
-                with torch.cuda.stream(transfer):
-                    mark(chunk_events, "gather")
-                    rk.gather_plan(self.alias, self.pool, miss_host, miss_device, self.page_size)
-                    gathered = torch.cuda.Event()
-                    gathered.record(transfer)
+            gathered = []
+            with torch.cuda.stream(transfer):
+                for i, s in enumerate(self.slices):
+                    mark("gather", i)
+                    rk.gather_plan(self.alias, self.pool, miss_host[s], miss_device[s], self.page_size)
+                    if side:
+                        done = torch.cuda.Event()
+                        done.record(transfer)
+                        gathered.append(done)
+            if side:
                 miss_host.record_stream(transfer)
                 miss_device.record_stream(transfer)
-                result = ChunkResult(s, positions, physical, counts, chunk_events)
-                results.append(result)
-                if waiting:  # attend the previous chunk now that this one's plan is enqueued
-                    self._finish(query, out, *waiting.pop())
-                waiting.append((result, gathered))
-            while waiting:
-                self._finish(query, out, *waiting.pop())
-        return out, results
-
-    def _finish(self, query, out, result, gathered):
-        compute = self.compute
-        compute.wait_event(gathered)
-        if result.events is not None:
-            rk.set_launch_events(*result.events["attention"])
-        s = result.requests
-        self._attend(query[s], result.physical, out[s])
-
-
-def gather_results(results):
-    """Concatenate the per-chunk positions, rows and counts along the batch."""
-    return (
-        torch.cat([r.positions for r in results]),
-        torch.cat([r.physical for r in results]),
-        torch.cat([r.counts for r in results]),
-    )
+            for i, s in enumerate(self.slices):
+                if side:
+                    compute.wait_event(gathered[i])
+                mark("attention", i)
+                self._attend(query[s], physical[s], out[s])
+        return out, StepResult(positions, physical, counts, list(self.slices))

@@ -16,16 +16,17 @@
  * The selectors sum fp32 terms in one fixed order, which the HIP kernels
  * follow exactly (the reference sums in torch's CPU reduction order, which
  * no other implementation reproduces): a bound row of head_dim elements is
- * cut into E-element chunks (E = 16 bytes / element size when the row is a
- * multiple of 16 bytes, else 1); each chunk is summed sequentially from
- * 0.0; the chunk sums, padded with +0.0 to a power of two, are added as a
- * pairwise tree in chunk order; the per-head sums are added sequentially.
- * The Quest term max(q*kmin, q*kmax) (selection.py:84) is accumulated as
- * fma(q-, kmin, fma(q+, kmax, t)) with q+ = max(q, 0), q- = min(q, 0): for
- * 16-bit queries and bounds the products are exact, so each step adds the
- * reference's term (up to the sign of a zero); for fp32 inputs the products
- * are not rounded before the addition. The mean selector rounds each
- * product before adding it. Build with -ffp-contract=off so no other
+ * cut into E-element chunks (Quest: E = 32 bytes / element size when the
+ * row is a multiple of 32 bytes; otherwise, and for the mean selector, 16
+ * bytes / element size when the row is a multiple of 16 bytes, else 1);
+ * each chunk is summed sequentially from 0.0; the chunk sums, padded with
+ * +0.0 to a power of two, are added as a pairwise tree in chunk order; the
+ * per-head sums are added sequentially. The Quest term max(q*kmin, q*kmax)
+ * (selection.py:84) is q * (q > 0 ? kmax : kmin), accumulated with one
+ * fma: for 16-bit queries and bounds the product is exact, so each step
+ * adds the reference's term (up to the sign of a zero); for fp32 inputs the
+ * product is not rounded before the addition. The mean selector rounds
+ * each product before adding it. Build with -ffp-contract=off so no other
  * product is fused.
  */
 #include <math.h>
@@ -144,6 +145,13 @@ static int chunk_elems(int head_dim, int esize) {
   return 0;
 }
 
+/* Quest cuts a bound row into 32-byte chunks when it is a multiple of 32
+   bytes of at most 64 chunks, else as chunk_elems() does. */
+static int quest_chunk_elems(int head_dim, int esize) {
+  if ((head_dim * esize) % 32 == 0 && head_dim * esize / 32 <= 64) return 32 / esize;
+  return chunk_elems(head_dim, esize);
+}
+
 static int pow2_at_least(int v) {
   int p = 1;
   while (p < v) p <<= 1;
@@ -167,7 +175,7 @@ static int page_count(int64_t len, int page_size, int max_pages) {
 static void quest_scores_one(const void* q, int q_dtype, int64_t q_hs, const void* lo, const void* hi, int bdt,
                              int q_heads, int kv_heads, int head_dim, int count, float* scores) {
   const int group = q_heads / kv_heads;
-  const int E = chunk_elems(head_dim, elem_size(bdt));
+  const int E = quest_chunk_elems(head_dim, elem_size(bdt));
   const int used = head_dim / E, L = pow2_at_least(used);
   float* t = (float*)malloc(sizeof(float) * (size_t)L);
   float* hs = (float*)malloc(sizeof(float) * (size_t)q_heads);
@@ -179,13 +187,13 @@ static void quest_scores_one(const void* q, int q_dtype, int64_t q_hs, const voi
         t[l] = 0.0f;
         if (l >= used) continue;
         for (int e = 0; e < E; ++e) {
-          /* max(q*kmin, q*kmax) added to t as fma(q-, kmin, fma(q+, kmax, t)):
-             exact for 16-bit inputs, whose products fit in fp32 */
+          /* max(q*kmin, q*kmax) = q * (q > 0 ? kmax : kmin) for kmin <= kmax,
+             added to t with one fma: exact per step for 16-bit inputs, whose
+             products fit in fp32 */
           int d = l * E + e;
           float qd = load_elem(q, q_dtype, (int64_t)h * q_hs + d);
-          float qpos = qd > 0.0f ? qd : 0.0f, qneg = qd < 0.0f ? qd : 0.0f;
-          t[l] = fmaf(qpos, load_elem(hi, bdt, base + d), t[l]);
-          t[l] = fmaf(qneg, load_elem(lo, bdt, base + d), t[l]);
+          float k = qd > 0.0f ? load_elem(hi, bdt, base + d) : load_elem(lo, bdt, base + d);
+          t[l] = fmaf(qd, k, t[l]);
         }
       }
       hs[h] = tree_sum(t, L);

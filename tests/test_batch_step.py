@@ -1,4 +1,5 @@
-"""The pipelined batched decode step (nano_hisparse.batch_step) against the C
+"""The batched decode step (nano_hisparse.batch_step, gathers pipelined with
+attention in chunks of requests on a side stream) against the C
 oracle run request by request: selected positions, resolved rows, the
 gathered pool bytes and the tags/LRU state bit-exact; attention within 2e-2
 (bf16 KV) or 1e-4 (fp32 KV) max-abs of the oracle's float64 softmax.
@@ -81,7 +82,7 @@ def oracle_step(host, pool, tables, q, page, top_pages, tags, lru):
 )
 def test_pipelined_step_matches_oracle(gpu, batch, n_pages, page, kv_heads, head_dim, q_heads, top_pages,
                                        hot_rows, dtype, chunks, tol):
-    from nano_hisparse.batch_step import BatchTables, SparseDecodeBatch, gather_results
+    from nano_hisparse.batch_step import BatchTables, SparseDecodeBatch
 
     host, pool, tables, q = build(batch, n_pages, page, kv_heads, head_dim, q_heads, top_pages, hot_rows, dtype, 7)
     dev = BatchTables(*(t.to(gpu) for t in (tables.source, tables.resident, tables.hot, tables.tags, tables.lru,
@@ -93,8 +94,8 @@ def test_pipelined_step_matches_oracle(gpu, batch, n_pages, page, kv_heads, head
     cpool = pool.clone()
     for it in range(3):  # the tables evolve: later steps hit rows earlier steps gathered
         query = q if it == 0 else torch.randn(q.shape, generator=torch.Generator().manual_seed(it)).to(dtype)
-        out, results = step.step(query.to(gpu))
-        positions, physical, counts = gather_results(results)
+        out, result = step.step(query.to(gpu))
+        positions, physical, counts = result.positions, result.physical, result.counts
         torch.cuda.synchronize()
         e_pos, e_phys, e_out = oracle_step(host, cpool, tables, query, page, top_pages, tags, lru)
         assert torch.equal(positions.cpu(), e_pos), f"step {it}: positions"
