@@ -29,6 +29,8 @@ constexpr int kMaxK = NHS_MAX_POSITIONS;          // sorted entries per item
 constexpr int kMaxH = NHS_MAX_HOT_ROWS;           // hot rows per item
 constexpr int kKPerThread = kMaxK / kResolveThreads;  // 4
 constexpr int kHashCap = 2 * kMaxK;                // load factor <= 1/2
+constexpr int kRegH = 8;        // hot rows per thread whose tag and lru are loaded at entry (H <= 8192)
+constexpr int kHotCache = 1024; // hot blocks staged in LDS at entry
 
 struct ResolveArgs {
   int n;  // positions per item
@@ -72,13 +74,17 @@ struct ResolveShared {
   int32_t victims[kMaxK];     // victims[0 .. min(n, H)-1]
   int64_t scan64[kResolveThreads / 64 + 1];
   int32_t wcount[2][kResolveThreads / 64][4];  // per-wave category counts, double-buffered
+  int32_t hot[kHotCache];                      // the item's hot block table, when it fits
 };
 
 // Ranks within one 1024-slot chunk: for category `cat` (0..3, or -1 for an
 // empty slot) returns the number of lower threads of the block with the same
 // category and writes the chunk's per-category totals to tot[4]. One barrier;
 // the count table alternates between two buffers, so a buffer is rewritten
-// only after every thread has passed the next chunk's barrier.
+// only after every thread has passed the next chunk's barrier. After the
+// barrier lane w * 4 + c of every wave holds wave w's count of category c,
+// and a shuffle scan with stride 4 gives every wave the prefix over waves.
+static_assert(kResolveThreads / 64 * 4 == 64, "one lane per (wave, category)");
 __device__ __forceinline__ int chunk_rank(int cat, int32_t (*wcount)[kResolveThreads / 64][4], int parity,
                                           int* tot) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -91,18 +97,16 @@ __device__ __forceinline__ int chunk_rank(int cat, int32_t (*wcount)[kResolveThr
     if (lane == 0) wcount[parity][wave][c] = __popcll(m);
   }
   __syncthreads();
-  int before = 0;
+  const int v = (&wcount[parity][0][0])[lane];
+  int incl = v;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) tot[c] = 0;
-#pragma unroll 1
-  for (int w = 0; w < kResolveThreads / 64; ++w) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      int v = wcount[parity][w][c];
-      tot[c] += v;
-      if (w < wave && c == cat) before += v;
-    }
+  for (int d = 4; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d);
+    if (lane >= d) incl += o;
   }
+  const int before = __shfl(incl - v, wave * 4 + (cat < 0 ? 0 : cat));
+#pragma unroll
+  for (int c = 0; c < 4; ++c) tot[c] = __shfl(incl, 60 + c);
   return before + mine;
 }
 
@@ -129,44 +133,90 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   int kp = 1;
   while (kp < n) kp <<= 1;
 
-  // ---- 1. keys and bitonic sort -------------------------------------------
-  for (int i = tid; i < kp; i += kResolveThreads) {
-    uint64_t key = ~0ull;
-    if (i < n) {
-      int64_t raw = a.positions_i64
-                        ? static_cast<const int64_t*>(a.positions)[(int64_t)b * a.positions_stride + i]
-                        : (int64_t) static_cast<const int32_t*>(a.positions)[(int64_t)b * a.positions_stride + i];
-      int64_t norm = (raw >= 0 && raw < length) ? raw : length;
-      key = ((uint64_t)norm << 32) | (uint32_t)i;
-    }
-    sh.u.keys[i] = key;
+  // Loads that depend on nothing are issued first: the tags and lru of the
+  // first kRegH * kResolveThreads hot rows (registers) and the hot block
+  // table (LDS), so their latency overlaps the position lookups below.
+  const int32_t* tags_in = a.tags + (int64_t)b * a.tags_stride;
+  const int64_t* lru_in = a.lru + (int64_t)b * a.lru_stride;
+  int32_t tag_r[kRegH];
+  int64_t lru_r[kRegH];
+#pragma unroll
+  for (int i = 0; i < kRegH; ++i) {
+    const int r = i * kResolveThreads + tid;
+    tag_r[i] = r < H ? tags_in[r] : -1;
+    lru_r[i] = r < H ? lru_in[r] : 0;
   }
-  __syncthreads();
+  const int hot_blocks = (H + P - 1) / P;
+  const bool hot_cached = hot_blocks <= kHotCache;
+  const int32_t* hot = a.hot + (int64_t)b * a.hot_stride;
+  if (hot_cached)
+    for (int i = tid; i < hot_blocks; i += kResolveThreads) sh.hot[i] = hot[i];
+
+  // ---- 1. keys; sorted unless a pair is inverted ---------------------------
+  // A thread owns the contiguous run j0 .. j0 + per - 1 of sorted entries.
   // Selector output is already in order (ascending positions, -1 padding at
-  // the end maps to `length`); the sort is skipped when no pair is inverted.
+  // the end maps to `length`), so the page table lookups for the entries in
+  // input order are issued right away and kept when no pair is inverted.
+  const int per = (n + kResolveThreads - 1) / kResolveThreads;  // <= kKPerThread
+  const int j0 = tid * per;
+  uint64_t key[kKPerThread];
+  int64_t src[kKPerThread], res[kKPerThread];
+  auto lookup = [&](int q) {
+    const int64_t lg = (int64_t)(key[q] >> 32);
+    // Positions are < 2^31 (int32 host tags); page = min(lg / P, n_pages - 1).
+    const uint32_t pg = a.page_div.div((uint32_t)lg);
+    const int64_t page = pg < (uint32_t)(a.n_pages - 1) ? (int64_t)pg : (int64_t)(a.n_pages - 1);
+    src[q] = a.source[(int64_t)b * a.page_stride + page];
+    res[q] = a.resident[(int64_t)b * a.page_stride + page];
+  };
+#pragma unroll
+  for (int q = 0; q < kKPerThread; ++q) {
+    const int j = j0 + q;
+    key[q] = ~0ull;
+    src[q] = res[q] = -1;
+    if (q < per && j < n) {
+      const int64_t raw = a.positions_i64
+                              ? static_cast<const int64_t*>(a.positions)[(int64_t)b * a.positions_stride + j]
+                              : (int64_t) static_cast<const int32_t*>(a.positions)[(int64_t)b * a.positions_stride + j];
+      const int64_t norm = (raw >= 0 && raw < length) ? raw : length;
+      key[q] = ((uint64_t)norm << 32) | (uint32_t)j;
+      sh.u.keys[j] = key[q];
+      lookup(q);
+    }
+  }
+  for (int i = n + tid; i < kp; i += kResolveThreads) sh.u.keys[i] = ~0ull;  // sort padding
+  __syncthreads();
   int inverted = 0;
   for (int i = tid; i + 1 < n; i += kResolveThreads) inverted |= sh.u.keys[i] > sh.u.keys[i + 1];
   const bool sorted = !__syncthreads_or(inverted);
-  for (int k = 2; !sorted && k <= kp; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < kp; i += kResolveThreads) {
-        int ixj = i ^ j;
-        if (ixj > i) {
-          uint64_t x = sh.u.keys[i], y = sh.u.keys[ixj];
-          bool up = (i & k) == 0;
-          if ((x > y) == up) {
-            sh.u.keys[i] = y;
-            sh.u.keys[ixj] = x;
+  if (!sorted) {
+    for (int k = 2; k <= kp; k <<= 1) {
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        for (int i = tid; i < kp; i += kResolveThreads) {
+          int ixj = i ^ j;
+          if (ixj > i) {
+            uint64_t x = sh.u.keys[i], y = sh.u.keys[ixj];
+            bool up = (i & k) == 0;
+            if ((x > y) == up) {
+              sh.u.keys[i] = y;
+              sh.u.keys[ixj] = x;
+            }
           }
         }
+        __syncthreads();
       }
-      __syncthreads();
+    }
+#pragma unroll
+    for (int q = 0; q < kKPerThread; ++q) {
+      const int j = j0 + q;
+      if (q < per && j < n) {
+        key[q] = sh.u.keys[j];
+        lookup(q);
+      }
     }
   }
 
-  // ---- 2. per sorted entry (thread owns a contiguous run of entries) -------
-  const int per = (n + kResolveThreads - 1) / kResolveThreads;  // <= kKPerThread
-  const int j0 = tid * per;
+  // ---- 2. per sorted entry -------------------------------------------------
   int64_t host[kKPerThread];
   int32_t in_idx[kKPerThread], res_blk[kKPerThread], off[kKPerThread];
   bool run_start[kKPerThread], rhit[kKPerThread], nhot[kKPerThread];
@@ -179,23 +229,18 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     res_blk[q] = -1;
     off[q] = 0;
     if (q < per && j < n) {
-      uint64_t key = sh.u.keys[j];
-      int64_t lg = (int64_t)(key >> 32);
-      in_idx[q] = (int32_t)(key & 0xffffffffu);
+      int64_t lg = (int64_t)(key[q] >> 32);
+      in_idx[q] = (int32_t)(key[q] & 0xffffffffu);
       run_start[q] = j == 0 || (int64_t)(sh.u.keys[j - 1] >> 32) != lg;
       bool unique = lg < length && run_start[q];
-      // Positions are < 2^31 (int32 host tags); page = min(lg / P, n_pages - 1).
       uint32_t pg = a.page_div.div((uint32_t)lg);
       int32_t o = (int32_t)((uint32_t)lg - pg * (uint32_t)P);
-      int64_t page = pg < (uint32_t)(a.n_pages - 1) ? (int64_t)pg : (int64_t)(a.n_pages - 1);
-      int64_t src = a.source[(int64_t)b * a.page_stride + page];
-      int64_t res = a.resident[(int64_t)b * a.page_stride + page];
       off[q] = o;
-      host[q] = src * P + o;
-      bool valid = unique && src >= 0;
-      rhit[q] = valid && res >= 0;
+      host[q] = src[q] * P + o;
+      bool valid = unique && src[q] >= 0;
+      rhit[q] = valid && res[q] >= 0;
       nhot[q] = valid && !rhit[q];
-      res_blk[q] = (int32_t)res;
+      res_blk[q] = (int32_t)res[q];
     }
   }
   __syncthreads();  // keys are dead from here on; the union becomes the hash
@@ -225,8 +270,7 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
 
   // ---- 4. scan tags: hot hits and protected slots ---------------------------
   int32_t* tags = a.tags + (int64_t)b * a.tags_stride;
-  for (int s = tid; s < H; s += kResolveThreads) {
-    int32_t t = tags[s];
+  auto scan_tag = [&](int s, int32_t t) {
     if (t >= 0) {
       int h = hash_find(sh.u.hash.hkey, t);
       if (h >= 0) {
@@ -234,7 +278,11 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
         atomicOr(&sh.prot[s >> 5], 1u << (s & 31));
       }
     }
-  }
+  };
+#pragma unroll
+  for (int i = 0; i < kRegH; ++i)
+    if (i * kResolveThreads + tid < H) scan_tag(i * kResolveThreads + tid, tag_r[i]);
+  for (int s = kRegH * kResolveThreads + tid; s < H; s += kResolveThreads) scan_tag(s, tags[s]);
   __syncthreads();
 
   bool hhit[kKPerThread], miss[kKPerThread];
@@ -256,9 +304,14 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
 
   // ---- 5. victims: lru stably partitioned, unprotected slots first ---------
   __syncthreads();  // the hash is dead; the union now stages the lru
-  const int64_t* lru_in = a.lru + (int64_t)b * a.lru_stride;
-  for (int r = tid; r < H; r += kResolveThreads) {
-    int64_t v = lru_in[r];  // a permutation of [0, H); clamped so bad input stays in bounds
+  // the lru is a permutation of [0, H); values are clamped so bad input stays in bounds
+#pragma unroll
+  for (int i = 0; i < kRegH; ++i) {
+    const int r = i * kResolveThreads + tid;
+    if (r < H) sh.u.lru16[r] = (uint16_t)(lru_r[i] < 0 ? 0 : lru_r[i] >= H ? H - 1 : lru_r[i]);
+  }
+  for (int r = kRegH * kResolveThreads + tid; r < H; r += kResolveThreads) {
+    const int64_t v = lru_in[r];
     sh.u.lru16[r] = (uint16_t)(v < 0 ? 0 : v >= H ? H - 1 : v);
   }
   int local_prot = 0;
@@ -295,7 +348,6 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   int64_t* phys_out = a.physical + (int64_t)b * a.plan_stride;
   int64_t* mh = a.miss_host + (int64_t)b * a.plan_stride;
   int64_t* md = a.miss_device + (int64_t)b * a.plan_stride;
-  const int32_t* hot = a.hot + (int64_t)b * a.hot_stride;
   int local_rhit = 0, local_hhit = 0;
   {
     int64_t rank = miss_before;
@@ -317,7 +369,7 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
           s = sh.victims[vr];
         }
         uint32_t sb = a.page_div.div((uint32_t)s);
-        int64_t hp = (int64_t)hot[sb] * P + (int64_t)((uint32_t)s - sb * (uint32_t)P);
+        int64_t hp = (int64_t)(hot_cached ? sh.hot[sb] : hot[sb]) * P + (int64_t)((uint32_t)s - sb * (uint32_t)P);
         phys = hp;
         if (miss[q]) {
           mh[rank] = host[q];
