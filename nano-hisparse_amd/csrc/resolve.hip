@@ -31,6 +31,8 @@ constexpr int kKPerThread = kMaxK / kResolveThreads;  // 4
 constexpr int kHashCap = 2 * kMaxK;                // load factor <= 1/2
 constexpr int kRegH = 8;        // hot rows per thread whose tag and lru are loaded at entry (H <= 8192)
 constexpr int kHotCache = 1024; // hot blocks staged in LDS at entry
+constexpr int kWaves = kResolveThreads / 64;
+constexpr int kRankGroup = 4;   // 1024-slot chunks ranked per barrier
 
 struct ResolveArgs {
   int n;  // positions per item
@@ -72,42 +74,102 @@ struct ResolveShared {
   uint32_t prot[kMaxH / 32];  // protected slot bits
   uint32_t ins[kMaxH / 32];   // inserted slot bits
   int32_t victims[kMaxK];     // victims[0 .. min(n, H)-1]
-  int64_t scan64[kResolveThreads / 64 + 1];
-  int32_t wcount[2][kResolveThreads / 64][4];  // per-wave category counts, double-buffered
+  int32_t red[3][kWaves * 8];                    // one scratch row per block reduction
+  int32_t wcount[2][kRankGroup][kWaves][4];      // per-wave category counts, double-buffered
   int32_t hot[kHotCache];                      // the item's hot block table, when it fits
 };
 
-// Ranks within one 1024-slot chunk: for category `cat` (0..3, or -1 for an
-// empty slot) returns the number of lower threads of the block with the same
-// category and writes the chunk's per-category totals to tot[4]. One barrier;
-// the count table alternates between two buffers, so a buffer is rewritten
-// only after every thread has passed the next chunk's barrier. After the
-// barrier lane w * 4 + c of every wave holds wave w's count of category c,
-// and a shuffle scan with stride 4 gives every wave the prefix over waves.
-static_assert(kResolveThreads / 64 * 4 == 64, "one lane per (wave, category)");
-__device__ __forceinline__ int chunk_rank(int cat, int32_t (*wcount)[kResolveThreads / 64][4], int parity,
-                                          int* tot) {
+// Block reductions with one barrier each. Every call site passes its own
+// scratch row, so no barrier is needed before the scratch is reused.
+
+// Sums of N ints over the block; every thread receives the sums.
+template <int N>
+__device__ __forceinline__ void block_sums(int (&v)[N], int32_t* scratch) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t lt = (1ull << lane) - 1ull;
-  int mine = 0;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    uint64_t m = __ballot(cat == c);
-    if (cat == c) mine = __popcll(m & lt);
-    if (lane == 0) wcount[parity][wave][c] = __popcll(m);
-  }
+  for (int d = 1; d < 64; d <<= 1)
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], d);
+  if (lane == 0)
+#pragma unroll
+    for (int i = 0; i < N; ++i) scratch[wave * N + i] = v[i];
   __syncthreads();
-  const int v = (&wcount[parity][0][0])[lane];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) t += scratch[w * N + i];
+    v[i] = t;
+  }
+}
+
+// Exclusive prefix sum over the block in thread order; *total gets the sum.
+__device__ __forceinline__ int block_scan(int v, int32_t* scratch, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int incl = v;
 #pragma unroll
-  for (int d = 4; d < 64; d <<= 1) {
+  for (int d = 1; d < 64; d <<= 1) {
     const int o = __shfl_up(incl, d);
     if (lane >= d) incl += o;
   }
-  const int before = __shfl(incl - v, wave * 4 + (cat < 0 ? 0 : cat));
+  if (lane == 63) scratch[wave] = incl;
+  __syncthreads();
+  int before = 0, t = 0;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) tot[c] = __shfl(incl, 60 + c);
-  return before + mine;
+  for (int w = 0; w < kWaves; ++w) {
+    const int x = scratch[w];
+    t += x;
+    before += w < wave ? x : 0;
+  }
+  *total = t;
+  return before + incl - v;
+}
+
+// Ranks within up to kRankGroup 1024-slot chunks at once: for the category
+// cat[c] (0..3, or -1 for an empty slot) of this thread's slot in chunk c,
+// within[c] = number of lower threads of the block with the same category in
+// that chunk, and tot[c][k] = chunk c's count of category k. One barrier;
+// the count table alternates between two buffers, so a buffer is rewritten
+// only after every thread has passed the next group's barrier. After the
+// barrier lane w * 4 + k of every wave holds wave w's count of category k,
+// and a shuffle scan with stride 4 gives the prefix over waves.
+static_assert(kWaves * 4 == 64, "one lane per (wave, category)");
+__device__ __forceinline__ void rank_group(const int (&cat)[kRankGroup], int chunks,
+                                           int32_t (*wcount)[kWaves][4], int (&within)[kRankGroup],
+                                           int (&tot)[kRankGroup][4]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  int mine[kRankGroup];
+#pragma unroll
+  for (int c = 0; c < kRankGroup; ++c) {
+    mine[c] = 0;
+    if (c < chunks)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint64_t m = __ballot(cat[c] == k);
+        if (cat[c] == k) mine[c] = __popcll(m & lt);
+        if (lane == 0) wcount[c][wave][k] = __popcll(m);
+      }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < kRankGroup; ++c) {
+    within[c] = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) tot[c][k] = 0;
+    if (c < chunks) {
+      const int v = (&wcount[c][0][0])[lane];
+      int incl = v;
+#pragma unroll
+      for (int d = 4; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+      }
+      within[c] = __shfl(incl - v, wave * 4 + (cat[c] < 0 ? 0 : cat[c])) + mine[c];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) tot[c][k] = __shfl(incl, 60 + k);
+    }
+  }
 }
 
 __device__ __forceinline__ uint32_t hash_row(int32_t key) { return (uint32_t)key * 2654435761u; }
@@ -314,35 +376,42 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     const int64_t v = lru_in[r];
     sh.u.lru16[r] = (uint16_t)(v < 0 ? 0 : v >= H ? H - 1 : v);
   }
-  int local_prot = 0;
-  for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) local_prot += __popc(sh.prot[i]);
-  const int64_t n_prot = block_sum<int64_t>(local_prot, sh.scan64);  // barrier: lru16 staged
-  const int64_t n_unprot = H - n_prot;
+  int n_prot_v[1] = {0};
+  for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) n_prot_v[0] += __popc(sh.prot[i]);
+  block_sums<1>(n_prot_v, sh.red[0]);  // barrier: lru16 staged
+  const int n_unprot = H - n_prot_v[0];
   const int vlimit = n < H ? n : H;
   auto prot_bit = [&](int v) { return (int)((sh.prot[v >> 5] >> (v & 31)) & 1u); };
   auto ins_bit = [&](int v) { return (int)((sh.ins[v >> 5] >> (v & 31)) & 1u); };
+  const int n_chunks = (H + kResolveThreads - 1) / kResolveThreads;
   {
-    int64_t base_u = 0, base_p = 0;
-    int parity = 0;
-    for (int c0 = 0; c0 < H; c0 += kResolveThreads, parity ^= 1) {
-      const int r = c0 + tid;
-      int v = r < H ? sh.u.lru16[r] : 0;
-      int cat = r < H ? prot_bit(v) : -1;  // 0 unprotected, 1 protected
-      int tot[4];
-      int within = chunk_rank(cat, sh.wcount, parity, tot);
-      if (cat >= 0) {
-        int64_t rank = cat == 0 ? base_u + within : n_unprot + base_p + within;
-        if (rank < vlimit) sh.victims[rank] = v;
+    int base_u = 0, base_p = 0, parity = 0;
+    for (int g0 = 0; g0 < n_chunks; g0 += kRankGroup, parity ^= 1) {
+      const int chunks = min(kRankGroup, n_chunks - g0);
+      int cat[kRankGroup], vv[kRankGroup], within[kRankGroup], tot[kRankGroup][4];
+#pragma unroll
+      for (int c = 0; c < kRankGroup; ++c) {
+        const int r = (g0 + c) * kResolveThreads + tid;
+        vv[c] = r < H ? sh.u.lru16[r] : 0;
+        cat[c] = r < H ? prot_bit(vv[c]) : -1;  // 0 unprotected, 1 protected
       }
-      base_u += tot[0];
-      base_p += tot[1];
+      rank_group(cat, chunks, sh.wcount[parity], within, tot);
+#pragma unroll
+      for (int c = 0; c < kRankGroup; ++c) {
+        if (c < chunks && cat[c] >= 0) {
+          const int rank = cat[c] == 0 ? base_u + within[c] : n_unprot + base_p + within[c];
+          if (rank < vlimit) sh.victims[rank] = vv[c];
+        }
+        base_u += tot[c][0];
+        base_p += tot[c][1];
+      }
     }
   }
   __syncthreads();  // victims complete
 
   // ---- 6. miss ranks ----------------------------------------------------------
-  int64_t n_miss;
-  int64_t miss_before = block_exclusive_scan<int64_t>(local_miss, sh.scan64, &n_miss);
+  int n_miss;
+  const int miss_before = block_scan(local_miss, sh.red[1], &n_miss);
 
   // ---- 7. physical rows, plan, tag writes, counts ----------------------------
   int64_t* phys_out = a.physical + (int64_t)b * a.plan_stride;
@@ -387,60 +456,62 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
       mh[i] = -1;
       md[i] = -1;
     }
-  int64_t n_rhit = block_sum<int64_t>(local_rhit, sh.scan64);
-  int64_t n_hhit = block_sum<int64_t>(local_hhit, sh.scan64);
-  if (tid == 0) {
-    int64_t* c = a.counts + (int64_t)b * 3;
-    c[0] = n_rhit;
-    c[1] = n_hhit;
-    c[2] = n_miss;
-    if (a.counts_total) {
-      atomicAdd((unsigned long long*)&a.counts_total[0], (unsigned long long)n_rhit);
-      atomicAdd((unsigned long long*)&a.counts_total[1], (unsigned long long)n_hhit);
-      atomicAdd((unsigned long long*)&a.counts_total[2], (unsigned long long)n_miss);
-    }
-  }
   __syncthreads();  // ins bits complete
 
   // ---- 8. lru stably partitioned by category ----------------------------------
   // category = inserted + 2 * protected: 0 untouched, 1 inserted, 2 hit.
-  int local_cnt[4] = {0, 0, 0, 0};
+  // one reduction: slots inserted only, protected only, both; resident and hot hits
+  int sums[5] = {0, 0, 0, local_rhit, local_hhit};
   for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) {
     uint32_t in = sh.ins[i], pr = sh.prot[i];
     uint32_t valid_bits = (i == (H - 1) / 32 && (H & 31)) ? ((1u << (H & 31)) - 1u) : 0xffffffffu;
-    local_cnt[1] += __popc(in & ~pr & valid_bits);
-    local_cnt[2] += __popc(pr & ~in & valid_bits);
-    local_cnt[3] += __popc(in & pr & valid_bits);
+    sums[0] += __popc(in & ~pr & valid_bits);
+    sums[1] += __popc(pr & ~in & valid_bits);
+    sums[2] += __popc(in & pr & valid_bits);
   }
-  int64_t start[4];
-  start[1] = block_sum<int64_t>(local_cnt[1], sh.scan64);
-  start[2] = block_sum<int64_t>(local_cnt[2], sh.scan64);
-  start[3] = block_sum<int64_t>(local_cnt[3], sh.scan64);
+  block_sums<5>(sums, sh.red[2]);
+  if (tid == 0) {
+    int64_t* c = a.counts + (int64_t)b * 3;
+    c[0] = sums[3];
+    c[1] = sums[4];
+    c[2] = n_miss;
+    if (a.counts_total) {
+      atomicAdd((unsigned long long*)&a.counts_total[0], (unsigned long long)sums[3]);
+      atomicAdd((unsigned long long*)&a.counts_total[1], (unsigned long long)sums[4]);
+      atomicAdd((unsigned long long*)&a.counts_total[2], (unsigned long long)n_miss);
+    }
+  }
   // start[c] = number of slots in lower categories
-  start[0] = 0;
+  int start[4];
   {
-    int64_t n1 = start[1], n2 = start[2], n3 = start[3];
-    int64_t n0 = H - n1 - n2 - n3;
+    const int n1 = sums[0], n2 = sums[1], n0 = H - sums[0] - sums[1] - sums[2];
+    start[0] = 0;
     start[1] = n0;
     start[2] = n0 + n1;
     start[3] = n0 + n1 + n2;
-    (void)n3;
   }
   int64_t* lru_out = a.lru + (int64_t)b * a.lru_stride;
   {
     int parity = 0;
-    for (int c0 = 0; c0 < H; c0 += kResolveThreads, parity ^= 1) {
-      const int r = c0 + tid;
-      int v = r < H ? sh.u.lru16[r] : 0;
-      int cat = r < H ? ins_bit(v) + 2 * prot_bit(v) : -1;
-      int tot[4];
-      int within = chunk_rank(cat, sh.wcount, parity, tot);
-      if (cat >= 0) {
-        int64_t pos = start[cat] + within;
-        if (pos < H) lru_out[pos] = v;
-      }
+    for (int g0 = 0; g0 < n_chunks; g0 += kRankGroup, parity ^= 1) {
+      const int chunks = min(kRankGroup, n_chunks - g0);
+      int cat[kRankGroup], vv[kRankGroup], within[kRankGroup], tot[kRankGroup][4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) start[c] += tot[c];
+      for (int c = 0; c < kRankGroup; ++c) {
+        const int r = (g0 + c) * kResolveThreads + tid;
+        vv[c] = r < H ? sh.u.lru16[r] : 0;
+        cat[c] = r < H ? ins_bit(vv[c]) + 2 * prot_bit(vv[c]) : -1;
+      }
+      rank_group(cat, chunks, sh.wcount[parity], within, tot);
+#pragma unroll
+      for (int c = 0; c < kRankGroup; ++c) {
+        if (c < chunks && cat[c] >= 0) {
+          const int pos = start[cat[c]] + within[c];
+          if (pos < H) lru_out[pos] = vv[c];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) start[k] += tot[c][k];
+      }
     }
   }
 }
