@@ -1,0 +1,172 @@
+"""Full-size decode workloads on the GPU against the C oracle.
+
+- Resolver stress: 64 requests with Qwen2-7B heads (28 query / 4 KV heads x
+  128, bf16), contexts uniform in [4096, 65536], pages of 32, a 1024-row
+  budget (32 pages), 2048 hot rows per request all occupied, 16 decode steps
+  with fresh queries: selected pages, row addresses, miss plans, tags and
+  LRU order bit-exact at every step.
+- Miss-heavy long context: 4 requests of 131072 tokens (2048 pages of 64),
+  Llama-3-8B heads, a 4096-row budget (64 pages) of which only the two tail
+  pages are resident and 4 are in the hot buffer, so ~90% of the rows are
+  gathered from pinned host memory; K/V are N(0, 1) plus a per-page offset
+  N(0, 0.5) so Quest scores are spread out. Selection, rows and gathered
+  bytes bit-exact; attention within 2e-2.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from nano_hisparse import row_kernels as rk
+
+
+def log_case(**kw):
+    print("case:", kw, flush=True)
+
+
+@pytest.mark.gpu
+def test_resolver_stress_64_requests_16_steps(gpu):
+    log_case(test="resolver-stress", B=64, steps=16)
+    B, Hq, Hkv, D, P, K, H = 64, 28, 4, 128, 32, 1024, 2048
+    top = K // P
+    g = torch.Generator(device=gpu).manual_seed(42)
+    rng = np.random.default_rng(42)
+    lengths = rng.integers(4096, 65536 + 1, size=B)
+    n_pages = int(-(-lengths.max() // P))
+    counts = -(-lengths // P)
+    # per-page key bounds of random N(0,1) keys (bf16, exact min/max of 32 rows)
+    minimum = torch.empty(B, n_pages, Hkv, D, dtype=torch.bfloat16, device=gpu)
+    maximum = torch.empty_like(minimum)
+    for b in range(B):
+        keys = torch.randn(n_pages, P, Hkv, D, generator=g, device=gpu).to(torch.bfloat16)
+        minimum[b], maximum[b] = keys.amin(1), keys.amax(1)
+    # host pages, resident pages (30% of each history) and a fully occupied hot buffer
+    hot_blocks = H // P
+    source = np.full((B, n_pages), -1, np.int32)
+    resident = np.full((B, n_pages), -1, np.int32)
+    hot = np.zeros((B, hot_blocks), np.int32)
+    tags = np.full((B, H), -1, np.int32)
+    lru = np.zeros((B, H), np.int64)
+    next_host, next_block = 0, 0
+    for b in range(B):
+        c = int(counts[b])
+        source[b, :c] = np.arange(next_host, next_host + c)
+        next_host += c
+        hot[b] = np.arange(next_block, next_block + hot_blocks)
+        next_block += hot_blocks
+        res = rng.permutation(c)[: (3 * c) // 10]
+        resident[b, res] = np.arange(next_block, next_block + res.size)
+        next_block += res.size
+        nonres = np.flatnonzero(resident[b, :c] < 0)
+        cand = (source[b, nonres][:, None].astype(np.int64) * P + np.arange(P)).ravel()
+        tags[b] = rng.choice(cand, size=H, replace=False)  # 100% occupancy
+        lru[b] = rng.permutation(H)
+    g_len = torch.from_numpy(lengths).to(gpu)
+    g_src, g_res, g_hot = (torch.from_numpy(x).to(gpu) for x in (source, resident, hot))
+    g_tags, g_lru = torch.from_numpy(tags).to(gpu), torch.from_numpy(lru).to(gpu)
+    o_tags, o_lru = tags.astype(np.int64), lru.copy()
+    c_min, c_max = minimum.cpu(), maximum.cpu()
+    replaced = 0
+    for step in range(16):
+        q = torch.randn(B, Hq, D, generator=g, device=gpu).to(torch.bfloat16)
+        pages, positions, _ = rk.quest_batched(q, minimum, maximum, g_len, P, top)
+        if step < 2:  # the CPU Quest oracle over all 64 requests takes seconds
+            _, e_pages, e_pos = oracle.quest_select(q.cpu(), c_min, c_max, lengths, P, top)
+            assert torch.equal(pages.cpu(), e_pages), f"step {step}: pages"
+            assert torch.equal(positions.cpu(), e_pos), f"step {step}: positions"
+        phys, mh, md, cnt = rk.resolve_batched(positions, g_src, g_res, g_hot, g_tags, g_lru, g_len, P)
+        pos_np = positions.cpu().numpy()
+        phys, mh, md, cnt = (t.cpu().numpy() for t in (phys, mh, md, cnt))
+        for b in range(B):
+            e_phys, e_mh, e_md, e_cnt = oracle.resolve_rows(
+                pos_np[b], source[b], resident[b], hot[b], o_tags[b], o_lru[b], lengths[b], P
+            )
+            np.testing.assert_array_equal(phys[b], e_phys, err_msg=f"step {step} request {b}: rows")
+            np.testing.assert_array_equal(mh[b], e_mh)
+            np.testing.assert_array_equal(md[b], e_md)
+            np.testing.assert_array_equal(cnt[b], e_cnt)
+            replaced += int(e_cnt[2])
+        np.testing.assert_array_equal(g_tags.cpu().numpy(), o_tags, err_msg=f"step {step}: tags")
+        np.testing.assert_array_equal(g_lru.cpu().numpy(), o_lru, err_msg=f"step {step}: lru")
+    assert replaced > 0  # every step evicts from a full hot buffer
+
+
+@pytest.mark.gpu
+def test_miss_heavy_long_context(gpu):
+    log_case(test="miss-heavy", B=4, context=131072)
+    from nano_hisparse.batch_step import BatchTables, SparseDecodeBatch
+
+    B, Hq, Hkv, D, P, ctx, top, H = 4, 32, 8, 128, 64, 131072, 64, 8192
+    n_pages, K = ctx // P, top * P
+    dtype = torch.bfloat16
+    g = torch.Generator(device=gpu).manual_seed(43)
+    host = torch.empty(B * n_pages, 2, P, Hkv, D, dtype=dtype, pin_memory=True)
+    mn = torch.empty(B * n_pages, Hkv, D, dtype=dtype, device=gpu)
+    mx = torch.empty_like(mn)
+    chunk = 512
+    for s in range(0, B * n_pages, chunk):
+        kv = torch.randn(chunk, 2, P, Hkv, D, generator=g, device=gpu)
+        kv += 0.5 * torch.randn(chunk, 1, 1, 1, 1, generator=g, device=gpu)  # per-page offset
+        kv = kv.to(dtype)
+        host[s : s + chunk].copy_(kv)
+        mn[s : s + chunk] = kv[:, 0].amin(1)
+        mx[s : s + chunk] = kv[:, 0].amax(1)
+    minimum, maximum = mn.view(B, n_pages, Hkv, D), mx.view(B, n_pages, Hkv, D)
+    q = torch.randn(B, Hq, D, generator=g, device=gpu).to(dtype)
+    lengths = torch.full((B,), ctx, dtype=torch.int64, device=gpu)
+    pages, _, _ = rk.quest_batched(q, minimum, maximum, lengths, P, top)
+    pages = pages.cpu()
+    # residency over the selected pages: the two tail pages resident, 4 pages
+    # in the hot buffer, the other 58 only in host memory
+    hot_blocks = H // P
+    blocks_per = hot_blocks + 2
+    pool = torch.zeros(B * blocks_per, 2, P, Hkv, D, dtype=dtype, device=gpu)
+    source = torch.arange(B * n_pages, dtype=torch.int32).view(B, n_pages)
+    resident = torch.full((B, n_pages), -1, dtype=torch.int32)
+    hot = torch.empty(B, hot_blocks, dtype=torch.int32)
+    tags = torch.full((B, H), -1, dtype=torch.int32)
+    rng = np.random.default_rng(7)
+    for b in range(B):
+        sel = pages[b].tolist()
+        base = b * blocks_per
+        hot[b] = torch.arange(base, base + hot_blocks, dtype=torch.int32)
+        for i, p in enumerate((n_pages - 2, n_pages - 1)):
+            resident[b, p] = base + hot_blocks + i
+            pool[base + hot_blocks + i] = host[b * n_pages + p].to(gpu)
+        others = [p for p in sel if p < n_pages - 2]
+        hot_pages = rng.choice(others, size=4, replace=False)
+        slots = rng.permutation(H)[: 4 * P]
+        rows = torch.tensor([(b * n_pages + int(p)) * P + o for p in hot_pages for o in range(P)], dtype=torch.int32)
+        tags[b, torch.from_numpy(slots)] = rows
+        for s_, r in zip(slots.tolist(), rows.tolist()):
+            hb, ho = divmod(r, P)
+            pool[int(hot[b, s_ // P]), :, s_ % P] = host[hb, :, ho].to(gpu)
+    lru = torch.stack([torch.from_numpy(rng.permutation(H)) for _ in range(B)])
+    tables = BatchTables(source, resident, hot, tags, lru, minimum.cpu(), maximum.cpu(), lengths.cpu())
+    dev = BatchTables(source.to(gpu), resident.to(gpu), hot.to(gpu), tags.to(gpu), lru.to(gpu), minimum, maximum,
+                      lengths)
+    cpool = pool.cpu()
+    step = SparseDecodeBatch(pool, host, dev, P, top)
+    out, result = step.step(q)
+    torch.cuda.synchronize()
+    # the oracle, request by request
+    _, e_pages, e_pos = oracle.quest_select(q.cpu(), tables.minimum, tables.maximum, tables.lengths, P, top)
+    assert torch.equal(result.positions.cpu(), e_pos)
+    o_tags, o_lru = tags.numpy().astype(np.int64), lru.numpy().copy()
+    e_phys = np.empty((B, K), np.int64)
+    misses = 0
+    for b in range(B):
+        ph, mh_, md_, cnt = oracle.resolve_rows(
+            e_pos[b].numpy(), source[b].numpy(), resident[b].numpy(), hot[b].numpy(), o_tags[b], o_lru[b], ctx, P
+        )
+        oracle.gather_rows(host, cpool, mh_, md_, P)
+        e_phys[b] = ph
+        misses += int(cnt[2])
+    assert misses >= int(0.85 * B * K)  # ~90% of the selected rows come from host memory
+    np.testing.assert_array_equal(result.physical.cpu().numpy(), e_phys)
+    np.testing.assert_array_equal(dev.tags.cpu().numpy(), o_tags)
+    np.testing.assert_array_equal(dev.lru.cpu().numpy(), o_lru)
+    assert torch.equal(pool.cpu().view(torch.uint8), cpool.view(torch.uint8))
+    e_out = oracle.attend_rows(q.cpu(), cpool, torch.from_numpy(e_phys), P)
+    assert (out.float().cpu() - e_out).abs().max().item() <= 2e-2
