@@ -85,7 +85,7 @@ int nhs_gather_rows(const void* host_alias, void* pool,
 
 /*
  * Physical-row GQA decode attention, split-K over rows with an online
- * softmax and a combine pass. For request b and query head h (kv head
+ * softmax. For request b and query head h (kv head
  * h / (q_heads / kv_heads)):
  *   out[b,h] = softmax_r(q[b,h] . K[row] * head_dim^-0.5) . V[row]
  * over the rows rows[b, h, c] >= 0 (c < n_rows); rows < 0 are masked and a
@@ -141,10 +141,13 @@ int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t po
  * Quest page selection for `batch` requests. Request b scores each of its
  * count = ceil(lengths[b]/page_size) pages (count is clamped to max_pages):
  *   score[p] = (sum_h sum_d max(q[h,d]*min[p,h/g,d], q[h,d]*max[p,h/g,d])) / q_heads
- * in fp32 with a fixed summation order (per lane: from 0.0, sequential over
- * its 16 bytes of bound elements, each term added as
- * fma(min(q,0), min, fma(max(q,0), max, t)); across lanes: pairwise tree;
- * across heads: sequential h = 0..q_heads-1). q_heads/kv_heads <= 8.
+ * in fp32 with a fixed summation order: a bound row is cut into chunks of
+ * 32 bytes when it is a multiple of 32 bytes of at most 64 chunks, else of
+ * 16 bytes when a multiple of 16 bytes, else of one element; each chunk is
+ * summed from 0.0 in element order with t = fma(q, q > 0 ? max : min, t);
+ * chunk sums (padded with +0.0 to a power of two) are added as a pairwise
+ * tree; head sums are added sequentially h = 0..q_heads-1.
+ * q_heads/kv_heads <= 8.
  * Page count-1, and page 0 when keep_sink and
  * top_pages > 1 and count > 1, score +inf. The top_pages pages by (score
  * descending, page ascending) are written ascending to pages[b, :top_pages]
@@ -174,6 +177,24 @@ int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q
                     int32_t q_heads, int32_t kv_heads, int32_t head_dim, const int64_t* lengths,
                     int64_t length, int32_t page_size, int32_t max_pages, int32_t top_pages,
                     float* scores, int32_t* pages, int32_t* positions, void* stream);
+
+/*
+ * Decode-time append into one page (replaces HostStore.append's block
+ * write, _update_bounds and _mirror, nano_hisparse/storage.py:258-331):
+ * rows [within, within + count) of pool block `block` (layout
+ * [2, page_size, row_elems], row_elems = kv_heads * head_dim) receive
+ * k[t * token_stride ...] and v[t * token_stride ...] for t < count. The
+ * page's minimum/maximum [row_elems] (KV dtype) fold in the new keys
+ * exactly (NaN propagates), and summary [row_elems] (fp32) becomes the mean
+ * of keys [0, within + count), summed in double in row order and rounded
+ * once. With a non-null host_alias (from nhs_host_device_ptr) the new rows
+ * are also written to host block `host_page`, so the host mirror is
+ * complete when the kernel is.
+ */
+int nhs_append_page(const void* k, const void* v, int64_t token_stride, int32_t kv_dtype, int32_t row_elems,
+                    int32_t page_size, void* pool, int64_t block, int32_t within, int32_t count,
+                    void* host_alias, int64_t host_page, float* summary, void* minimum, void* maximum,
+                    void* stream);
 
 /*
  * Legacy per-head selections: out[h, c] = columns[h, c] in [0, n) ?

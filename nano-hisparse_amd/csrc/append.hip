@@ -1,0 +1,105 @@
+// Decode-time append into one pool page, fused: the new K/V rows are
+// written to the page's pool block and (through the pinned host alias) to
+// its host block, the page's running per-element key minimum / maximum fold
+// in the new keys, and its fp32 mean key is recomputed over every valid row.
+// One thread owns one element of a row (kv_heads * head_dim elements), so
+// every access of a wave is contiguous.
+//
+// The mean is summed in double in row order and rounded to fp32 once (the
+// oracle sums in the same order). Min/max propagate NaN like torch.minimum
+// / torch.maximum.
+#include "nhs_common.h"
+
+namespace nhs {
+
+constexpr int kAppendThreads = 256;
+
+struct AppendArgs {
+  const void* k;
+  const void* v;
+  int64_t token_stride;  // elements between consecutive tokens of k and v
+  int dtype;
+  int row_elems;
+  int64_t plane_elems;   // page_size * row_elems
+  char* pool_block;      // the page's pool block [2, P, row_elems]
+  char* host_block;      // its host block, or null
+  int within, count;
+  float* summary;
+  void* minimum;
+  void* maximum;
+};
+
+__device__ __forceinline__ float nan_min(float a, float b) { return (a != a || b != b) ? a + b : (b < a ? b : a); }
+__device__ __forceinline__ float nan_max(float a, float b) { return (a != a || b != b) ? a + b : (b > a ? b : a); }
+
+__global__ __launch_bounds__(kAppendThreads) void append_page_kernel(AppendArgs a) {
+  const int e = blockIdx.x * kAppendThreads + threadIdx.x;
+  if (e >= a.row_elems) return;
+  const int esize = a.dtype == NHS_F32 ? 4 : 2;
+  float lo = load_elem(a.minimum, a.dtype, e);
+  float hi = load_elem(a.maximum, a.dtype, e);
+  double sum = 0.0;
+  for (int r = 0; r < a.within; ++r) sum += (double)load_elem(a.pool_block, a.dtype, (int64_t)r * a.row_elems + e);
+  for (int t = 0; t < a.count; ++t) {
+    const int64_t src = (int64_t)t * a.token_stride + e;
+    const int64_t row = (int64_t)(a.within + t) * a.row_elems + e;
+    // copy the raw element bits: no conversion touches the stored values
+    if (esize == 4) {
+      const uint32_t kb = static_cast<const uint32_t*>(a.k)[src], vb = static_cast<const uint32_t*>(a.v)[src];
+      reinterpret_cast<uint32_t*>(a.pool_block)[row] = kb;
+      reinterpret_cast<uint32_t*>(a.pool_block)[a.plane_elems + row] = vb;
+      if (a.host_block) {
+        reinterpret_cast<uint32_t*>(a.host_block)[row] = kb;
+        reinterpret_cast<uint32_t*>(a.host_block)[a.plane_elems + row] = vb;
+      }
+    } else {
+      const uint16_t kb = static_cast<const uint16_t*>(a.k)[src], vb = static_cast<const uint16_t*>(a.v)[src];
+      reinterpret_cast<uint16_t*>(a.pool_block)[row] = kb;
+      reinterpret_cast<uint16_t*>(a.pool_block)[a.plane_elems + row] = vb;
+      if (a.host_block) {
+        reinterpret_cast<uint16_t*>(a.host_block)[row] = kb;
+        reinterpret_cast<uint16_t*>(a.host_block)[a.plane_elems + row] = vb;
+      }
+    }
+    const float key = load_elem(a.k, a.dtype, src);
+    lo = nan_min(lo, key);
+    hi = nan_max(hi, key);
+    sum += (double)key;
+  }
+  store_elem(a.minimum, a.dtype, e, lo);
+  store_elem(a.maximum, a.dtype, e, hi);
+  a.summary[e] = (float)(sum / (double)(a.within + a.count));
+}
+
+}  // namespace nhs
+
+extern "C" int nhs_append_page(const void* k, const void* v, int64_t token_stride, int32_t kv_dtype,
+                               int32_t row_elems, int32_t page_size, void* pool, int64_t block, int32_t within,
+                               int32_t count, void* host_alias, int64_t host_page, float* summary, void* minimum,
+                               void* maximum, void* stream) {
+  using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
+  if (!k || !v || !pool || !summary || !minimum || !maximum) return fail(NHS_ERR_INVALID, "nhs_append_page: null pointer");
+  if (!valid_dtype(kv_dtype)) return fail(NHS_ERR_INVALID, "nhs_append_page: bad dtype");
+  if (row_elems < 1 || page_size < 1 || block < 0 || within < 0 || count < 1 || within + count > page_size ||
+      token_stride < row_elems || (host_alias && host_page < 0))
+    return fail(NHS_ERR_INVALID, "nhs_append_page: invalid page, rows or strides");
+  AppendArgs a;
+  a.k = k;
+  a.v = v;
+  a.token_stride = token_stride;
+  a.dtype = kv_dtype;
+  a.row_elems = row_elems;
+  a.plane_elems = (int64_t)page_size * row_elems;
+  const int64_t block_bytes = 2 * a.plane_elems * elem_size(kv_dtype);
+  a.pool_block = static_cast<char*>(pool) + block * block_bytes;
+  a.host_block = host_alias ? static_cast<char*>(host_alias) + host_page * block_bytes : nullptr;
+  a.within = within;
+  a.count = count;
+  a.summary = summary;
+  a.minimum = minimum;
+  a.maximum = maximum;
+  launch(append_page_kernel, dim3((unsigned)((row_elems + kAppendThreads - 1) / kAppendThreads)),
+         dim3(kAppendThreads), 0, (hipStream_t)stream, ev.start, ev.stop, a);
+  return launch_status("nhs_append_page");
+}

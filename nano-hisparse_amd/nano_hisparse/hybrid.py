@@ -110,11 +110,7 @@ class HybridKVCache:
         self.storage = HostStore(config, self.allocator)
         self.pool, self.device = self.allocator.storage, self.storage.device
         self.row_stats = torch.zeros(3, dtype=torch.int64, device=self.device)
-        self._host_pointer = None
-        if self.storage.cuda:
-            from .row_kernels import MappedHost
-
-            self._host_pointer = MappedHost(self.storage.host)
+        self._host_pointer = self.storage.host_alias
 
     # ---- capacity ---------------------------------------------------------------------
 

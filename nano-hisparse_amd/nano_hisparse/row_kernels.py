@@ -139,6 +139,41 @@ def gather_rows(host, pool, plan, config):
     gather_plan(host, pool, plan.miss_host_rows, plan.miss_device_rows, config.page_size)
 
 
+# ---- append ----------------------------------------------------------------------
+
+
+def append_page(k, v, pool, block, within, host, host_page, summary, minimum, maximum):
+    """Write K/V rows [count, Hkv, D] into rows within.. of pool block `block`
+    and, when `host` (a MappedHost) is given, of host block `host_page`; fold
+    the new keys into the page's minimum/maximum [Hkv, D] and recompute its
+    fp32 summary [Hkv, D] (mean key over every valid row)."""
+    device = _require_gpu("append_page", k, v, pool, summary, minimum, maximum)
+    if k.shape != v.shape or k.ndim != 3 or tuple(k.shape[1:]) != tuple(pool.shape[3:]):
+        raise ValueError("append_page: K/V must be [tokens, kv_heads, head_dim] of the pool")
+    if k.dtype != pool.dtype or v.dtype != pool.dtype or minimum.dtype != pool.dtype or maximum.dtype != pool.dtype:
+        raise ValueError("append_page: K/V and bounds must have the pool dtype")
+    if summary.dtype != torch.float32:
+        raise ValueError("append_page: the summary is float32")
+    for t in (summary, minimum, maximum):
+        if not t.is_contiguous() or t.numel() != pool[0, 0, 0].numel():
+            raise ValueError("append_page: summary and bounds are contiguous [kv_heads, head_dim]")
+    if k.stride(2) != 1 or k.stride(1) != k.shape[2] or k.stride(0) != v.stride(0) or v.stride(2) != 1 \
+            or v.stride(1) != v.shape[2]:
+        raise ValueError("append_page: K/V rows must be contiguous with equal token strides")
+    if not pool.is_contiguous():
+        raise ValueError("append_page: the pool must be contiguous")
+    count, row_elems, P = k.shape[0], k.shape[1] * k.shape[2], pool.shape[2]
+    if host is not None and host.dtype != pool.dtype:
+        raise ValueError("append_page: host and pool dtypes differ")
+    lib = _hip.load()
+    status = lib.nhs_append_page(
+        _ptr(k), _ptr(v), k.stride(0), dtype_code(pool.dtype), row_elems, P, _ptr(pool), int(block), int(within),
+        count, ctypes.c_void_p(host.data_ptr() if host is not None else 0), int(host_page if host is not None else 0),
+        _ptr(summary), _ptr(minimum), _ptr(maximum), _stream(device),
+    )
+    _hip.check(status, "nhs_append_page")
+
+
 # ---- attention ------------------------------------------------------------------
 
 _workspaces: dict = {}

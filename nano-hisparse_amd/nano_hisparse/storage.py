@@ -41,7 +41,7 @@ class Page:
     pins: int = 0
     ready: object = None  # compute-stream event: device contents written
     last_use: object = None  # compute-stream event: last reader done
-    host_ready: object = None  # transfer-stream event: host mirror written
+    host_ready: object = None  # event after which the host mirror is written (the append kernel's on a GPU)
     content_version: int = 0
     host_enqueued_version: int = 0
     host_committed_version: int = 0
@@ -129,6 +129,11 @@ class HostStore:
             raise RuntimeError("CUDA unavailable; use device='cpu' for the reference path")
         shape = (config.host_pages, 2, config.page_size, config.kv_heads, config.head_dim)
         self.host = torch.empty(shape, dtype=config.dtype, pin_memory=self.cuda)
+        self.host_alias = None
+        if self.cuda:
+            from .row_kernels import MappedHost
+
+            self.host_alias = MappedHost(self.host)
         self.compute = torch.cuda.current_stream(self.device) if self.cuda else None
         self.transfer = torch.cuda.Stream(device=self.device) if self.cuda else None
         self.pages: dict = {}
@@ -288,16 +293,29 @@ class HostStore:
                 lease.wait()
             for ev in (page.ready, page.last_use, page.host_ready):
                 self.wait(self.compute, ev)  # earlier readers and mirrors of this page
-            block = self.pool[page.slot]
-            block[0, within : within + count].copy_(k[done : done + count])
-            block[1, within : within + count].copy_(v[done : done + count])
             page.valid_tokens = within + count
             page.content_version += 1
             page.sealed = page.valid_tokens == P
-            self._update_bounds(request, layer, index, block, within, count)
-            page.ready = self.event(self.compute)
             page.location = Location.RESIDENT
-            self._mirror(page, block, within, count)
+            if self.cuda:
+                # one kernel: pool rows, host mirror rows, bounds and summary
+                from .row_kernels import append_page
+
+                append_page(
+                    k[done : done + count].contiguous(), v[done : done + count].contiguous(), self.pool, page.slot,
+                    within, self.host_alias, page.host_slot, request.summaries[layer, index],
+                    request.minimum[layer, index], request.maximum[layer, index],
+                )
+                page.ready = self.event(self.compute)
+                page.host_ready = page.ready
+                page.host_enqueued_version = page.content_version
+            else:
+                block = self.pool[page.slot]
+                block[0, within : within + count].copy_(k[done : done + count])
+                block[1, within : within + count].copy_(v[done : done + count])
+                self._update_bounds(request, layer, index, block, within, count)
+                page.ready = self.event(self.compute)
+                self._mirror(page, block, within, count)
             self.stats["d2h_bytes"] += self.page_bytes * count // P
             if lease is not None:
                 lease.release()
@@ -308,7 +326,8 @@ class HostStore:
 
     def _update_bounds(self, request, layer, index, block, within, count):
         """Page mean key (fp32) and running min/max of the new keys
-        (reference storage.py:302-309)."""
+        (reference storage.py:302-309); CPU caches only (a GPU cache does
+        this inside nhs_append_page)."""
         valid = within + count
         request.summaries[layer, index].copy_(block[0, :valid].float().mean(0))
         new_keys = block[0, within:valid].float()
@@ -317,7 +336,8 @@ class HostStore:
         hi.copy_(torch.maximum(hi, new_keys.amax(0)))
 
     def _mirror(self, page, block, within, count):
-        """Copy the new rows to the page's host block on the transfer stream."""
+        """Copy the new rows to the page's host block (CPU caches; a GPU
+        cache writes them inside nhs_append_page)."""
         self.wait(self.transfer, page.ready)
         with self.context(self.transfer):
             if within == 0 and count == self.config.page_size:

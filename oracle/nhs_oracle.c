@@ -506,8 +506,11 @@ void oracle_append_bounds(const void* page_keys, int kv_dtype, int within, int c
     summary[e] = (float)(s / valid);
     for (int t = within; t < valid; ++t) {
       float k = load_elem(page_keys, kv_dtype, (int64_t)t * row_elems + e);
-      if (k < minimum[e]) minimum[e] = k;
-      if (k > maximum[e]) maximum[e] = k;
+      /* torch.minimum / torch.maximum: NaN from either side propagates */
+      if (k != k || minimum[e] != minimum[e]) minimum[e] = k + minimum[e];
+      else if (k < minimum[e]) minimum[e] = k;
+      if (k != k || maximum[e] != maximum[e]) maximum[e] = k + maximum[e];
+      else if (k > maximum[e]) maximum[e] = k;
     }
   }
 }

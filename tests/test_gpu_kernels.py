@@ -315,3 +315,49 @@ def test_mean_select_bit_exact(gpu, B, Hq, Hkv, D, P, n_pages, top):
     pages, pos, scores = rk.mean_batched(q.to(gpu), summ.to(gpu), lengths.to(gpu), P, top)
     assert torch.equal(pages.cpu(), e_pages)
     assert torch.equal(pos.cpu(), e_pos)
+
+
+# ---- append ---------------------------------------------------------------------------
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,P,Hkv,D", [(torch.bfloat16, 64, 8, 128), (torch.float16, 16, 2, 24),
+                                           (torch.float32, 7, 1, 8)])
+def test_append_page_matches_oracle(gpu, dtype, P, Hkv, D):
+    log_case(test="append", dtype=str(dtype), P=P, Hkv=Hkv, D=D)
+    g = torch.Generator().manual_seed(P * 100 + D)
+    blocks, host_pages = 3, 5
+    pool = torch.randn(blocks, 2, P, Hkv, D, generator=g).to(dtype)
+    host = torch.empty(host_pages, 2, P, Hkv, D, dtype=dtype, pin_memory=True)
+    host.copy_(torch.randn(host.shape, generator=g).to(dtype))
+    host_before = host.clone()
+    dpool = pool.to(gpu)
+    alias = rk.MappedHost(host)
+    block, host_page = 1, 3
+    summary = torch.zeros(Hkv, D, device=gpu)
+    lo = torch.full((Hkv, D), float("inf"), device=gpu).to(dtype)
+    hi = torch.full((Hkv, D), float("-inf"), device=gpu).to(dtype)
+    e_summary = torch.zeros(Hkv, D)
+    e_lo = torch.full((Hkv, D), float("inf"))
+    e_hi = torch.full((Hkv, D), float("-inf"))
+    keys = torch.randn(P, Hkv, D, generator=g).to(dtype)
+    vals = torch.randn(P, Hkv, D, generator=g).to(dtype)
+    within = 0
+    for count in (1, 2, P // 3 or 1, 1, P):  # appends until the page is full
+        count = min(count, P - within)
+        if count == 0:
+            break
+        rk.append_page(keys[within : within + count].to(gpu), vals[within : within + count].to(gpu), dpool, block,
+                       within, alias, host_page, summary, lo, hi)
+        oracle.append_bounds(keys, within, count, e_summary, e_lo, e_hi)
+        pool[block, 0, within : within + count] = keys[within : within + count]
+        pool[block, 1, within : within + count] = vals[within : within + count]
+        within += count
+        torch.cuda.synchronize()
+        assert torch.equal(dpool.cpu().view(torch.uint8), pool.view(torch.uint8))
+        for plane, src in ((0, keys), (1, vals)):
+            assert torch.equal(host[host_page, plane, :within].view(torch.uint8), src[:within].view(torch.uint8))
+        assert torch.equal(summary.cpu(), e_summary)  # double sum in row order, rounded once
+        assert torch.equal(lo.float().cpu(), e_lo) and torch.equal(hi.float().cpu(), e_hi)
+    others = [i for i in range(host_pages) if i != host_page]
+    assert torch.equal(host[others].view(torch.uint8), host_before[others].view(torch.uint8))

@@ -262,16 +262,23 @@ def test_page_stays_pinned_until_its_mirror_event_completes(gpu):
     cache.reserve("a", 64, 1)
     k = torch.randn(12, 1, 8, device=cache.device)
     v = torch.randn(12, 1, 8, device=cache.device)
-    cache.storage.synchronize()
-    with torch.cuda.stream(cache.storage.transfer):
-        torch.cuda._sleep(100_000_000)
     cache.write("a", 0, k, v)
+    cache.storage.synchronize()
+    # the append kernel writes the host mirror on the compute stream; stand in
+    # for a mirror still in flight with an event held back on a side stream
     page = cache.storage.pages["a", 0, 0]
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        torch.cuda._sleep(100_000_000)
+        pending = torch.cuda.Event()
+        pending.record(side)
+    page.host_ready, page.host_committed_version = pending, 0
+    cache.pending_clean.add(page.key)
     cache.transition_to_host("a", 0)
     assert not page.host_ready.query()
     assert page.slot not in cache.allocator.reclaimable
     assert cache.storage.stats["pressure_mirror_waits"] == 0
-    cache.storage.synchronize()
+    side.synchronize()
     cache.collect()
     assert cache.page_state(page.key)["residency"] == "clean_unpinned"
     cache.assert_invariants()
