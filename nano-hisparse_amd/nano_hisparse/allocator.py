@@ -7,10 +7,18 @@ readers add temporary references. A block whose allocation reference was
 given up (unpinned) stays readable until it is reclaimed, which runs the
 owner's callback; `fence` is the event that must complete before the block's
 bytes may be overwritten.
+
+Besides the reference's structures the allocator keeps indexes that make the
+residency policy independent of the pool size: the bound blocks of each
+(request, layer) in binding order, a min-heap of empty blocks (stale entries
+are skipped lazily) and the number of unpinned blocks that readers still
+reference, so "allocatable blocks" is counted and enumerated in order
+without a scan.
 """
 
 from __future__ import annotations
 
+import heapq
 from collections import Counter, OrderedDict
 from dataclasses import dataclass
 
@@ -39,6 +47,10 @@ class DeviceAllocator:
         # owner key -> slot, in binding order
         self.lru: OrderedDict[tuple, int] = OrderedDict()
         self.occupancy: Counter = Counter()
+        # (request, layer) -> {owner key: slot} in binding order
+        self.group_blocks: dict[tuple, OrderedDict] = {}
+        self._empty_heap = list(range(config.gpu_pages))
+        self.referenced_unpinned = 0  # reclaimable blocks with reader references
 
     def _allocation_refs(self, slot) -> int:
         return 0 if slot in self.reclaimable else 1
@@ -51,6 +63,7 @@ class DeviceAllocator:
         frame.owner, frame.ref_cnt = key, 1
         self.lru[key] = slot
         self.occupancy[key[0]] += 1
+        self.group_blocks.setdefault(key[:2], OrderedDict())[key] = slot
 
     def release(self, slot, fence):
         frame = self.slots[slot]
@@ -61,8 +74,15 @@ class DeviceAllocator:
         self.reclaimable.pop(slot, None)
         del self.lru[owner]
         self.occupancy[owner[0]] -= 1
+        group = self.group_blocks[owner[:2]]
+        del group[owner]
+        if not group:
+            del self.group_blocks[owner[:2]]
         frame.owner, frame.ref_cnt, frame.fence = None, 0, fence
         self.free.add(slot)
+        heapq.heappush(self._empty_heap, slot)
+        if len(self._empty_heap) > 2 * len(self.slots) + 64:
+            self._empty_heap = sorted(self.free)
 
     def unpin(self, slot, on_reuse):
         """Give up the allocation reference; contents stay readable."""
@@ -73,6 +93,8 @@ class DeviceAllocator:
         assert frame.ref_cnt > 0
         frame.ref_cnt -= 1
         self.reclaimable[slot] = on_reuse
+        if frame.ref_cnt:
+            self.referenced_unpinned += 1
 
     def reclaim(self, slot):
         """Take an unpinned block: its owner callback detaches the old mapping."""
@@ -86,6 +108,8 @@ class DeviceAllocator:
         frame = self.slots[slot]
         if frame.owner is None:
             raise RuntimeError("cannot reference an unbound block")
+        if frame.ref_cnt == 0 and slot in self.reclaimable:
+            self.referenced_unpinned += 1
         frame.ref_cnt += 1
 
     def decref(self, slot):
@@ -93,3 +117,46 @@ class DeviceAllocator:
         if frame.owner is None or frame.ref_cnt <= self._allocation_refs(slot):
             raise RuntimeError("no reader reference to release")
         frame.ref_cnt -= 1
+        if frame.ref_cnt == 0 and slot in self.reclaimable:
+            self.referenced_unpinned -= 1
+
+    # ---- allocatable blocks: empty ones ascending, then unreferenced unpinned
+    # ---- ones in unpin order, all below the budget
+
+    def _empty_prefix(self, count):
+        """The `count` lowest empty blocks below the budget, ascending."""
+        heap, out, seen = self._empty_heap, [], set()
+        while heap and len(out) < count:
+            slot = heap[0]
+            if slot not in self.free or slot in seen:
+                heapq.heappop(heap)
+                continue
+            if slot >= self.budget:
+                break
+            seen.add(heapq.heappop(heap))
+            out.append(slot)
+        for slot in out:
+            heapq.heappush(heap, slot)
+        return out
+
+    def available(self, count=None):
+        """Allocatable blocks in allocation order (the first `count`)."""
+        limit = len(self.slots) if count is None else count
+        out = self._empty_prefix(limit)
+        if len(out) < limit:
+            for slot in self.reclaimable:
+                if slot < self.budget and self.slots[slot].ref_cnt == 0:
+                    out.append(slot)
+                    if len(out) == limit:
+                        break
+        return out
+
+    def available_count(self):
+        if self.budget >= len(self.slots):
+            return len(self.free) + len(self.reclaimable) - self.referenced_unpinned
+        return len(self.available())
+
+    def group_keys(self, group):
+        """Owner keys bound for one (request, layer), in binding order."""
+        blocks = self.group_blocks.get(group)
+        return list(blocks) if blocks else []

@@ -10,10 +10,22 @@ reused. Attention resolves selected token positions to physical rows
 (libnhs_hip.so resolver), gathers missed rows from pinned host memory into
 hot rows on the transfer stream (libnhs_hip.so gather) and runs row
 attention on the compute stream; events order the two streams.
+
+The policy makes the reference's decisions in the reference's order, but
+visits only the layers that can act: a layer is "dirty" from the moment one
+of its pages may have become unpinnable (a mirror published, readers gone,
+a page sealed or pushed out of the active tails, a hot region bound) until
+its clean history is unpinned, and a layer "awaits" a hot region until it
+has one. A policy tick sweeps dirty and awaiting layers in admission order;
+every other layer would be a no-op in a full sweep. Allocatable blocks come
+from the allocator's indexes, and finished mirrors are found by querying
+pending events in recording order, stopping at the first incomplete event
+of each stream.
 """
 
 from __future__ import annotations
 
+import heapq
 from collections import Counter
 from contextlib import suppress
 from dataclasses import dataclass, field
@@ -96,6 +108,17 @@ class RowLease(PageLease):
         self.tables.busy = False
 
 
+class _OrderedKeys(dict):
+    """Insertion-ordered set; re-adding a key moves it to the end."""
+
+    def add(self, key):
+        self.pop(key, None)
+        self[key] = None
+
+    def discard(self, key):
+        self.pop(key, None)
+
+
 class HybridKVCache:
     def __init__(self, config, hot: HotConfig):
         if config.host_pages * config.page_size >= 2**31:
@@ -104,10 +127,16 @@ class HybridKVCache:
         self.hot_config = hot
         self.hot_blocks = ceil(hot.hot_rows / config.page_size)
         self.tables: dict = {}
-        self.pending_clean: set = set()
+        self.pending_clean = _OrderedKeys()  # pages whose host mirror is in flight
         self._writing_key = None
+        self._rank: dict = {}  # (request, layer) -> admission order
+        self._next_rank = 0
+        self._dirty: set = set()  # layers that may hold unpinnable clean history
+        self._awaiting: set = set()  # layers without a hot region
+        self._sweep = None  # (heap, rank cursor, group filter) while a tick runs
         self.allocator = DeviceAllocator(config)
         self.storage = HostStore(config, self.allocator)
+        self.storage.listener = self._candidate
         self.pool, self.device = self.allocator.storage, self.storage.device
         self.row_stats = torch.zeros(3, dtype=torch.int64, device=self.device)
         self._host_pointer = self.storage.host_alias
@@ -138,13 +167,11 @@ class HybridKVCache:
         configured = self.hot_config.transition_watermark
         return max(self.hot_blocks, self.budget // 10) if configured is None else configured
 
-    def _available_blocks(self):
+    def _available_blocks(self, count=None):
         """Allocatable blocks: empty ones first (ascending), then readable
-        unpinned blocks nobody references, in the order they were unpinned."""
-        alloc = self.allocator
-        empty = sorted(i for i in alloc.free if i < self.budget)
-        readable = [i for i in alloc.reclaimable if i < self.budget and alloc.slots[i].ref_cnt == 0]
-        return empty + readable
+        unpinned blocks nobody references, in the order they were unpinned
+        (the first `count` of them)."""
+        return self.allocator.available(count)
 
     def _take_block(self, slot):
         if slot in self.allocator.reclaimable:
@@ -152,7 +179,7 @@ class HybridKVCache:
         return slot
 
     def _on_block_reused(self, slot):
-        page = self.storage.pages[self.owners[slot]]
+        page = self.storage.pages[self.allocator.slots[slot].owner]
         assert self.allocator.slots[slot].ref_cnt == 0
         assert page.host_committed_version == page.content_version
         self._detach(page)
@@ -176,16 +203,54 @@ class HybridKVCache:
             return torch.full((size,), -1, dtype=torch.int32, device=self.device)
 
         for layer in range(layers):
-            self.tables[request_id, layer] = LayerTables(
+            group = (request_id, layer)
+            self.tables[group] = LayerTables(
                 unset(n), unset(n), unset(self.hot_blocks), unset(H),
                 torch.arange(H, dtype=torch.int64, device=self.device),
             )
+            self._rank[group] = self._next_rank
+            self._next_rank += 1
+            self._awaiting.add(group)
+
+    # ---- policy bookkeeping ----------------------------------------------------------------
+
+    def _mark(self, group):
+        """A page of `group` may have become unpinnable."""
+        if group not in self.tables:
+            return
+        self._dirty.add(group)
+        sweep = self._sweep
+        if sweep is not None and self._rank[group] > sweep[1] and sweep[2](group):
+            heapq.heappush(sweep[0], (self._rank[group], group))
+
+    def _candidate(self, page):
+        """Marks the page's layer if the page now meets every unpin condition
+        but the hot region (sealed, clean, pinned, past the active tails)."""
+        group = page.key[:2]
+        if (
+            group in self.tables
+            and page.sealed
+            and page.slot is not None
+            and page.host_committed_version == page.content_version
+            and page.slot not in self.allocator.reclaimable
+            and page.key[2] <= self._tail_index(group) - ACTIVE_TAIL_PAGES
+        ):
+            self._mark(group)
+
+    def _in_order(self, groups):
+        return sorted(groups, key=self._rank.__getitem__)
+
+    def _selector(self, request_id, layer):
+        if request_id is None and layer is None:
+            return lambda g: True
+        return lambda g: (request_id is None or g[0] == request_id) and (layer is None or g[1] == layer)
 
     # ---- placement ----------------------------------------------------------------------
 
     def _prepare_append(self, page):
         self._writing_key = page.key
-        self.tables[page.key[:2]].source[page.key[2]] = page.host_slot
+        if not page.valid_tokens:  # a new page: the active tails move on
+            self._mark(page.key[:2])
         if page.valid_tokens:  # appending to an existing tail page
             if page.slot is None:
                 raise RuntimeError("active append tail lost its resident lease")
@@ -193,6 +258,7 @@ class HybridKVCache:
             self.storage.stats["append_resident_hits"] += 1
             return PageLease(self.storage, [page])
         slot = self._slot()
+        self.tables[page.key[:2]].source[page.key[2]] = page.host_slot
         self.storage.wait(self.storage.compute, self.allocator.slots[slot].fence)
         self._bind(page, slot, Location.RESIDENT)
         return None
@@ -218,7 +284,7 @@ class HybridKVCache:
         alloc, pages = self.allocator, self.storage.pages
         tails = {}
         out = []
-        for key in alloc.lru:
+        for key in alloc.lru if group is None else alloc.group_keys(group):
             if key[2] < 0:  # a hot block, not a KV page
                 continue
             if group is not None and key[:2] != group:
@@ -233,18 +299,31 @@ class HybridKVCache:
         return out
 
     def _publish_clean(self):
+        """Publish every pending mirror whose event has completed. Events of
+        one stream complete in recording order and pending pages are kept in
+        that order, so a stream's first incomplete event ends its queries."""
+        blocked = set()
         for key in list(self.pending_clean):
             page = self.storage.pages.get(key)
             if page is None:
                 self.pending_clean.discard(key)
-            elif page.host_ready is None or page.host_ready.query():
+                continue
+            event = page.host_ready
+            stream = getattr(event, "stream", None)
+            if stream is not None and stream in blocked:
+                continue
+            if event is None or event.query():
                 page.host_committed_version = page.host_enqueued_version
                 self.pending_clean.discard(key)
                 self.storage.stats["host_mirror_completions"] += 1
+                self._candidate(page)
+            elif stream is not None:
+                blocked.add(stream)
 
     def _unpin_clean_pages(self, group):
         """Once a layer has its hot region, its clean history gives up the
         allocation reference (newest page first) and stays readable."""
+        self._dirty.discard(group)
         if not self.tables[group].blocks:
             return
         for page in sorted(self._historical_pages(group), key=lambda p: -p.key[2]):
@@ -260,32 +339,48 @@ class HybridKVCache:
 
     def update_residency(self, request_id=None, layer=None, *, upcoming_allocation=False):
         """Publish finished mirrors and raise or serve hot-region demand,
-        without blocking (reference hybrid.py:256-294)."""
+        without blocking (reference hybrid.py:256-294): first every selected
+        layer unpins its clean history, then, layer by layer in admission
+        order, hot-region demand is raised and served and the layer unpins
+        again. Layers neither dirty nor awaiting a hot region are skipped
+        (both steps are no-ops for them); a layer that a later layer's
+        transition makes dirty is still visited in this tick if it comes
+        after the one being served, as in a full sweep."""
         self.storage.check_stream()
         self._publish_clean()
-        groups = [
-            g for g in self.tables
-            if g[0] in self.storage.requests
-            and (request_id is None or g[0] == request_id)
-            and (layer is None or g[1] == layer)
-        ]
-        for group in groups:
+        selected = self._selector(request_id, layer)
+        for group in self._in_order([g for g in self._dirty if selected(g)]):
             self._unpin_clean_pages(group)
-        for group in groups:
-            tables = self.tables[group]
-            residents = sum(p.slot is not None for p in self.storage.group_pages.get(group, ()))
-            if not residents:
-                continue
-            if not tables.hot_required:
-                free = len(self._available_blocks()) - int(upcoming_allocation)
-                if free < self.transition_watermark:
-                    self._require_hot(group, "watermark")
-                elif residents >= self.hot_config.resident_window_pages:
-                    self._require_hot(group, "window")
-            if tables.hot_required and not tables.blocks and not tables.busy:
-                with suppress(CapacityError):  # retried at the next policy tick
-                    self.transition_to_host(*group)
-            self._unpin_clean_pages(group)
+        heap = [(self._rank[g], g) for g in self._awaiting | self._dirty if selected(g)]
+        heapq.heapify(heap)
+        visited = set()
+        outer, self._sweep = self._sweep, [heap, -1, selected]
+        try:
+            while heap:
+                rank, group = heapq.heappop(heap)
+                if group in visited or group not in self.tables:
+                    continue
+                visited.add(group)
+                self._sweep[1] = rank
+                self._serve(group, upcoming_allocation)
+        finally:
+            self._sweep = outer
+
+    def _serve(self, group, upcoming_allocation):
+        tables = self.tables[group]
+        residents = self.storage.resident_pages[group]
+        if not residents:
+            return
+        if not tables.hot_required:
+            free = self.allocator.available_count() - int(upcoming_allocation)
+            if free < self.transition_watermark:
+                self._require_hot(group, "watermark")
+            elif residents >= self.hot_config.resident_window_pages:
+                self._require_hot(group, "window")
+        if tables.hot_required and not tables.blocks and not tables.busy:
+            with suppress(CapacityError):  # retried at the next policy tick
+                self.transition_to_host(*group)
+        self._unpin_clean_pages(group)
 
     def transition_to_host(self, request_id, layer):
         """Bind the layer's whole hot region at once, then make clean history
@@ -299,27 +394,31 @@ class HybridKVCache:
         if tables.busy:
             raise CapacityError("cannot transition an active row lease")
         self._publish_clean()
-        free = self._available_blocks()
-        victims = [
-            p for p in self._historical_pages(group)
-            if p.host_committed_version == p.content_version and p.slot not in free
-        ]
-        needed = max(0, self.hot_blocks - len(free))
-        if len(victims) < needed:
-            raise CapacityError("cannot acquire complete hot region while blocks are leased")
-        for page in victims[:needed]:  # every check precedes every mutation
-            free.append(page.slot)
-            self.allocator.unpin(page.slot, self._on_block_reused)
-            self.storage.stats["clean_page_unpins"] += 1
-        blocks = free[: self.hot_blocks]
+        free = self._available_blocks(self.hot_blocks)
+        needed = self.hot_blocks - len(free)
+        if needed:
+            # historical pages already unpinned are allocatable, hence in `free`
+            victims = [
+                p for p in self._historical_pages(group)
+                if p.host_committed_version == p.content_version and p.slot not in self.allocator.reclaimable
+            ]
+            if len(victims) < needed:
+                raise CapacityError("cannot acquire complete hot region while blocks are leased")
+            for page in victims[:needed]:  # every check precedes every mutation
+                free.append(page.slot)
+                self.allocator.unpin(page.slot, self._on_block_reused)
+                self.storage.stats["clean_page_unpins"] += 1
+        blocks = free
         for i, block in enumerate(blocks):
             self._take_block(block)
             self.storage.wait(self.storage.transfer, self.allocator.slots[block].fence)
             self.allocator.bind(block, (request_id, layer, -i - 1))
         tables.blocks = blocks
+        self._awaiting.discard(group)
         tables.hot.copy_(torch.tensor(blocks, dtype=torch.int32, device=self.device))
         tables.ready = self.storage.event(self.storage.transfer)
         self.storage.stats["hot_region_allocations"] += 1
+        self._mark(group)
         self._unpin_clean_pages(group)
 
     def _slot(self):
@@ -328,9 +427,9 @@ class HybridKVCache:
             self.update_residency(upcoming_allocation=True)
             # a later group's transition may have published an earlier group's
             # mirrors: refresh every group's reclaimable history
-            for group in self.tables:
+            for group in self._in_order(self._dirty):
                 self._unpin_clean_pages(group)
-            free = self._available_blocks()
+            free = self._available_blocks(1)
             if free:
                 return self._take_block(free[0])
             candidates = self._historical_pages()
@@ -342,7 +441,7 @@ class HybridKVCache:
                         self.transition_to_host(*group)
                     except CapacityError:
                         continue
-                    free = self._available_blocks()
+                    free = self._available_blocks(1)
                     if free:
                         return self._take_block(free[0])
             if not pending:
@@ -454,6 +553,9 @@ class HybridKVCache:
         store.retire(request_id, keepalive=groups)
         for key in [k for k in self.tables if k[0] == request_id]:
             del self.tables[key]
+            del self._rank[key]
+            self._dirty.discard(key)
+            self._awaiting.discard(key)
         self.collect(wait=wait)
 
     def collect(self, wait=False):
@@ -507,7 +609,7 @@ class HybridKVCache:
             transition_watermark=self.transition_watermark,
             empty_device_blocks=len(self.allocator.free),
             readable_unpinned_blocks=len(self.allocator.reclaimable),
-            allocatable_device_blocks=len(self._available_blocks()),
+            allocatable_device_blocks=self.allocator.available_count(),
             pending_clean_pages=len(self.pending_clean),
             hot_pending_groups=sum(t.hot_required and not t.blocks for t in self.tables.values()),
             hot_leased_blocks=sum(len(t.blocks) for t in self.tables.values()),
@@ -524,6 +626,9 @@ class HybridKVCache:
     def assert_invariants(self):
         store, alloc = self.storage, self.allocator
         store.assert_invariants()
+        assert alloc.available_count() == len(self._available_blocks())
+        assert self._awaiting == {g for g, t in self.tables.items() if not t.blocks}
+        assert set(self._rank) == set(self.tables)
         for name, request in store.requests.items():
             assert request.extra_index_bytes == sum(t.nbytes for g, t in self.tables.items() if g[0] == name)
         assert not (alloc.free & alloc.reclaimable.keys())

@@ -109,6 +109,7 @@ class PageLease:
         for s in self.slots:
             self.store.allocator.decref(s)
         self.released = True
+        self.store.notify(self.pages)
 
     def __enter__(self):
         self.wait()
@@ -138,6 +139,10 @@ class HostStore:
         self.transfer = torch.cuda.Stream(device=self.device) if self.cuda else None
         self.pages: dict = {}
         self.group_pages: dict = {}  # (request_id, layer) -> pages in index order
+        self.resident_pages: Counter = Counter()  # (request_id, layer) -> pages holding a block
+        # called with each page that lost its readers or published its host
+        # mirror (a residency policy's unpin candidates)
+        self.listener = None
         self.requests: dict = {}
         self.free_host = list(range(config.host_pages - 1, -1, -1))
         self.stats: Counter = Counter()
@@ -181,11 +186,18 @@ class HostStore:
         return torch.cuda.stream(stream) if self.cuda else nullcontext()
 
     def event(self, stream):
+        """A recorded event; `.stream` names the stream it completes in order on."""
         if not self.cuda:
             return None
         ev = torch.cuda.Event()
         ev.record(stream)
+        ev.stream = stream
         return ev
+
+    def notify(self, pages):
+        if self.listener is not None:
+            for page in pages:
+                self.listener(page)
 
     def wait(self, stream, event):
         if event is not None:
@@ -239,6 +251,18 @@ class HostStore:
             self.stats["materialized_pages"] += 1
         return page
 
+    def _unmaterialize(self, page: Page):
+        """Undo materialize() of a page that never held data."""
+        key = page.key
+        assert page.slot is None and page.valid_tokens == 0 and self.pages[key] is page
+        request = self.requests[key[0]]
+        del self.pages[key]
+        self.group_pages[key[:2]].remove(page)
+        request.keys.remove(key)
+        request.host_credits += 1
+        self.free_host.append(page.host_slot)
+        self.stats["materialized_pages"] -= 1
+
     def detach(self, page: Page):
         """Drop a page's device block; reuse of the block waits on its events."""
         assert self.pages.get(page.key) is page
@@ -248,11 +272,13 @@ class HostStore:
             self.wait(self.transfer, ev)
         self.allocator.release(page.slot, self.event(self.transfer))
         page.slot, page.location = None, Location.HOST
+        self.resident_pages[page.key[:2]] -= 1
         self.stats["evictions"] += 1
 
     def bind(self, page: Page, slot, location):
         page.slot, page.location, page.last_use = slot, location, None
         self.allocator.bind(slot, page.key)
+        self.resident_pages[page.key[:2]] += 1
         self.stats["peak_device_pages"] = max(self.stats["peak_device_pages"], len(self.allocator.lru))
 
     @torch.inference_mode()
@@ -287,8 +313,14 @@ class HostStore:
         while done < len(k):
             index, within = divmod(start + done, P)
             count = min(P - within, len(k) - done)
+            fresh = (request_id, layer, index) not in self.pages
             page = self.materialize(request_id, layer, index)
-            lease = prepare_page(page)
+            try:
+                lease = prepare_page(page)
+            except Exception:
+                if fresh:  # a failed placement leaves no empty page behind
+                    self._unmaterialize(page)
+                raise
             if lease is not None:
                 lease.wait()
             for ev in (page.ready, page.last_use, page.host_ready):
@@ -319,10 +351,10 @@ class HostStore:
             self.stats["d2h_bytes"] += self.page_bytes * count // P
             if lease is not None:
                 lease.release()
+            done += count
+            request.lengths[layer] = start + done  # pages written so far stay counted if a later one fails
             if after_write is not None:
                 after_write(page)
-            done += count
-        request.lengths[layer] += len(k)
 
     def _update_bounds(self, request, layer, index, block, within, count):
         """Page mean key (fp32) and running min/max of the new keys
@@ -366,6 +398,7 @@ class HostStore:
         del self.requests[request_id]
         for layer in range(request.layers):
             self.group_pages.pop((request_id, layer), None)
+            self.resident_pages.pop((request_id, layer), None)
         request.keepalive = tuple(keepalive)
         done = self.event(self.transfer)
         self.retired.append((done, request, retired))
@@ -393,8 +426,9 @@ class HostStore:
     def page_state(self, key):
         page = self.pages[key]
         backup_pending = page.host_ready is not None and not page.host_ready.query()
-        if not backup_pending:
+        if not backup_pending and page.host_committed_version != page.host_enqueued_version:
             page.host_committed_version = page.host_enqueued_version
+            self.notify((page,))
         return {
             "location": page.location.value,
             "loading": page.ready is not None and not page.ready.query(),
@@ -449,6 +483,14 @@ class HostStore:
         assert self.available_host_credits >= 0
         assert self.pinned == {p.key for p in self.pages.values() if p.pins}
         assert set(self.allocator.lru) == set(occupied)
+        by_group = {}
+        for key, slot in self.allocator.lru.items():
+            by_group.setdefault(key[:2], []).append((key, slot))
+        assert {g: list(b.items()) for g, b in self.allocator.group_blocks.items()} == by_group
+        assert self.allocator.referenced_unpinned == sum(
+            1 for s in self.allocator.reclaimable if self.allocator.slots[s].ref_cnt
+        )
+        assert +self.resident_pages == Counter(p.key[:2] for p in self.pages.values() if p.slot is not None)
         assert self.allocator.free == {i for i, k in enumerate(owners) if k is None}
         assert +self.allocator.occupancy == Counter(k[0] for k in occupied)
         for slot in self.allocator.slots:

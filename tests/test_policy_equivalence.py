@@ -1,0 +1,190 @@
+"""The indexed residency policy against a full-sweep model of it.
+
+HybridKVCache skips layers that cannot act and reads allocatable blocks
+from indexes; scan_policy.ScanningCache visits every layer and every bound
+block on each tick, like the reference (hybrid.py:206-368). Both run the
+same random sequences of admissions, appends, decode steps, reads (with
+leases held across other operations), transitions, reclaims, state queries
+and releases, and must agree after every operation on block owners,
+reference counts, the unpin order, page states, tables, counters and
+raised errors.
+"""
+
+import random
+
+import pytest
+import torch
+
+from nano_hisparse.config import CacheConfig
+from nano_hisparse.hybrid import HotConfig, HybridKVCache
+from nano_hisparse.attention import row_attention
+from nano_hisparse.row_index import LogicalTopK
+from scan_policy import ScanningCache
+
+P = 4
+
+
+def state(cache):
+    a, s = cache.allocator, cache.storage
+    pages = {
+        k: (p.slot, p.location.value, p.valid_tokens, p.sealed, p.content_version, p.host_committed_version, p.pins)
+        for k, p in s.pages.items()
+    }
+    tables = {
+        g: (tuple(t.blocks), t.hot_required, t.trigger, t.busy, t.tags.tolist(), t.lru.tolist(),
+            t.resident.tolist(), t.source.tolist())
+        for g, t in cache.tables.items()
+    }
+    return (
+        [(x.owner, x.ref_cnt) for x in a.slots],
+        list(a.reclaimable),
+        sorted(a.free),
+        pages,
+        tables,
+        dict(s.stats),
+        cache.row_stats.tolist(),
+        sorted(s.free_host),
+        {n: r.lengths for n, r in s.requests.items()},
+    )
+
+
+def attempt(fn):
+    try:
+        return ("ok", fn())
+    except Exception as exc:  # the two implementations must fail alike
+        return ("error", type(exc).__name__, str(exc))
+
+
+class Twin:
+    """The same operation on both caches; results and states must match."""
+
+    def __init__(self, cfg, hot):
+        self.caches = (HybridKVCache(cfg, hot), ScanningCache(cfg, hot))
+        self.leases = {}
+
+    def do(self, name, fn):
+        results = [attempt(lambda c=c: fn(c)) for c in self.caches]
+        assert _comparable(results[0]) == _comparable(results[1]), name
+        a, b = (state(c) for c in self.caches)
+        assert a == b, name
+        for c in self.caches:
+            c.assert_invariants()
+        return results[0]
+
+
+def _comparable(result):
+    if result[0] == "ok" and isinstance(result[1], torch.Tensor):
+        return ("ok", result[1].tolist())
+    if result[0] == "ok":
+        return ("ok", None)
+    return result
+
+
+def run(seed, ops=70):
+    rng = random.Random(seed)
+    hot_rows = rng.choice([4, 8])
+    # from seed 40: no window, watermark 0 (transitions only when the last
+    # block goes) and no explicit transitions, so the pool runs full
+    pressure_only = seed >= 40
+    hot = HotConfig(
+        4,
+        hot_rows,
+        resident_window_pages=64 if pressure_only else rng.choice([2, 3, 4, 6, 64]),
+        transition_watermark=0 if pressure_only else rng.choice([None, 0, 1, 3]),
+    )
+    layers_max = 2
+    admission = hot.admission_blocks(P, layers_max)
+    cfg = CacheConfig(
+        gpu_pages=admission + rng.randrange(0, 10),
+        host_pages=96,
+        page_size=P,
+        kv_heads=1,
+        head_dim=8,
+        device="cpu",
+    )
+    twin = Twin(cfg, hot)
+    gen = torch.Generator().manual_seed(seed)
+    names = []
+    for step in range(ops):
+        op = rng.random()
+        live = [n for n in names if n in twin.caches[0].storage.requests]
+        if op < 0.12 or not live:
+            name = f"r{step}"
+            layers = rng.randint(1, layers_max)
+            max_tokens = rng.randint(8, 48)
+            res = twin.do(f"{step} reserve", lambda c: c.reserve(name, max_tokens, layers))
+            if res[0] == "ok":
+                names.append(name)
+            continue
+        name = rng.choice(live)
+        request = twin.caches[0].storage.requests[name]
+        layer = rng.randrange(request.layers)
+        if op < 0.45:
+            room = request.max_tokens - request.lengths[layer]
+            count = min(room, rng.choice([1, 1, 2, 3, P, 2 * P + 1])) if room else 1
+            k = torch.randn(count, 1, 8, generator=gen)
+            v = torch.randn(count, 1, 8, generator=gen)
+            twin.do(f"{step} write {name}/{layer} x{count}", lambda c: c.write(name, layer, k.clone(), v.clone()))
+        elif op < 0.65:
+            length = request.lengths[layer]
+            if not length:
+                continue
+            width = rng.randint(1, 4)
+            chosen = sorted(rng.sample(range(length), min(width, length)))
+            q = torch.randn(2, 8, generator=gen)
+            topk = LogicalTopK(torch.tensor(chosen, dtype=torch.int32))
+            twin.do(f"{step} attend {name}/{layer}", lambda c: row_attention(q, c, name, layer, topk))
+        elif op < 0.72:
+            key = (name, layer)
+            if key in twin.leases:
+                leases = twin.leases.pop(key)
+                twin.do(f"{step} release lease {key}", lambda c: leases[twin.caches.index(c)].release())
+            elif request.lengths[layer]:
+                length = request.lengths[layer]
+                chosen = sorted(rng.sample(range(length), min(3, length)))
+                topk = LogicalTopK(torch.tensor(chosen, dtype=torch.int32))
+                held = []
+                res = twin.do(f"{step} hold lease {key}", lambda c: held.append(c.resolve(name, layer, topk)))
+                if res[0] == "ok":
+                    twin.leases[key] = held
+        elif op < 0.86 and pressure_only:  # no explicit transitions: more appends instead
+            k = torch.randn(P, 1, 8, generator=gen)
+            v = torch.randn(P, 1, 8, generator=gen)
+            if request.lengths[layer] + P <= request.max_tokens:
+                twin.do(f"{step} write {name}/{layer} x{P}", lambda c: c.write(name, layer, k.clone(), v.clone()))
+        elif op < 0.80:
+            twin.do(f"{step} transition {name}/{layer}", lambda c: c.transition_to_host(name, layer))
+        elif op < 0.86:
+            evict = rng.random() < 0.5
+            twin.do(f"{step} reclaim {name}/{layer}", lambda c: c.reclaim_history(name, layer, evict=evict))
+        elif op < 0.92:
+            keys = sorted(k for k in twin.caches[0].storage.pages if k[0] == name)
+            if keys:
+                key = rng.choice(keys)
+                twin.do(f"{step} page_state {key}", lambda c: c.page_state(key))
+            twin.do(f"{step} collect", lambda c: c.collect())
+        else:
+            for key in [k for k in twin.leases if k[0] == name]:
+                leases = twin.leases.pop(key)
+                twin.do(f"{step} release lease {key}", lambda c: leases[twin.caches.index(c)].release())
+            twin.do(f"{step} release {name}", lambda c: c.release_request(name))
+    return twin
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_indexed_policy_matches_full_sweeps(cpu_kernels, seed):
+    twin = run(seed)
+    stats = twin.caches[0].storage.stats
+    assert stats["materialized_pages"] > 0
+
+
+def test_random_sequences_reach_every_policy_path(cpu_kernels):
+    """The seeds above exercise transitions, unpins, reuse and every trigger."""
+    totals = {}
+    for seed in range(60):
+        stats = run(seed).caches[0].storage.stats
+        for key, value in stats.items():
+            totals[key] = totals.get(key, 0) + value
+    for key in ("hot_region_allocations", "clean_page_unpins", "unpinned_block_reuses", "hot_trigger_window",
+                "hot_trigger_watermark", "hot_trigger_explicit", "evictions"):
+        assert totals.get(key, 0) > 0, key

@@ -248,7 +248,9 @@ def test_allocation_revisits_a_group_published_late(cpu_kernels, monkeypatch):
     assert not cache.allocator.free
 
     def publish_after_the_policy_tick(**kwargs):
-        page.host_committed_version = page.content_version
+        # the mirror completes only after the tick has visited the group
+        cache.pending_clean.add(page.key)
+        cache._publish_clean()
 
     monkeypatch.setattr(cache, "update_residency", publish_after_the_policy_tick)
     assert cache._slot() == slot
