@@ -44,6 +44,27 @@ enum { NHS_F32 = 0, NHS_F16 = 1, NHS_BF16 = 2 };
 #define NHS_MAX_HOT_ROWS 32768   /* resolver: hot rows per item (hybrid.py:36) */
 #define NHS_MAX_SELECT_PAGES 16384 /* selectors: pages scored per request */
 
+/*
+ * Device tables of one (request, layer), for the batched decode entry points
+ * (nhs_*_items): an array of these lives in device memory, one entry per
+ * batch item, and stays valid while the request is admitted (the tables are
+ * allocated at admission and only their contents change). Layouts are those
+ * of the strided entry points; alignment (16 bytes for the bounds and
+ * summaries) is the caller's duty and is not checked, since the library
+ * cannot read device memory before launching.
+ */
+typedef struct nhs_layer_item {
+  const int32_t* source;   /* page -> host page, -1 unset      [n_pages] */
+  const int32_t* resident; /* page -> pool block, -1 none      [n_pages] */
+  const int32_t* hot;      /* hot block table    [ceil(hot_rows/page_size)] */
+  int32_t* tags;           /* hot row tags (host rows, -1 empty) [hot_rows] */
+  int64_t* lru;            /* hot slot LRU order                 [hot_rows] */
+  void* minimum;           /* Quest key bounds, KV dtype [n_pages, kv_heads, head_dim] */
+  void* maximum;
+  float* summaries;        /* fp32 mean keys             [n_pages, kv_heads, head_dim] */
+  int64_t n_pages;
+} nhs_layer_item;
+
 int nhs_abi_version(void);
 const char* nhs_last_error(void);
 
@@ -195,6 +216,46 @@ int nhs_append_page(const void* k, const void* v, int64_t token_stride, int32_t 
                     int32_t page_size, void* pool, int64_t block, int32_t within, int32_t count,
                     void* host_alias, int64_t host_page, float* summary, void* minimum, void* maximum,
                     void* stream);
+
+/*
+ * Batched decode-time append: item b appends one token, k/v rows at
+ * k + b * token_stride (row_elems elements each), at position lengths[b]
+ * (its layer length before the append) of items[b]: page
+ * p = lengths[b] / page_size, row lengths[b] % page_size of pool block
+ * items[b].resident[p] and, with a host_alias, of host page
+ * items[b].source[p]. Bounds and the page mean are updated as in
+ * nhs_append_page (same arithmetic, bit-identical results). The caller binds
+ * the page (resident[p], source[p]) before the call and increments its
+ * lengths after it. No counterpart in the reference, which appends request
+ * by request (storage.py:258-331); this is the batched engine step's form.
+ */
+int nhs_append_items(int32_t batch, const void* k, const void* v, int64_t token_stride, int32_t kv_dtype,
+                     int32_t row_elems, int32_t page_size, void* pool, void* host_alias,
+                     const nhs_layer_item* items, const int64_t* lengths, void* stream);
+
+/*
+ * nhs_quest_select over per-item bounds: item b reads items[b].minimum /
+ * .maximum ([n_pages, kv_heads, head_dim], n_pages >= its page count) and
+ * lengths[b]. Results are bit-identical to nhs_quest_select on the same
+ * bounds. Batched form of quest_selection, nano_hisparse/selection.py:69-91.
+ */
+int nhs_quest_select_items(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                           int64_t q_head_stride, const nhs_layer_item* items, int32_t bounds_dtype,
+                           int32_t q_heads, int32_t kv_heads, int32_t head_dim, const int64_t* lengths,
+                           int32_t page_size, int32_t max_pages, int32_t top_pages, int32_t keep_sink,
+                           float* scores, int32_t* pages, int32_t* positions, void* stream);
+
+/*
+ * nhs_resolve_rows over per-item tables: item b reads items[b].source /
+ * .resident (n_pages entries), .hot and updates .tags / .lru in place.
+ * Outputs and limits as nhs_resolve_rows; lengths is required. Batched form
+ * of resolve_rows, nano_hisparse/row_index.py:62-140.
+ */
+int nhs_resolve_items(int32_t batch, int32_t n, const void* positions, int32_t positions_i64,
+                      int64_t positions_stride, const nhs_layer_item* items, int32_t hot_rows,
+                      const int64_t* lengths, int32_t page_size, int64_t* physical, int64_t* miss_host,
+                      int64_t* miss_device, int64_t plan_stride, int64_t* counts, int64_t* counts_total,
+                      void* stream);
 
 /*
  * Legacy per-head selections: out[h, c] = columns[h, c] in [0, n) ?

@@ -32,9 +32,8 @@ struct AppendArgs {
 __device__ __forceinline__ float nan_min(float a, float b) { return (a != a || b != b) ? a + b : (b < a ? b : a); }
 __device__ __forceinline__ float nan_max(float a, float b) { return (a != a || b != b) ? a + b : (b > a ? b : a); }
 
-__global__ __launch_bounds__(kAppendThreads) void append_page_kernel(AppendArgs a) {
-  const int e = blockIdx.x * kAppendThreads + threadIdx.x;
-  if (e >= a.row_elems) return;
+// Element e of every appended row of one page.
+__device__ __forceinline__ void append_element(const AppendArgs& a, int e) {
   const int esize = a.dtype == NHS_F32 ? 4 : 2;
   float lo = load_elem(a.minimum, a.dtype, e);
   float hi = load_elem(a.maximum, a.dtype, e);
@@ -71,6 +70,52 @@ __global__ __launch_bounds__(kAppendThreads) void append_page_kernel(AppendArgs 
   a.summary[e] = (float)(sum / (double)(a.within + a.count));
 }
 
+__global__ __launch_bounds__(kAppendThreads) void append_page_kernel(AppendArgs a) {
+  const int e = blockIdx.x * kAppendThreads + threadIdx.x;
+  if (e < a.row_elems) append_element(a, e);
+}
+
+struct AppendItemsArgs {
+  const char* k;
+  const char* v;
+  int64_t token_stride;  // elements between the items' rows
+  int dtype, row_elems, page_size;
+  char* pool;
+  char* host;
+  const nhs_layer_item* items;
+  const int64_t* lengths;
+};
+
+// Item blockIdx.y appends its one token; its page and row follow from its
+// length and its page tables.
+__global__ __launch_bounds__(kAppendThreads) void append_items_kernel(AppendItemsArgs g) {
+  const int e = blockIdx.x * kAppendThreads + threadIdx.x;
+  if (e >= g.row_elems) return;
+  const int b = blockIdx.y;
+  const nhs_layer_item& item = g.items[b];
+  const int64_t length = g.lengths[b];
+  const int64_t page = length / g.page_size;
+  const int esize = g.dtype == NHS_F32 ? 4 : 2;
+  const int64_t plane = (int64_t)g.page_size * g.row_elems;
+  const int64_t block_bytes = 2 * plane * esize;
+  const int64_t page_offset = page * g.row_elems;
+  AppendArgs a;
+  a.k = g.k + (int64_t)b * g.token_stride * esize;
+  a.v = g.v + (int64_t)b * g.token_stride * esize;
+  a.token_stride = g.token_stride;
+  a.dtype = g.dtype;
+  a.row_elems = g.row_elems;
+  a.plane_elems = plane;
+  a.pool_block = g.pool + (int64_t)item.resident[page] * block_bytes;
+  a.host_block = g.host ? g.host + (int64_t)item.source[page] * block_bytes : nullptr;
+  a.within = (int)(length - page * g.page_size);
+  a.count = 1;
+  a.summary = item.summaries + page_offset;
+  a.minimum = static_cast<char*>(item.minimum) + page_offset * esize;
+  a.maximum = static_cast<char*>(item.maximum) + page_offset * esize;
+  append_element(a, e);
+}
+
 }  // namespace nhs
 
 extern "C" int nhs_append_page(const void* k, const void* v, int64_t token_stride, int32_t kv_dtype,
@@ -102,4 +147,30 @@ extern "C" int nhs_append_page(const void* k, const void* v, int64_t token_strid
   launch(append_page_kernel, dim3((unsigned)((row_elems + kAppendThreads - 1) / kAppendThreads)),
          dim3(kAppendThreads), 0, (hipStream_t)stream, ev.start, ev.stop, a);
   return launch_status("nhs_append_page");
+}
+
+extern "C" int nhs_append_items(int32_t batch, const void* k, const void* v, int64_t token_stride, int32_t kv_dtype,
+                                int32_t row_elems, int32_t page_size, void* pool, void* host_alias,
+                                const nhs_layer_item* items, const int64_t* lengths, void* stream) {
+  using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
+  if (!k || !v || !pool || !items || !lengths) return fail(NHS_ERR_INVALID, "nhs_append_items: null pointer");
+  if (!valid_dtype(kv_dtype)) return fail(NHS_ERR_INVALID, "nhs_append_items: bad dtype");
+  if (batch < 0 || batch > 65535 || row_elems < 1 || page_size < 1 || token_stride < row_elems)
+    return fail(NHS_ERR_INVALID, "nhs_append_items: invalid batch, rows or strides");
+  if (batch == 0) return NHS_OK;
+  AppendItemsArgs g;
+  g.k = static_cast<const char*>(k);
+  g.v = static_cast<const char*>(v);
+  g.token_stride = token_stride;
+  g.dtype = kv_dtype;
+  g.row_elems = row_elems;
+  g.page_size = page_size;
+  g.pool = static_cast<char*>(pool);
+  g.host = static_cast<char*>(host_alias);
+  g.items = items;
+  g.lengths = lengths;
+  launch(append_items_kernel, dim3((unsigned)((row_elems + kAppendThreads - 1) / kAppendThreads), (unsigned)batch),
+         dim3(kAppendThreads), 0, (hipStream_t)stream, ev.start, ev.stop, g);
+  return launch_status("nhs_append_items");
 }

@@ -60,6 +60,7 @@ struct ResolveArgs {
   int64_t plan_stride;
   int64_t* counts;
   int64_t* counts_total;
+  const nhs_layer_item* items;  // per-item tables (then the strided table fields are unused)
 };
 
 struct ResolveShared {
@@ -195,11 +196,19 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   int kp = 1;
   while (kp < n) kp <<= 1;
 
+  // This item's tables: from its entry in the item table, or strided.
+  const nhs_layer_item* item = a.items ? a.items + b : nullptr;
+  const int32_t* source = item ? item->source : a.source + (int64_t)b * a.page_stride;
+  const int32_t* resident = item ? item->resident : a.resident + (int64_t)b * a.page_stride;
+  const int n_pages = item ? (int)item->n_pages : a.n_pages;
+  int32_t* const tags = item ? item->tags : a.tags + (int64_t)b * a.tags_stride;
+  int64_t* const lru_out = item ? item->lru : a.lru + (int64_t)b * a.lru_stride;
+
   // Loads that depend on nothing are issued first: the tags and lru of the
   // first kRegH * kResolveThreads hot rows (registers) and the hot block
   // table (LDS), so their latency overlaps the position lookups below.
-  const int32_t* tags_in = a.tags + (int64_t)b * a.tags_stride;
-  const int64_t* lru_in = a.lru + (int64_t)b * a.lru_stride;
+  const int32_t* tags_in = tags;
+  const int64_t* lru_in = lru_out;
   int32_t tag_r[kRegH];
   int64_t lru_r[kRegH];
 #pragma unroll
@@ -210,7 +219,7 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   }
   const int hot_blocks = (H + P - 1) / P;
   const bool hot_cached = hot_blocks <= kHotCache;
-  const int32_t* hot = a.hot + (int64_t)b * a.hot_stride;
+  const int32_t* hot = item ? item->hot : a.hot + (int64_t)b * a.hot_stride;
   if (hot_cached)
     for (int i = tid; i < hot_blocks; i += kResolveThreads) sh.hot[i] = hot[i];
 
@@ -227,9 +236,9 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     const int64_t lg = (int64_t)(key[q] >> 32);
     // Positions are < 2^31 (int32 host tags); page = min(lg / P, n_pages - 1).
     const uint32_t pg = a.page_div.div((uint32_t)lg);
-    const int64_t page = pg < (uint32_t)(a.n_pages - 1) ? (int64_t)pg : (int64_t)(a.n_pages - 1);
-    src[q] = a.source[(int64_t)b * a.page_stride + page];
-    res[q] = a.resident[(int64_t)b * a.page_stride + page];
+    const int64_t page = pg < (uint32_t)(n_pages - 1) ? (int64_t)pg : (int64_t)(n_pages - 1);
+    src[q] = source[page];
+    res[q] = resident[page];
   };
 #pragma unroll
   for (int q = 0; q < kKPerThread; ++q) {
@@ -331,7 +340,6 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   __syncthreads();
 
   // ---- 4. scan tags: hot hits and protected slots ---------------------------
-  int32_t* tags = a.tags + (int64_t)b * a.tags_stride;
   auto scan_tag = [&](int s, int32_t t) {
     if (t >= 0) {
       int h = hash_find(sh.u.hash.hkey, t);
@@ -490,7 +498,6 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     start[2] = n0 + n1;
     start[3] = n0 + n1 + n2;
   }
-  int64_t* lru_out = a.lru + (int64_t)b * a.lru_stride;
   {
     int parity = 0;
     for (int g0 = 0; g0 < n_chunks; g0 += kRankGroup, parity ^= 1) {
@@ -518,40 +525,31 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
 
 }  // namespace nhs
 
-extern "C" int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t positions_i64,
-                                int64_t positions_stride, const int32_t* source, const int32_t* resident,
-                                int64_t page_table_stride, int32_t n_pages, const int32_t* hot, int64_t hot_stride,
-                                int32_t* tags, int64_t tags_stride, int64_t* lru, int64_t lru_stride,
-                                int32_t hot_rows, const int64_t* lengths, int64_t length, int32_t page_size,
-                                int64_t* physical, int64_t* miss_host, int64_t* miss_device, int64_t plan_stride,
-                                int64_t* counts, int64_t* counts_total, void* stream) {
-  using namespace nhs;
-  const LaunchEvents ev = take_launch_events();
-  if (!positions || !source || !resident || !hot || !tags || !lru || !physical || !miss_host || !miss_device ||
-      !counts)
-    return fail(NHS_ERR_INVALID, "nhs_resolve_rows: null pointer");
-  if (batch < 0 || n < 1 || n_pages < 1 || hot_rows < 1 || page_size < 1)
-    return fail(NHS_ERR_INVALID, "nhs_resolve_rows: need n, n_pages, hot_rows, page_size >= 1");
+namespace nhs {
+
+static int check_resolve(const char* who, int32_t batch, int32_t n, const void* positions, int32_t hot_rows,
+                         const int64_t* lengths, int64_t length, int32_t page_size, const int64_t* physical,
+                         const int64_t* miss_host, const int64_t* miss_device, const int64_t* counts) {
+  if (!positions || !physical || !miss_host || !miss_device || !counts)
+    return fail(NHS_ERR_INVALID, "%s: null pointer", who);
+  if (batch < 0 || n < 1 || hot_rows < 1 || page_size < 1)
+    return fail(NHS_ERR_INVALID, "%s: need n, n_pages, hot_rows, page_size >= 1", who);
   if (n > kMaxK || hot_rows > kMaxH)
-    return fail(NHS_ERR_UNSUPPORTED, "nhs_resolve_rows: n <= %d and hot_rows <= %d required", kMaxK, kMaxH);
+    return fail(NHS_ERR_UNSUPPORTED, "%s: n <= %d and hot_rows <= %d required", who, kMaxK, kMaxH);
   if (!lengths && (length < 0 || length >= (1ll << 31)))
-    return fail(NHS_ERR_INVALID, "nhs_resolve_rows: length must be in [0, 2^31)");
-  if (batch == 0) return NHS_OK;
-  ResolveArgs a;
+    return fail(NHS_ERR_INVALID, "%s: length must be in [0, 2^31)", who);
+  return NHS_OK;
+}
+
+static void fill_common(ResolveArgs& a, int32_t n, const void* positions, int32_t positions_i64,
+                        int64_t positions_stride, int32_t hot_rows, const int64_t* lengths, int64_t length,
+                        int32_t page_size, int64_t* physical, int64_t* miss_host, int64_t* miss_device,
+                        int64_t plan_stride, int64_t* counts, int64_t* counts_total) {
+  a = ResolveArgs{};
   a.n = n;
   a.positions = positions;
   a.positions_i64 = positions_i64;
   a.positions_stride = positions_stride;
-  a.source = source;
-  a.resident = resident;
-  a.page_stride = page_table_stride;
-  a.n_pages = n_pages;
-  a.hot = hot;
-  a.hot_stride = hot_stride;
-  a.tags = tags;
-  a.tags_stride = tags_stride;
-  a.lru = lru;
-  a.lru_stride = lru_stride;
   a.hot_rows = hot_rows;
   a.lengths = lengths;
   a.length = length;
@@ -563,7 +561,62 @@ extern "C" int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions,
   a.plan_stride = plan_stride;
   a.counts = counts;
   a.counts_total = counts_total;
+}
+
+}  // namespace nhs
+
+extern "C" int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t positions_i64,
+                                int64_t positions_stride, const int32_t* source, const int32_t* resident,
+                                int64_t page_table_stride, int32_t n_pages, const int32_t* hot, int64_t hot_stride,
+                                int32_t* tags, int64_t tags_stride, int64_t* lru, int64_t lru_stride,
+                                int32_t hot_rows, const int64_t* lengths, int64_t length, int32_t page_size,
+                                int64_t* physical, int64_t* miss_host, int64_t* miss_device, int64_t plan_stride,
+                                int64_t* counts, int64_t* counts_total, void* stream) {
+  using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
+  const char* who = "nhs_resolve_rows";
+  int st = check_resolve(who, batch, n, positions, hot_rows, lengths, length, page_size, physical, miss_host,
+                         miss_device, counts);
+  if (st != NHS_OK) return st;
+  if (!source || !resident || !hot || !tags || !lru) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
+  if (n_pages < 1) return fail(NHS_ERR_INVALID, "%s: need n, n_pages, hot_rows, page_size >= 1", who);
+  if (batch == 0) return NHS_OK;
+  ResolveArgs a;
+  fill_common(a, n, positions, positions_i64, positions_stride, hot_rows, lengths, length, page_size, physical,
+              miss_host, miss_device, plan_stride, counts, counts_total);
+  a.source = source;
+  a.resident = resident;
+  a.page_stride = page_table_stride;
+  a.n_pages = n_pages;
+  a.hot = hot;
+  a.hot_stride = hot_stride;
+  a.tags = tags;
+  a.tags_stride = tags_stride;
+  a.lru = lru;
+  a.lru_stride = lru_stride;
   launch(resolve_rows_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0, (hipStream_t)stream, ev.start, ev.stop,
          a);
-  return launch_status("nhs_resolve_rows");
+  return launch_status(who);
+}
+
+extern "C" int nhs_resolve_items(int32_t batch, int32_t n, const void* positions, int32_t positions_i64,
+                                 int64_t positions_stride, const nhs_layer_item* items, int32_t hot_rows,
+                                 const int64_t* lengths, int32_t page_size, int64_t* physical, int64_t* miss_host,
+                                 int64_t* miss_device, int64_t plan_stride, int64_t* counts, int64_t* counts_total,
+                                 void* stream) {
+  using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
+  const char* who = "nhs_resolve_items";
+  int st = check_resolve(who, batch, n, positions, hot_rows, lengths, 0, page_size, physical, miss_host,
+                         miss_device, counts);
+  if (st != NHS_OK) return st;
+  if (!items || !lengths) return fail(NHS_ERR_INVALID, "%s: null items or lengths", who);
+  if (batch == 0) return NHS_OK;
+  ResolveArgs a;
+  fill_common(a, n, positions, positions_i64, positions_stride, hot_rows, lengths, 0, page_size, physical, miss_host,
+              miss_device, plan_stride, counts, counts_total);
+  a.items = items;
+  launch(resolve_rows_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0, (hipStream_t)stream, ev.start, ev.stop,
+         a);
+  return launch_status(who);
 }

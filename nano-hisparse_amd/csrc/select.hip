@@ -48,7 +48,20 @@ struct ScoreArgs {
   int64_t length;
   int page_size, max_pages;
   float* scores;
+  const nhs_layer_item* items;  // per-item bounds (then lo, hi and b_bs are unused)
 };
+
+// Request b's bound rows: from its item entry, or strided from lo / hi.
+template <typename T>
+__device__ __forceinline__ void bounds_of(const ScoreArgs& a, int b, const char*& lo, const char*& hi) {
+  if (a.items) {
+    lo = static_cast<const char*>(a.items[b].minimum);
+    hi = static_cast<const char*>(a.items[b].maximum);
+  } else {
+    lo = static_cast<const char*>(a.lo) + (int64_t)b * a.b_bs * T::bytes;
+    hi = static_cast<const char*>(a.hi) + (int64_t)b * a.b_bs * T::bytes;
+  }
+}
 
 __device__ __forceinline__ float torch_maximum(float a, float b) {
   // torch.maximum propagates NaN from either operand.
@@ -103,8 +116,8 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < E; ++e) qv[g][e] = data && g < a.group ? qs[(kh * a.group + g) * a.head_dim + sub * E + e] : 0.f;
-  const char* lo = static_cast<const char*>(a.lo) + (int64_t)b * a.b_bs * T::bytes;
-  const char* hi = static_cast<const char*>(a.hi) + (int64_t)b * a.b_bs * T::bytes;
+  const char *lo, *hi;
+  bounds_of<T>(a, b, lo, hi);
   const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
   const int64_t lane_off = data ? (int64_t)kh * a.head_dim + sub * E : 0;
   auto load = [&](int p, float (&mn)[E], float (&mx)[E]) {
@@ -195,8 +208,8 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
     if (!(data && g < a.group))
 #pragma unroll
       for (int e = 0; e < E; ++e) qv[g][e] = 0.f;
-  const char* lo = static_cast<const char*>(a.lo) + (int64_t)b * a.b_bs * T::bytes;
-  const char* hi = static_cast<const char*>(a.hi) + (int64_t)b * a.b_bs * T::bytes;
+  const char *lo, *hi;
+  bounds_of<T>(a, b, lo, hi);
   const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
   const int64_t lane_off = data ? (int64_t)kh * a.head_dim + sub * E : 0;
   float mn[kPageSlots][E], mx[kPageSlots][E];
@@ -480,30 +493,32 @@ static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, con
 
 }  // namespace nhs
 
-extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
-                                int64_t q_head_stride, const void* minimum, const void* maximum,
-                                int32_t bounds_dtype, int64_t bounds_batch_stride, int32_t q_heads, int32_t kv_heads,
-                                int32_t head_dim, const int64_t* lengths, int64_t length, int32_t page_size,
-                                int32_t max_pages, int32_t top_pages, int32_t keep_sink, float* scores,
-                                int32_t* pages, int32_t* positions, void* stream) {
-  using namespace nhs;
+namespace nhs {
+
+// nhs_quest_select and nhs_quest_select_items: strided bounds (minimum,
+// maximum, bounds_batch_stride) or per-item bounds (items).
+static int quest_select(const char* who, int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                        int64_t q_head_stride, const void* minimum, const void* maximum, int64_t bounds_batch_stride,
+                        const nhs_layer_item* items, int32_t bounds_dtype, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, const int64_t* lengths, int64_t length, int32_t page_size,
+                        int32_t max_pages, int32_t top_pages, int32_t keep_sink, float* scores, int32_t* pages,
+                        int32_t* positions, void* stream) {
   LaunchEvents ev = take_launch_events();
-  const char* who = "nhs_quest_select";
   int st = check_select_common(who, batch, query, q_dtype, q_heads, kv_heads, head_dim, lengths, length, page_size,
                                max_pages, top_pages, scores, pages, positions);
   if (st != NHS_OK) return st;
-  if (!minimum || !maximum) return fail(NHS_ERR_INVALID, "%s: null bounds", who);
+  if (items ? !lengths : (!minimum || !maximum)) return fail(NHS_ERR_INVALID, "%s: null bounds", who);
   if (!valid_dtype(bounds_dtype)) return fail(NHS_ERR_INVALID, "%s: bad bounds dtype", who);
   if ((int64_t)q_heads * head_dim + 8 * q_heads > 16384)
     return fail(NHS_ERR_UNSUPPORTED, "%s: q_heads * head_dim too large", who);
   const int esize = elem_size(bounds_dtype);
   const int E = quest_chunk_elems(head_dim, esize);
   if (E == 0) return fail(NHS_ERR_UNSUPPORTED, "%s: head_dim %d unsupported", who, head_dim);
-  if (E > 1 && (((uintptr_t)minimum | (uintptr_t)maximum) % 16 || (bounds_batch_stride * esize) % 16))
+  if (!items && E > 1 && (((uintptr_t)minimum | (uintptr_t)maximum) % 16 || (bounds_batch_stride * esize) % 16))
     return fail(NHS_ERR_INVALID, "%s: bounds must be 16-byte aligned", who);
   if (batch == 0) return NHS_OK;
   hipStream_t s = (hipStream_t)stream;
-  ScoreArgs a;
+  ScoreArgs a{};
   a.q = query;
   a.q_dtype = q_dtype;
   {
@@ -516,6 +531,7 @@ extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtyp
   a.lo = minimum;
   a.hi = maximum;
   a.b_bs = bounds_batch_stride;
+  a.items = items;
   a.q_heads = q_heads;
   a.kv_heads = kv_heads;
   a.head_dim = head_dim;
@@ -600,6 +616,30 @@ extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtyp
   return launch_select(sa, batch, s, who, ev.start, ev.stop);
 }
 
+}  // namespace nhs
+
+extern "C" int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                                int64_t q_head_stride, const void* minimum, const void* maximum,
+                                int32_t bounds_dtype, int64_t bounds_batch_stride, int32_t q_heads, int32_t kv_heads,
+                                int32_t head_dim, const int64_t* lengths, int64_t length, int32_t page_size,
+                                int32_t max_pages, int32_t top_pages, int32_t keep_sink, float* scores,
+                                int32_t* pages, int32_t* positions, void* stream) {
+  return nhs::quest_select("nhs_quest_select", batch, query, q_dtype, q_batch_stride, q_head_stride, minimum, maximum,
+                           bounds_batch_stride, nullptr, bounds_dtype, q_heads, kv_heads, head_dim, lengths, length,
+                           page_size, max_pages, top_pages, keep_sink, scores, pages, positions, stream);
+}
+
+extern "C" int nhs_quest_select_items(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                                      int64_t q_head_stride, const nhs_layer_item* items, int32_t bounds_dtype,
+                                      int32_t q_heads, int32_t kv_heads, int32_t head_dim, const int64_t* lengths,
+                                      int32_t page_size, int32_t max_pages, int32_t top_pages, int32_t keep_sink,
+                                      float* scores, int32_t* pages, int32_t* positions, void* stream) {
+  if (!items) return nhs::fail(NHS_ERR_INVALID, "nhs_quest_select_items: null items");
+  return nhs::quest_select("nhs_quest_select_items", batch, query, q_dtype, q_batch_stride, q_head_stride, nullptr,
+                           nullptr, 0, items, bounds_dtype, q_heads, kv_heads, head_dim, lengths, 0, page_size,
+                           max_pages, top_pages, keep_sink, scores, pages, positions, stream);
+}
+
 extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
                                int64_t q_head_stride, const float* summaries, int64_t summaries_batch_stride,
                                int32_t q_heads, int32_t kv_heads, int32_t head_dim, const int64_t* lengths,
@@ -619,7 +659,7 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
   if (E > 1 && (uintptr_t)summaries % 16) return fail(NHS_ERR_INVALID, "%s: summaries must be 16-byte aligned", who);
   if (batch == 0) return NHS_OK;
   hipStream_t s = (hipStream_t)stream;
-  ScoreArgs a;
+  ScoreArgs a{};
   a.q = query;
   a.q_dtype = q_dtype;
   a.q_bs = q_batch_stride;

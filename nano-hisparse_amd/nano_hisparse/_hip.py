@@ -50,8 +50,20 @@ SIGNATURES = {
         [_i32, _p, _i32, _i64, _i64, _p, _i64, _i32, _i32, _i32, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p],
         ctypes.c_int,
     ),
+    "nhs_append_items": ([_i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p], ctypes.c_int),
+    "nhs_quest_select_items": (
+        [_i32, _p, _i32, _i64, _i64, _p, _i32, _i32, _i32, _i32, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _p],
+        ctypes.c_int,
+    ),
+    "nhs_resolve_items": (
+        [_i32, _i32, _p, _i32, _i64, _p, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p],
+        ctypes.c_int,
+    ),
     "nhs_expand_columns": ([_p, _i64, _p, _i64, _i64, _p, _p], ctypes.c_int),
 }
+
+# nhs_layer_item: eight pointers and n_pages, 72 bytes
+LAYER_ITEM_FIELDS = ("source", "resident", "hot", "tags", "lru", "minimum", "maximum", "summaries", "n_pages")
 
 _lib = None
 

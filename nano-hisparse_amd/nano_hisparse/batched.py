@@ -1,0 +1,187 @@
+"""One decode token for a batch of requests, one launch per stage and layer.
+
+The reference decodes request by request (engine.py:111-121, model.py:
+182-221): per layer and request an append, a Quest selection, a resolve, a
+gather and an attention. BatchDecode runs the same stages for every request
+of the batch at once on a GPU cache: per layer one append launch
+(nhs_append_items), one Quest launch (nhs_quest_select_items), one resolver
+launch (nhs_resolve_items), one gather of the concatenated miss plans on the
+transfer stream and one attention launch over all requests' rows. Each
+request keeps its own tables; the kernels read them through a device table
+of per-(request, layer) pointers built once per batch composition.
+
+Host bookkeeping stays per request but is O(1) per request and layer:
+page placement (and the residency policy) runs only for the requests whose
+token opens a new page; events are shared by the batch; the batch's reads
+are fenced per layer (HostStore.layer_reads) instead of by per-block
+reader references, since nothing else runs on the cache between a layer's
+resolve and its attention launch.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import row_kernels as rk
+
+
+class BatchDecode:
+    """Appends and attends one decode token per request, layer by layer.
+
+    Usage: step = cache.decode_batch(ids); for each layer l in order:
+    step.append(l, k, v); out = step.attend(l, q, top_pages). Every layer
+    must be appended before it is attended; lengths advance per layer.
+    """
+
+    def __init__(self, cache, request_ids):
+        store = cache.storage
+        if not store.cuda:
+            raise RuntimeError("batched decode runs on a GPU cache (libnhs_hip.so)")
+        store.check_stream()
+        ids = list(request_ids)
+        if not ids or len(set(ids)) != len(ids):
+            raise ValueError("a batch needs distinct request IDs")
+        lengths = []
+        for rid in ids:
+            request = store.requests.get(rid)
+            if request is None:
+                raise KeyError(f"unknown request {rid}")
+            if len(set(request.lengths)) != 1 or request.lengths[0] == 0:
+                raise ValueError("all layers must have the same nonempty history")
+            if request.lengths[0] + 1 > request.max_tokens:
+                raise ValueError("decode would exceed the request's reserved tokens")
+            if any(cache.tables[rid, layer].busy for layer in range(request.layers)):
+                raise RuntimeError("cannot decode during a row lease")
+            lengths.append(request.lengths[0])
+        if len({store.requests[r].layers for r in ids}) != 1:
+            raise ValueError("requests of a batch must have the same layer count")
+        self.cache, self.ids, self.lengths = cache, ids, lengths
+        self.layers = store.requests[ids[0]].layers
+        self.items = cache._layer_items(ids)
+        self.max_pages = max(store.requests[r].page_count for r in ids)
+        both = torch.tensor([lengths, [n + 1 for n in lengths]], dtype=torch.int64)
+        self.dev_lengths = both.pin_memory().to(cache.device, non_blocking=True)
+        self._appended = set()
+
+    # ---- append --------------------------------------------------------------------------
+
+    def _place(self, layer):
+        """Place each request's page for its new token; returns the pages.
+        A failure rolls back the pages this call opened."""
+        cache, store = self.cache, self.cache.storage
+        P = cache.config.page_size
+        pages, opened = [], []
+        try:
+            for rid, length in zip(self.ids, self.lengths):
+                index = length // P
+                fresh = (rid, layer, index) not in store.pages
+                page = store.materialize(rid, layer, index)
+                if fresh:
+                    opened.append(page)
+                if page.valid_tokens:  # the active tail keeps its allocation reference
+                    if page.slot is None:
+                        raise RuntimeError("active append tail lost its resident lease")
+                    store.stats["resident_hits"] += 1
+                    store.stats["append_resident_hits"] += 1
+                else:
+                    try:
+                        cache._prepare_append(page)
+                    finally:
+                        cache._writing_key = None
+                for ev in (page.ready, page.last_use, page.host_ready):
+                    if ev is not None and getattr(ev, "stream", None) != store.compute:
+                        store.wait(store.compute, ev)
+                pages.append(page)
+        except Exception:
+            for page in reversed(opened):
+                if page.slot is not None:
+                    cache._detach(page)
+                    cache.tables[page.key[:2]].source[page.key[2]] = -1
+                store._unmaterialize(page)
+            raise
+        return pages
+
+    @torch.inference_mode()
+    def append(self, layer, k, v):
+        """k, v: [B, kv_heads, head_dim] in the cache dtype, on its device."""
+        cache, store = self.cache, self.cache.storage
+        cfg = cache.config
+        B = len(self.ids)
+        if layer in self._appended or not 0 <= layer < self.layers:
+            raise ValueError("each layer is appended once per step")
+        if k.shape != (B, cfg.kv_heads, cfg.head_dim) or v.shape != k.shape:
+            raise ValueError(f"expected [{B}, {cfg.kv_heads}, {cfg.head_dim}] K/V")
+        if k.dtype != cfg.dtype or v.dtype != cfg.dtype or k.device != cache.pool.device:
+            raise ValueError("K/V dtype/device must match the cache")
+        k, v = k.contiguous(), v.contiguous()
+        pages = self._place(layer)
+        rk.append_items(k, v, cache.pool, store.host_alias, self.items[layer], self.dev_lengths[0])
+        written = store.event(store.compute)
+        P = cfg.page_size
+        row_bytes = store.page_bytes // P
+        for rid, length, page in zip(self.ids, self.lengths, pages):
+            page.valid_tokens = length % P + 1
+            page.content_version += 1
+            page.sealed = page.valid_tokens == P
+            page.ready = page.host_ready = written
+            page.host_enqueued_version = page.content_version
+            store.requests[rid].lengths[layer] = length + 1
+            cache.pending_clean.add(page.key)
+        store.stats["d2h_bytes"] += row_bytes * B
+        self._appended.add(layer)
+        cache.update_residency()
+
+    # ---- attention -----------------------------------------------------------------------
+
+    @torch.inference_mode()
+    def attend(self, layer, query, top_pages, keep_sink=True):
+        """query [B, q_heads, head_dim] -> [B, q_heads, head_dim]: Quest
+        top_pages selection, resolve, gather and row attention for every
+        request of the batch."""
+        cache, store = self.cache, self.cache.storage
+        cfg = cache.config
+        if layer not in self._appended:
+            raise ValueError("append the layer's token before attending")
+        if query.ndim != 3 or query.shape[0] != len(self.ids) or query.shape[2] != cfg.head_dim:
+            raise ValueError("query must be [B, q_heads, head_dim]")
+        if query.shape[1] % cfg.kv_heads or query.device != cache.pool.device:
+            raise ValueError("query GQA/device mismatch")
+        if top_pages < 1:
+            raise ValueError("top_pages must be positive")
+        if top_pages * cfg.page_size > cache.hot_config.max_union_rows:
+            raise ValueError("top-k width/union exceeds the admitted max_union_rows")
+        query = query.contiguous()
+        items, lengths = self.items[layer], self.dev_lengths[1]
+        tables = [cache.tables[rid, layer] for rid in self.ids]
+        _, positions, _ = rk.quest_items(
+            query, items, cfg.dtype, cfg.kv_heads, lengths, cfg.page_size, self.max_pages, top_pages, keep_sink
+        )
+        _wait_all(store, store.compute, (t.ready for t in tables))
+        physical, miss_host, miss_device, _ = rk.resolve_items(
+            positions, items, cache.hot_config.hot_rows, lengths, cfg.page_size, counts_total=cache.row_stats
+        )
+        resolved = store.event(store.compute)
+        store.wait(store.transfer, resolved)
+        _wait_all(store, store.transfer, (t.last_use for t in tables))
+        with store.context(store.transfer):
+            rk.gather_plan(store.host_alias, cache.pool, miss_host.view(-1), miss_device.view(-1), cfg.page_size)
+        miss_host.record_stream(store.transfer)
+        miss_device.record_stream(store.transfer)
+        gathered = store.event(store.transfer)
+        store.wait(store.compute, gathered)
+        out = rk.attend_batched(query, cache.pool, physical, cfg.page_size)
+        done = store.event(store.compute)
+        for rid, t in zip(self.ids, tables):
+            t.ready, t.last_use = gathered, done
+            store.layer_reads[rid, layer] = done
+        return out
+
+
+def _wait_all(store, stream, events):
+    """Make `stream` wait for each distinct event not recorded on it."""
+    seen = set()
+    for ev in events:
+        if ev is None or id(ev) in seen or getattr(ev, "stream", None) == stream:
+            continue
+        seen.add(id(ev))
+        store.wait(stream, ev)

@@ -27,7 +27,11 @@ class Request:
 
 
 class Engine:
-    def __init__(self, model: Model, cache, top_k=None, backend="auto", eos_token_id=None, selector="quest"):
+    def __init__(self, model: Model, cache, top_k=None, backend="auto", eos_token_id=None, selector="quest",
+                 batch_decode=False):
+        """batch_decode=True gives all running requests their decode turn in
+        one Model.decode_batch call (GPU cache, Quest top_k); emission order
+        and admission are unchanged."""
         cfg, kv = model.config, cache.config
         if (cfg.num_key_value_heads, cfg.head_dim) != (kv.kv_heads, kv.head_dim):
             raise ValueError("model/cache head dimensions differ")
@@ -38,6 +42,9 @@ class Engine:
         self.model, self.cache, self.top_k, self.backend = model, cache, top_k, backend
         self.eos_token_id = eos_token_id
         self.selector = selector
+        if batch_decode and (top_k is None or selector != "quest" or not cache.storage.cuda):
+            raise ValueError("batched decode needs a GPU cache and the Quest selector with a top_k")
+        self.batch_decode = batch_decode
         self.requests: dict = {}
         self.waiting: deque = deque()
         self.running: deque = deque()
@@ -61,8 +68,9 @@ class Engine:
         self.waiting.append(request)
         return request
 
-    def _emit(self, request, logits):
-        token = int(logits.argmax().item())
+    def _emit(self, request, logits=None, token=None):
+        if token is None:
+            token = int(logits.argmax().item())
         request.generated.append(token)
         if token == self.eos_token_id or len(request.generated) >= request.max_new_tokens:
             request.finished = True
@@ -98,6 +106,18 @@ class Engine:
             emitted.append((request.request_id, self._emit(request, logits)))
             if not request.finished:
                 self.running.append(request)
+        if self.batch_decode and self.running:
+            batch = list(self.running)
+            self.running.clear()
+            logits = self.model.decode_batch(
+                [r.generated[-1] for r in batch], [r.request_id for r in batch], self.cache, self.top_k
+            )
+            for request, token in zip(batch, logits.argmax(-1).tolist()):
+                request.decode_count += 1
+                emitted.append((request.request_id, self._emit(request, token=token)))
+                if not request.finished:
+                    self.running.append(request)
+            return emitted
         for _ in range(len(self.running)):
             request = self.running.popleft()
             logits = self.model.decode(

@@ -134,6 +134,7 @@ class HybridKVCache:
         self._dirty: set = set()  # layers that may hold unpinnable clean history
         self._awaiting: set = set()  # layers without a hot region
         self._sweep = None  # (heap, rank cursor, group filter) while a tick runs
+        self._item_tables: dict = {}  # batch composition -> device nhs_layer_item table
         self.allocator = DeviceAllocator(config)
         self.storage = HostStore(config, self.allocator)
         self.storage.listener = self._candidate
@@ -531,6 +532,40 @@ class HybridKVCache:
             lease.release()
             raise
 
+    # ---- batched decode ---------------------------------------------------------------------
+
+    def decode_batch(self, request_ids):
+        """A BatchDecode step over `request_ids` (one new token each)."""
+        from .batched import BatchDecode
+
+        return BatchDecode(self, request_ids)
+
+    def _layer_items(self, request_ids):
+        """Device table [layers, B, nhs_layer_item] of the requests' tables,
+        cached per batch composition until one of them is released."""
+        key = tuple(request_ids)
+        items = self._item_tables.get(key)
+        if items is None:
+            from .row_kernels import layer_items
+
+            store = self.storage
+            layers = store.requests[key[0]].layers
+            rows = []
+            for layer in range(layers):
+                row = []
+                for rid in key:
+                    t, request = self.tables[rid, layer], store.requests[rid]
+                    row.append({
+                        "source": t.source, "resident": t.resident, "hot": t.hot, "tags": t.tags, "lru": t.lru,
+                        "minimum": request.minimum[layer], "maximum": request.maximum[layer],
+                        "summaries": request.summaries[layer], "n_pages": request.page_count,
+                    })
+                rows.append(row)
+            if len(self._item_tables) >= 16:
+                self._item_tables.pop(next(iter(self._item_tables)))
+            items = self._item_tables[key] = layer_items(rows, self.device)
+        return items
+
     # ---- lifetime --------------------------------------------------------------------------
 
     def release_request(self, request_id, wait=True):
@@ -550,6 +585,8 @@ class HybridKVCache:
             page = store.pages[key]
             if page.slot is not None:
                 self._detach(page)
+        for key in [k for k in self._item_tables if request_id in k]:
+            del self._item_tables[key]  # its tensors go with the request
         store.retire(request_id, keepalive=groups)
         for key in [k for k in self.tables if k[0] == request_id]:
             del self.tables[key]

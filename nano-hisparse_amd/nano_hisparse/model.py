@@ -131,6 +131,10 @@ class Model(nn.Module):
     def _project(self, layer, x, start):
         """RMSNorm, q/k/v projections and rotary embedding for tokens at
         positions start .. start + len(x) - 1."""
+        return self._project_at(layer, x, torch.arange(start, start + len(x), device=x.device))
+
+    def _project_at(self, layer, x, positions):
+        """_project for rows at arbitrary positions (an int tensor [len(x)])."""
         cfg, n = self.config, len(x)
         h = layer.input_layernorm(x)
         attn = layer.self_attn
@@ -138,7 +142,7 @@ class Model(nn.Module):
         k = attn.k_proj(h).view(n, cfg.num_key_value_heads, cfg.head_dim)
         v = attn.v_proj(h).view(n, cfg.num_key_value_heads, cfg.head_dim)
         inv_freq = cfg.rope_theta ** (-torch.arange(0, cfg.head_dim, 2, device=x.device).float() / cfg.head_dim)
-        angle = torch.arange(start, start + n, device=x.device).float()[:, None] * inv_freq[None, :]
+        angle = positions.float()[:, None] * inv_freq[None, :]
         angle = torch.cat((angle, angle), -1)[:, None, :]
         cos, sin = angle.cos().to(x.dtype), angle.sin().to(x.dtype)
 
@@ -204,3 +208,24 @@ class Model(nn.Module):
             attention = cache.attention(q[0], request_id, index, selection, backend)
             x = self._finish(layer, x, attention.unsqueeze(0))
         return self.lm_head(self.model.norm(x[0])).float()
+
+    @torch.inference_mode()
+    def decode_batch(self, tokens: list[int], request_ids: list, cache, top_k: int):
+        """One decode step for several requests at once (Quest top_k pages):
+        dense layers run on the [B, hidden] batch and the sparse stages run
+        once per layer for all requests (cache.decode_batch). Returns fp32
+        logits [B, vocab]; row b equals decode(tokens[b], request_ids[b])
+        up to the dense layers' batched arithmetic."""
+        if len(tokens) != len(request_ids):
+            raise ValueError("one token per request")
+        if top_k is None or top_k < 1:
+            raise ValueError("batched decode needs a positive Quest top_k")
+        step = cache.decode_batch(request_ids)
+        positions = torch.tensor(step.lengths, device=self.device)
+        x = self.model.embed_tokens(torch.tensor(tokens, device=self.device))
+        for index, layer in enumerate(self.model.layers):
+            q, k, v = self._project_at(layer, x, positions)
+            step.append(index, k, v)
+            attention = step.attend(index, q, top_k)
+            x = self._finish(layer, x, attention)
+        return self.lm_head(self.model.norm(x)).float()

@@ -362,3 +362,87 @@ def mean_batched(query, summaries, lengths, page_size, top_pages):
     )
     _hip.check(status, "nhs_mean_select")
     return pages, positions, scores
+
+
+# ---- batched decode over per-item tables (nhs_layer_item) ---------------------------------
+
+
+def layer_items(rows, device):
+    """Device table of nhs_layer_item entries: `rows` is a list of layers,
+    each a list of per-request dicts with the tensors named by
+    _hip.LAYER_ITEM_FIELDS (n_pages an int). Returns int64 [layers, B, 9];
+    the tensors must outlive the table."""
+    fields = _hip.LAYER_ITEM_FIELDS
+    table = []
+    for layer in rows:
+        for item in layer:
+            for name in fields[:-1]:
+                t = item[name]
+                if t.device != device or not t.is_contiguous():
+                    raise ValueError(f"layer item {name} must be a contiguous tensor on {device}")
+            table.append([item[name].data_ptr() for name in fields[:-1]] + [int(item["n_pages"])])
+    out = torch.tensor(table, dtype=torch.int64).view(len(rows), -1, len(fields))
+    return out.pin_memory().to(device, non_blocking=True)
+
+
+def append_items(k, v, pool, host, items, lengths):
+    """One token per item: k/v [B, Hkv, D] rows appended at lengths[b] of
+    each item's layer (nhs_append_items)."""
+    device = _require_gpu("append_items", k, v, pool, items, lengths)
+    B = k.shape[0]
+    if k.shape != v.shape or k.dtype != v.dtype or k.dtype != pool.dtype or k.stride() != v.stride():
+        raise ValueError("k and v must match each other and the pool")
+    row_elems = k[0].numel()
+    if row_elems != pool.shape[3] * pool.shape[4] or not k[0].is_contiguous():
+        raise ValueError("k/v rows must be contiguous [Hkv, D] rows of the pool's shape")
+    if items.shape[0] != B or lengths.shape[0] != B or lengths.dtype != torch.int64:
+        raise ValueError("one item and one int64 length per row")
+    lib = _hip.load()
+    status = lib.nhs_append_items(
+        B, _ptr(k), _ptr(v), k.stride(0), dtype_code(k.dtype), row_elems, pool.shape[2], _ptr(pool),
+        ctypes.c_void_p(host.data_ptr()) if host is not None else None, _ptr(items), _ptr(lengths),
+        _stream(device),
+    )
+    _hip.check(status, "nhs_append_items")
+
+
+def quest_items(query, items, bounds_dtype, kv_heads, lengths, page_size, max_pages, top_pages, keep_sink=True):
+    """quest_batched over per-item bounds; returns (pages, positions, scores)."""
+    device = _require_gpu("quest_items", query, items, lengths)
+    B, Hq, D = query.shape
+    if query.stride(2) != 1 or items.shape[0] != B or lengths.shape[0] != B:
+        raise ValueError("query rows must be contiguous, with one item and one length per request")
+    scores = torch.empty(B, max_pages, dtype=torch.float32, device=device)
+    pages = torch.empty(B, top_pages, dtype=torch.int32, device=device)
+    positions = torch.empty(B, top_pages * page_size, dtype=torch.int32, device=device)
+    lib = _hip.load()
+    status = lib.nhs_quest_select_items(
+        B, _ptr(query), dtype_code(query.dtype), query.stride(0), query.stride(1), _ptr(items),
+        dtype_code(bounds_dtype), Hq, kv_heads, D, _ptr(lengths), page_size, max_pages, top_pages,
+        int(bool(keep_sink)), _ptr(scores), _ptr(pages), _ptr(positions), _stream(device),
+    )
+    _hip.check(status, "nhs_quest_select_items")
+    return pages, positions, scores
+
+
+def resolve_items(positions, items, hot_rows, lengths, page_size, counts_total=None):
+    """resolve_batched over per-item tables; returns (physical, miss_host,
+    miss_device, counts)."""
+    device = _require_gpu("resolve_items", positions, items, lengths)
+    B, K = positions.shape
+    if positions.dtype not in (torch.int32, torch.int64) or positions.stride(1) != 1:
+        raise ValueError("positions must be a [B, K] int32/int64 tensor with unit stride")
+    if items.shape[0] != B or lengths.shape[0] != B:
+        raise ValueError("one item and one length per request")
+    physical = torch.empty(B, K, dtype=torch.int64, device=device)
+    miss_host = torch.empty_like(physical)
+    miss_device = torch.empty_like(physical)
+    counts = torch.empty(B, 3, dtype=torch.int64, device=device)
+    lib = _hip.load()
+    status = lib.nhs_resolve_items(
+        B, K, _ptr(positions), int(positions.dtype == torch.int64), positions.stride(0), _ptr(items), hot_rows,
+        _ptr(lengths), page_size, _ptr(physical), _ptr(miss_host), _ptr(miss_device), K, _ptr(counts),
+        _ptr(counts_total), _stream(device),
+    )
+    _hip.check(status, "nhs_resolve_items")
+    return physical, miss_host, miss_device, counts

@@ -140,6 +140,9 @@ class HostStore:
         self.pages: dict = {}
         self.group_pages: dict = {}  # (request_id, layer) -> pages in index order
         self.resident_pages: Counter = Counter()  # (request_id, layer) -> pages holding a block
+        # (request_id, layer) -> compute event of the last batched read of the
+        # layer's pages (a batched step fences reuse per layer, not per page)
+        self.layer_reads: dict = {}
         # called with each page that lost its readers or published its host
         # mirror (a residency policy's unpin candidates)
         self.listener = None
@@ -268,7 +271,7 @@ class HostStore:
         assert self.pages.get(page.key) is page
         assert page.slot is not None and page.pins == 0
         assert page.host_enqueued_version == page.content_version
-        for ev in (page.ready, page.last_use, page.host_ready):
+        for ev in (page.ready, page.last_use, page.host_ready, self.layer_reads.get(page.key[:2])):
             self.wait(self.transfer, ev)
         self.allocator.release(page.slot, self.event(self.transfer))
         page.slot, page.location = None, Location.HOST
@@ -388,17 +391,20 @@ class HostStore:
         request = self.requests[request_id]
         if any(self.pages[key].pins for key in request.keys):
             raise RuntimeError("cannot free a request with active leases")
-        retired = []
+        retired, waited = [], set()
         for key in request.keys:
             page = self.pages[key]
             assert page.slot is None, "detach resident blocks before retiring host backing"
             for ev in (page.ready, page.last_use, page.host_ready):
-                self.wait(self.transfer, ev)
+                if ev is not None and id(ev) not in waited:  # pages of a batched step share events
+                    waited.add(id(ev))
+                    self.wait(self.transfer, ev)
             retired.append(self.pages.pop(key))
         del self.requests[request_id]
         for layer in range(request.layers):
             self.group_pages.pop((request_id, layer), None)
             self.resident_pages.pop((request_id, layer), None)
+            self.wait(self.transfer, self.layer_reads.pop((request_id, layer), None))
         request.keepalive = tuple(keepalive)
         done = self.event(self.transfer)
         self.retired.append((done, request, retired))

@@ -1,0 +1,193 @@
+"""Batched decode (one launch per stage and layer for all running requests).
+
+- The per-item entry points (nhs_append_items, nhs_quest_select_items,
+  nhs_resolve_items) against their strided twins on the same tables: bounds,
+  summaries, pool and host bytes, selections, rows, plans, tags and LRU
+  bit-exact.
+- BatchDecode against the per-request cache path (write + Quest selection +
+  attention) on the same queries and K/V over many steps: identical
+  selections and host histories, attention within tolerance, invariants.
+- Engine(batch_decode=True) against the sequential engine: same tokens.
+"""
+
+import pytest
+import torch
+
+from nano_hisparse import row_kernels as rk
+from nano_hisparse.config import CacheConfig
+from nano_hisparse.engine import Engine
+from nano_hisparse.hybrid import HotConfig, HybridKVCache
+from nano_hisparse.model import Model, ModelConfig
+from nano_hisparse.selection import quest_selection
+
+
+def log_case(**kw):
+    print("case:", kw, flush=True)
+
+
+def make_cache(device, dtype=torch.float32, gpu_pages=48, P=8, Hkv=2, D=16, union=32, hot_rows=48):
+    cfg = CacheConfig(gpu_pages=gpu_pages, host_pages=512, page_size=P, kv_heads=Hkv, head_dim=D, dtype=dtype,
+                      device=device)
+    return HybridKVCache(cfg, HotConfig(union, hot_rows, resident_window_pages=6))
+
+
+def test_batched_decode_needs_a_gpu_cache(cpu_kernels):
+    cache = make_cache("cpu")
+    cache.reserve("a", 64, 1)
+    cache.write("a", 0, torch.randn(9, 2, 16), torch.randn(9, 2, 16))
+    with pytest.raises(RuntimeError, match="GPU cache"):
+        cache.decode_batch(["a"])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_item_entry_points_match_the_strided_ones(gpu, dtype):
+    log_case(test="item-kernels", dtype=str(dtype))
+    g = torch.Generator(device=gpu).manual_seed(5)
+    B, Hq, Hkv, D, P, H = 3, 8, 2, 64, 16, 64
+    n_pages = [9, 14, 6]
+    blocks = 64
+    pool = torch.randn(blocks, 2, P, Hkv, D, generator=g, device=gpu).to(dtype)
+    host = torch.zeros(64, 2, P, Hkv, D, dtype=dtype, pin_memory=True)
+    alias = rk.MappedHost(host)
+    lengths = [n * P - 3 for n in n_pages]  # the appended token lands mid-page
+    tabs = []
+    for b, n in enumerate(n_pages):
+        source = torch.arange(n, dtype=torch.int32, device=gpu) + 20 * b
+        resident = torch.randperm(blocks, generator=g, device=gpu)[:n].to(torch.int32)
+        hot = torch.randperm(blocks, generator=g, device=gpu)[: H // P].to(torch.int32)
+        tags = torch.full((H,), -1, dtype=torch.int32, device=gpu)
+        lru = torch.randperm(H, generator=g, device=gpu)
+        mn = torch.randn(n, Hkv, D, generator=g, device=gpu).to(dtype)
+        mx = mn + torch.rand(n, Hkv, D, generator=g, device=gpu).to(dtype)
+        summ = torch.randn(n, Hkv, D, generator=g, device=gpu)
+        tabs.append(dict(source=source, resident=resident, hot=hot, tags=tags, lru=lru, minimum=mn, maximum=mx,
+                         summaries=summ, n_pages=n))
+    # resident blocks must be distinct across items for the append comparison
+    used = torch.randperm(blocks, generator=g, device=gpu)[: sum(n_pages)].to(torch.int32)
+    off = 0
+    for t, n in zip(tabs, n_pages):
+        t["resident"] = used[off: off + n].clone()
+        off += n
+    ref = [{k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in t.items()} for t in tabs]
+    items = rk.layer_items([tabs], gpu)[0]
+    dev_len = torch.tensor(lengths, dtype=torch.int64, device=gpu)
+    k = torch.randn(B, Hkv, D, generator=g, device=gpu).to(dtype)
+    v = torch.randn(B, Hkv, D, generator=g, device=gpu).to(dtype)
+    ref_pool, ref_host = pool.clone(), host.clone().pin_memory()
+    ref_alias = rk.MappedHost(ref_host)
+    rk.append_items(k, v, pool, alias, items, dev_len)
+    for b, t in enumerate(ref):
+        page, within = divmod(lengths[b], P)
+        rk.append_page(k[b: b + 1], v[b: b + 1], ref_pool, int(t["resident"][page]), within, ref_alias,
+                       int(t["source"][page]), t["summaries"][page], t["minimum"][page], t["maximum"][page])
+    torch.cuda.synchronize()
+    assert torch.equal(pool.view(torch.uint8), ref_pool.view(torch.uint8))
+    assert torch.equal(host.view(torch.uint8), ref_host.view(torch.uint8))
+    for t, r in zip(tabs, ref):
+        for name in ("minimum", "maximum", "summaries"):
+            assert torch.equal(t[name].view(torch.uint8), r[name].view(torch.uint8)), name
+    # Quest over per-item bounds vs the strided kernel, request by request
+    after = dev_len + 1
+    q = torch.randn(B, Hq, D, generator=g, device=gpu).to(dtype)
+    top = 4
+    pages, positions, _ = rk.quest_items(q, items, dtype, Hkv, after, P, max(n_pages), top)
+    for b, t in enumerate(tabs):
+        e_pages, e_pos, _ = rk.quest_batched(q[b: b + 1], t["minimum"][None], t["maximum"][None],
+                                             int(after[b]), P, top)
+        assert torch.equal(pages[b], e_pages[0]) and torch.equal(positions[b], e_pos[0])
+    # resolver over per-item tables vs the strided kernel, twice (tags and LRU
+    # evolve); every other page is host-only so both steps have misses
+    for t in tabs:
+        t["resident"][0:-1:2] = -1
+    for _ in range(2):
+        before = [(t["tags"].clone(), t["lru"].clone()) for t in tabs]
+        phys, mh, md, cnt = rk.resolve_items(positions, items, H, after, P)
+        for b, t in enumerate(tabs):
+            tags, lru = before[b]
+            e = rk.resolve_batched(positions[b: b + 1], t["source"][None], t["resident"][None], t["hot"][None],
+                                   tags[None], lru[None], int(after[b]), P)
+            for got, want in zip((phys[b], mh[b], md[b], cnt[b]), (x[0] for x in e)):
+                assert torch.equal(got, want)
+            assert torch.equal(t["tags"], tags) and torch.equal(t["lru"], lru)
+
+
+def _prefill(caches, names, lengths, layers, g, device, dtype):
+    cfg = caches[0].config
+    for name, n in zip(names, lengths):
+        for c in caches:
+            c.reserve(name, n + 64, layers)
+        for layer in range(layers):
+            k = torch.randn(n, cfg.kv_heads, cfg.head_dim, generator=g, device=device).to(dtype)
+            v = torch.randn(n, cfg.kv_heads, cfg.head_dim, generator=g, device=device).to(dtype)
+            for c in caches:
+                c.write(name, layer, k, v)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_batch_decode_matches_the_per_request_cache_path(gpu, dtype, tol):
+    log_case(test="batch-decode-vs-sequential", dtype=str(dtype))
+    g = torch.Generator(device=gpu).manual_seed(11)
+    seq, bat = make_cache(gpu, dtype), make_cache(gpu, dtype)
+    names, lengths, layers, top = ["a", "b", "c"], [37, 70, 9], 2, 4
+    Hq = 4
+    _prefill((seq, bat), names, lengths, layers, g, gpu, dtype)
+    P = seq.config.page_size
+    for step in range(40):  # crosses page boundaries, transitions and hot-row reuse
+        step_b = bat.decode_batch(names)
+        for layer in range(layers):
+            k = torch.randn(3, 2, 16, generator=g, device=gpu).to(dtype)
+            v = torch.randn(3, 2, 16, generator=g, device=gpu).to(dtype)
+            q = torch.randn(3, Hq, 16, generator=g, device=gpu).to(dtype)
+            step_b.append(layer, k, v)
+            out_b = step_b.attend(layer, q, top)
+            for i, name in enumerate(names):
+                seq.write(name, layer, k[i: i + 1], v[i: i + 1])
+                request = seq.storage.requests[name]
+                sel = quest_selection(q[i], request.minimum[layer], request.maximum[layer],
+                                      request.lengths[layer], P, top)
+                out_s = seq.attention(q[i], name, layer, sel)
+                err = (out_b[i].float() - out_s.float()).abs().max().item()
+                assert err <= tol, (step, layer, name, err)
+        for c in (seq, bat):
+            c.assert_invariants()
+    for name in names:
+        for layer in range(layers):
+            ks, vs = seq.storage.host_kv(name, layer)
+            kb, vb = bat.storage.host_kv(name, layer)
+            assert torch.equal(ks.view(torch.uint8), kb.view(torch.uint8))
+            assert torch.equal(vs.view(torch.uint8), vb.view(torch.uint8))
+            rs, rb = seq.storage.requests[name], bat.storage.requests[name]
+            for field in ("minimum", "maximum", "summaries"):
+                a, b = getattr(rs, field)[layer], getattr(rb, field)[layer]
+                assert torch.equal(a.view(torch.uint8), b.view(torch.uint8)), field
+    assert bat.snapshot()["row_stats"]["misses"] > 0
+    for c in (seq, bat):
+        for name in names:
+            c.release_request(name)
+        c.assert_invariants()
+        assert not any(c.owners)
+
+
+@pytest.mark.gpu
+def test_engine_batch_decode_generates_the_sequential_tokens(gpu):
+    log_case(test="engine-batch-decode")
+    torch.manual_seed(31)
+    cfg = ModelConfig(hidden_size=64, intermediate_size=128, num_hidden_layers=2, num_attention_heads=4,
+                      num_key_value_heads=2, vocab_size=96)
+    model = Model(cfg).eval().to(gpu)
+    prompts = {"a": list(range(1, 40)), "b": list(range(5, 70)), "c": list(range(2, 19))}
+    results = []
+    for batch_decode in (False, True):
+        cache = HybridKVCache(
+            CacheConfig(gpu_pages=40, host_pages=256, page_size=4, kv_heads=2, head_dim=16, device=gpu),
+            HotConfig(16, 24, resident_window_pages=4),
+        )
+        engine = Engine(model, cache, top_k=4, batch_decode=batch_decode)
+        for name, prompt in prompts.items():
+            engine.add_request(name, prompt, 12)
+        results.append(engine.run())
+        assert not cache.storage.requests and not any(cache.owners)
+        cache.assert_invariants()
+    assert results[0] == results[1]
