@@ -25,6 +25,15 @@ Prints one JSON line.
 `--copy-calibration` instead runs a plain 256 MiB device-to-device copy three
 times: the known-size kernel that scales the FETCH_SIZE / WRITE_SIZE
 counters of a rocprofv3 --pmc run to bytes.
+
+`--workload model` instead measures whole-model greedy decode: a random-init
+Llama-3-8B-shaped decoder (32 layers, hidden 4096, 32/8 heads x 128, MLP
+14336, vocab 128256, bf16; q/k/v biases and RoPE theta 1e4 as the reference
+model) serving 8 requests with 16384-token random prompts through the engine
+with batched decode (Engine(batch_decode=True)): pages of 64, 2048 hot rows,
+Quest top-32 pages, a pool of the admission credits plus 30% of the
+history. All prompts are prefilled first (untimed); a step is one engine
+step giving every request one token.
 """
 
 from __future__ import annotations
@@ -58,6 +67,11 @@ def parse_args():
     ap.add_argument("--side-stream", action="store_true",
                     help="run the gather on a side stream ordered by events (the default with --chunks > 1)")
     ap.add_argument("--copy-calibration", action="store_true", help="run the PMC calibration copy and exit")
+    ap.add_argument("--workload", choices=("kernel", "model"), default="kernel",
+                    help="kernel: one-layer sparse decode step (default); model: whole-model batched decode")
+    ap.add_argument("--layers", type=int, default=32, help="model workload: decoder layers")
+    ap.add_argument("--prompt", type=int, default=16384, help="model workload: prompt tokens per request")
+    ap.add_argument("--requests", type=int, default=8, help="model workload: concurrent requests")
     return ap.parse_args()
 
 
@@ -242,6 +256,112 @@ def traffic_from_profile(kernel_tag):
     return None
 
 
+def run_model_decode(args):
+    """Whole-model batched decode; prints one JSON line."""
+    from math import ceil
+
+    import torch
+
+    from nano_hisparse import _hip
+    from nano_hisparse.config import CacheConfig
+    from nano_hisparse.engine import Engine
+    from nano_hisparse.hybrid import HotConfig, HybridKVCache
+    from nano_hisparse.model import Model, ModelConfig
+
+    _hip.load()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    B, L, T, K, W = args.requests, args.layers, args.prompt, args.steps, args.warmup
+    cfg = ModelConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=L,
+                      num_attention_heads=32, num_key_value_heads=8, rope_theta=10000.0)
+    t0 = time.perf_counter()
+    torch.manual_seed(args.seed)
+    default_dtype = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            model = Model(cfg).eval()
+    finally:
+        torch.set_default_dtype(default_dtype)
+    weight_bytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    print(f"[bench] model init {time.perf_counter() - t0:.1f} s, {weight_bytes / 1e9:.2f} GB of weights",
+          file=sys.stderr, flush=True)
+    P, H, top = 64, 2048, 32
+    new_tokens = B + W + K + 2  # nobody finishes before the timed steps end
+    pages = ceil((T + new_tokens) / P)
+    hot = HotConfig(H, H)
+    resident = int(0.3 * B * L * pages)
+    kv = CacheConfig(gpu_pages=B * hot.admission_blocks(P, L) + resident, host_pages=B * L * pages, page_size=P,
+                     kv_heads=8, head_dim=128, dtype=torch.bfloat16, device=str(device),
+                     index_budget_bytes=1 << 31)
+    t0 = time.perf_counter()
+    cache = HybridKVCache(kv, hot)
+    print(f"[bench] cache: {kv.gpu_pages} pool blocks ({kv.gpu_pages * kv.row_bytes * P / 2**30:.1f} GiB), "
+          f"{kv.host_pages} host pages ({kv.host_pages * kv.row_bytes * P / 2**30:.1f} GiB pinned), "
+          f"{time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    engine = Engine(model, cache, top_k=top, batch_decode=True)
+    gen = torch.Generator().manual_seed(args.seed)
+    for b in range(B):
+        engine.add_request(f"r{b}", torch.randint(0, cfg.vocab_size, (T,), generator=gen).tolist(), new_tokens)
+    t0 = time.perf_counter()
+    while engine.waiting:  # one prefill per engine step; admitted requests decode meanwhile
+        engine.step()
+        torch.cuda.synchronize()
+        print(f"[bench] admitted {B - len(engine.waiting)}/{B} at {time.perf_counter() - t0:.1f} s",
+              file=sys.stderr, flush=True)
+    for _ in range(W):
+        engine.step()
+    torch.cuda.synchronize()
+    stats0 = cache.row_stats.tolist()
+    compute = torch.cuda.current_stream(device)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(compute)
+    for _ in range(K):
+        emitted = engine.step()
+        if len(emitted) != B:
+            raise RuntimeError("a request finished inside the timed steps")
+    end.record(compute)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = start.elapsed_time(end) / K
+    resident_hits, hot_hits, misses = (a - b for a, b in zip(cache.row_stats.tolist(), stats0))
+    row_bytes = kv.row_bytes
+    selected_rows = B * L * top * P  # every context holds more than 32 pages
+    hbm_bytes = weight_bytes + selected_rows * row_bytes + B * L * pages * 8 * 128 * 2 * 2
+    pcie_bytes = misses * row_bytes / K
+    ideal_ms = 1e3 * max(hbm_bytes / HBM_PEAK, pcie_bytes / PCIE_PEAK)
+    result = {
+        "metric": METRIC,
+        "value": round(B / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, random prompt tokens)",
+        "config": {
+            "workload": f"whole-model batched greedy decode, Llama-3-8B shape ({L} layers, hidden 4096, 32q/8kv x 128, "
+            f"MLP 14336, vocab 128256), {B} requests x {T}-token prompts, page 64, hot rows 2048, Quest top-32 "
+            f"pages, pool = admission credits + 30% of history",
+            "requests": B,
+            "prompt": T,
+            "layers": L,
+            "parallelism": "single GPU",
+        },
+        "rows_per_step": {"resident_hits": resident_hits / K, "hot_hits": hot_hits / K, "misses": misses / K},
+        "pcie_gbs": round(pcie_bytes / (ms_per_step * 1e-3) / 1e9, 2),
+        "step_roofline": {"ideal_ms": round(ideal_ms, 3), "frac": round(ideal_ms / ms_per_step, 4),
+                          "hbm_bytes": hbm_bytes, "pcie_bytes": round(pcie_bytes)},
+        "wall_s_timed": round(wall, 3),
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -253,6 +373,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.workload == "model":
+        run_model_decode(args)
         return
     import torch
 
