@@ -258,6 +258,39 @@ int nhs_resolve_items(int32_t batch, int32_t n, const void* positions, int32_t p
                       void* stream);
 
 /*
+ * Elementwise stages of the batched decode layer (model.py:43-71, 140-158 of
+ * the reference run them as separate torch operations). Each computes in
+ * fp32 and rounds to the dtype wherever the torch expression rounds, so only
+ * the reduction order of the RMSNorm mean differs from torch.
+ *
+ * nhs_add_rmsnorm: per row of `width` elements, h = x + delta (rounded;
+ * delta may be NULL) is written back to x when write_back, and
+ * out = round(round(h * rsqrt(mean(h^2) + eps)) * weight)
+ * (RMSNorm.forward, model.py:49-51, after the residual add of _finish,
+ * model.py:156-158).
+ */
+int nhs_add_rmsnorm(int32_t rows, int32_t width, int32_t dtype, void* x, const void* delta, int32_t write_back,
+                    const void* weight, float eps, void* out, void* stream);
+
+/*
+ * nhs_rope: rotary embedding in place on `rows` rows of t (row_stride
+ * elements apart), each holding `heads` heads of head_dim; cos/sin are
+ * [rows, head_dim/2] in the dtype. For d < head_dim/2 with lo = t[d],
+ * hi = t[d + head_dim/2]: t[d] = round(round(lo*c) + round(-hi*s)),
+ * t[d + head_dim/2] = round(round(hi*c) + round(lo*s))
+ * (the rope closure, model.py:147-151).
+ */
+int nhs_rope(int32_t rows, int32_t heads, int32_t head_dim, int32_t dtype, void* t, int64_t row_stride,
+             const void* cos, const void* sin, void* stream);
+
+/*
+ * nhs_silu_mul: out[r, i] = round(round(silu(g)) * u) with g = gate_up[r, i],
+ * u = gate_up[r, inter + i] (MLP.forward, model.py:70-71, on a fused
+ * gate/up projection).
+ */
+int nhs_silu_mul(int32_t rows, int32_t inter, int32_t dtype, const void* gate_up, void* out, void* stream);
+
+/*
  * Legacy per-head selections: out[h, c] = columns[h, c] in [0, n) ?
  * shared_rows[columns[h, c]] : -1 for h < heads, c < width.
  * Replaces the head_columns branch of resolve_rows,

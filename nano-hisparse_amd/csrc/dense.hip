@@ -1,0 +1,181 @@
+// Elementwise stages of the batched decode layer, fused: residual add +
+// RMSNorm, rotary embedding of q and k in place, and SiLU(gate) * up. Each
+// reproduces the rounding steps of the torch expression it replaces (every
+// torch bf16/fp16 operation computes in fp32 and rounds its result to the
+// tensor dtype; separate torch operations never fuse a multiply into an
+// add, hence fp contract(off)), so only reduction order can differ.
+#include "nhs_common.h"
+
+namespace nhs {
+
+constexpr int kNormThreads = 256;
+
+template <typename T>
+__device__ __forceinline__ float rnd(float v) {
+  return T::to_float(T::from_float(v));
+}
+
+struct F32T {
+  using Bits = float;
+  __device__ static float to_float(float b) { return b; }
+  __device__ static float from_float(float v) { return v; }
+};
+struct BF16T {
+  using Bits = uint16_t;
+  __device__ static float to_float(uint16_t b) { return bf16_bits_to_f32(b); }
+  __device__ static uint16_t from_float(float v) { return f32_to_bf16_bits(v); }
+};
+struct F16T {
+  using Bits = uint16_t;
+  __device__ static float to_float(uint16_t b) { return f16_bits_to_f32(b); }
+  __device__ static uint16_t from_float(float v) { return f32_to_f16_bits(v); }
+};
+
+// h = x + delta (rounded; delta may be null), written back to x when
+// write_back; out = round(round(h * rsqrt(mean(h^2) + eps)) * weight).
+// One workgroup per row.
+template <typename T>
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(typename T::Bits* x, const typename T::Bits* delta,
+                                                                   const typename T::Bits* weight,
+                                                                   typename T::Bits* out, int width, float eps,
+                                                                   int write_back) {
+#pragma clang fp contract(off)
+  __shared__ float partial[kNormThreads / kWave];
+  const int row = blockIdx.x;
+  typename T::Bits* xr = x + (int64_t)row * width;
+  const typename T::Bits* dr = delta ? delta + (int64_t)row * width : nullptr;
+  float acc = 0.f;
+  for (int i = threadIdx.x; i < width; i += kNormThreads) {
+    float h = T::to_float(xr[i]);
+    if (dr) {
+      h = rnd<T>(h + T::to_float(dr[i]));
+      if (write_back) xr[i] = T::from_float(h);
+    }
+    acc += h * h;
+  }
+  acc = group_sum(acc, kWave);
+  if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = acc;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) total += partial[w];
+  const float r = rsqrtf(total / (float)width + eps);
+  typename T::Bits* orow = out + (int64_t)row * width;
+  for (int i = threadIdx.x; i < width; i += kNormThreads) {
+    float h = T::to_float(xr[i]);
+    if (dr && !write_back) h = rnd<T>(h + T::to_float(dr[i]));
+    orow[i] = T::from_float(rnd<T>(h * r) * T::to_float(weight[i]));
+  }
+}
+
+// Rotary embedding in place on rows of [heads, head_dim] (q heads then kv
+// heads of one fused projection row): for d < D/2 with lo = t[d],
+// hi = t[d + D/2], c = cos[row, d], s = sin[row, d]:
+//   t[d]       = round(round(lo * c) + round(-hi * s))
+//   t[d + D/2] = round(round(hi * c) + round(lo * s))
+// One thread per (row, head, d).
+template <typename T>
+__global__ void rope_kernel(typename T::Bits* t, int64_t row_stride, int heads, int half,
+                            const typename T::Bits* cos, const typename T::Bits* sin, int64_t total) {
+#pragma clang fp contract(off)
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int per_row = heads * half;
+  const int row = (int)(idx / per_row);
+  const int rem = (int)(idx - (int64_t)row * per_row);
+  const int head = rem / half, d = rem - head * half;
+  typename T::Bits* p = t + (int64_t)row * row_stride + (int64_t)head * 2 * half;
+  const float lo = T::to_float(p[d]), hi = T::to_float(p[d + half]);
+  const float c = T::to_float(cos[(int64_t)row * half + d]), s = T::to_float(sin[(int64_t)row * half + d]);
+  p[d] = T::from_float(rnd<T>(lo * c) + rnd<T>(-hi * s));
+  p[d + half] = T::from_float(rnd<T>(hi * c) + rnd<T>(lo * s));
+}
+
+// out[row, i] = round(round(silu(g)) * u), g = gu[row, i], u = gu[row, inter + i].
+template <typename T>
+__global__ void silu_mul_kernel(const typename T::Bits* gu, typename T::Bits* out, int inter, int64_t total) {
+#pragma clang fp contract(off)
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int64_t row = idx / inter;
+  const int i = (int)(idx - row * inter);
+  const float g = T::to_float(gu[row * 2 * inter + i]);
+  const float u = T::to_float(gu[row * 2 * inter + inter + i]);
+  const float s = rnd<T>(g / (1.0f + expf(-g)));
+  out[idx] = T::from_float(s * u);
+}
+
+}  // namespace nhs
+
+using namespace nhs;
+
+extern "C" int nhs_add_rmsnorm(int32_t rows, int32_t width, int32_t dtype, void* x, const void* delta,
+                               int32_t write_back, const void* weight, float eps, void* out, void* stream) {
+  const LaunchEvents ev = take_launch_events();
+  if (!x || !weight || !out) return fail(NHS_ERR_INVALID, "nhs_add_rmsnorm: null pointer");
+  if (rows < 0 || width < 1 || !valid_dtype(dtype)) return fail(NHS_ERR_INVALID, "nhs_add_rmsnorm: bad shape/dtype");
+  if (rows == 0) return NHS_OK;
+  const int wb = delta && write_back ? 1 : 0;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)rows), block(kNormThreads);
+  if (dtype == NHS_BF16)
+    launch(add_rmsnorm_kernel<BF16T>, grid, block, 0, s, ev.start, ev.stop, static_cast<uint16_t*>(x),
+           static_cast<const uint16_t*>(delta), static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
+           width, eps, wb);
+  else if (dtype == NHS_F16)
+    launch(add_rmsnorm_kernel<F16T>, grid, block, 0, s, ev.start, ev.stop, static_cast<uint16_t*>(x),
+           static_cast<const uint16_t*>(delta), static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
+           width, eps, wb);
+  else
+    launch(add_rmsnorm_kernel<F32T>, grid, block, 0, s, ev.start, ev.stop, static_cast<float*>(x),
+           static_cast<const float*>(delta), static_cast<const float*>(weight), static_cast<float*>(out), width,
+           eps, wb);
+  return launch_status("nhs_add_rmsnorm");
+}
+
+extern "C" int nhs_rope(int32_t rows, int32_t heads, int32_t head_dim, int32_t dtype, void* t, int64_t row_stride,
+                        const void* cos, const void* sin, void* stream) {
+  const LaunchEvents ev = take_launch_events();
+  if (!t || !cos || !sin) return fail(NHS_ERR_INVALID, "nhs_rope: null pointer");
+  if (rows < 0 || heads < 1 || head_dim < 2 || head_dim % 2 || !valid_dtype(dtype) ||
+      row_stride < (int64_t)heads * head_dim)
+    return fail(NHS_ERR_INVALID, "nhs_rope: bad shape/dtype");
+  if (rows == 0) return NHS_OK;
+  const int half = head_dim / 2;
+  const int64_t total = (int64_t)rows * heads * half;
+  const int threads = 256;
+  const dim3 grid((unsigned)((total + threads - 1) / threads)), block(threads);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NHS_BF16)
+    launch(rope_kernel<BF16T>, grid, block, 0, s, ev.start, ev.stop, static_cast<uint16_t*>(t), row_stride, heads,
+           half, static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin), total);
+  else if (dtype == NHS_F16)
+    launch(rope_kernel<F16T>, grid, block, 0, s, ev.start, ev.stop, static_cast<uint16_t*>(t), row_stride, heads,
+           half, static_cast<const uint16_t*>(cos), static_cast<const uint16_t*>(sin), total);
+  else
+    launch(rope_kernel<F32T>, grid, block, 0, s, ev.start, ev.stop, static_cast<float*>(t), row_stride, heads, half,
+           static_cast<const float*>(cos), static_cast<const float*>(sin), total);
+  return launch_status("nhs_rope");
+}
+
+extern "C" int nhs_silu_mul(int32_t rows, int32_t inter, int32_t dtype, const void* gate_up, void* out,
+                            void* stream) {
+  const LaunchEvents ev = take_launch_events();
+  if (!gate_up || !out) return fail(NHS_ERR_INVALID, "nhs_silu_mul: null pointer");
+  if (rows < 0 || inter < 1 || !valid_dtype(dtype)) return fail(NHS_ERR_INVALID, "nhs_silu_mul: bad shape/dtype");
+  if (rows == 0) return NHS_OK;
+  const int64_t total = (int64_t)rows * inter;
+  const int threads = 256;
+  const dim3 grid((unsigned)((total + threads - 1) / threads)), block(threads);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NHS_BF16)
+    launch(silu_mul_kernel<BF16T>, grid, block, 0, s, ev.start, ev.stop, static_cast<const uint16_t*>(gate_up),
+           static_cast<uint16_t*>(out), inter, total);
+  else if (dtype == NHS_F16)
+    launch(silu_mul_kernel<F16T>, grid, block, 0, s, ev.start, ev.stop, static_cast<const uint16_t*>(gate_up),
+           static_cast<uint16_t*>(out), inter, total);
+  else
+    launch(silu_mul_kernel<F32T>, grid, block, 0, s, ev.start, ev.stop, static_cast<const float*>(gate_up),
+           static_cast<float*>(out), inter, total);
+  return launch_status("nhs_silu_mul");
+}

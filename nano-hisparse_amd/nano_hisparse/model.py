@@ -209,23 +209,93 @@ class Model(nn.Module):
             x = self._finish(layer, x, attention.unsqueeze(0))
         return self.lm_head(self.model.norm(x[0])).float()
 
+    def _fused_projections(self):
+        """Per layer: the q/k/v weights and biases and the gate/up weights as
+        one tensor each, for one GEMM apiece in the batched decode. The
+        module parameters become views of the fused tensors (names, state
+        dicts and the per-request path are unchanged); fusing again happens
+        only if a parameter was replaced since (e.g. by .to())."""
+        fused = getattr(self, "_fused", None)
+        if fused is not None and fused[0] == self._projection_pointers():
+            return fused[1]
+        layers = []
+        for layer in self.model.layers:
+            attn, mlp = layer.self_attn, layer.mlp
+            qkv = (attn.q_proj, attn.k_proj, attn.v_proj)
+            layers.append((_fuse(qkv, "weight"), _fuse(qkv, "bias"), _fuse((mlp.gate_proj, mlp.up_proj), "weight")))
+        self._fused = (self._projection_pointers(), layers)
+        return layers
+
+    def _projection_pointers(self):
+        out = []
+        for layer in self.model.layers:
+            attn, mlp = layer.self_attn, layer.mlp
+            for m in (attn.q_proj, attn.k_proj, attn.v_proj, mlp.gate_proj, mlp.up_proj):
+                out.append(m.weight.data_ptr())
+        return out
+
     @torch.inference_mode()
     def decode_batch(self, tokens: list[int], request_ids: list, cache, top_k: int):
-        """One decode step for several requests at once (Quest top_k pages):
-        dense layers run on the [B, hidden] batch and the sparse stages run
-        once per layer for all requests (cache.decode_batch). Returns fp32
-        logits [B, vocab]; row b equals decode(tokens[b], request_ids[b])
-        up to the dense layers' batched arithmetic."""
+        """One decode step for several requests at once (Quest top_k pages).
+
+        Dense layers run on the [B, hidden] batch with fused projections
+        (one q/k/v GEMM, one gate/up GEMM) and libnhs_hip.so's fused
+        residual-add + RMSNorm, RoPE (cos/sin computed once per step) and
+        SiLU * up kernels; the sparse stages run once per layer for all
+        requests (cache.decode_batch). Returns fp32 logits [B, vocab]; row b
+        equals decode(tokens[b], request_ids[b]) up to the order of the
+        dense layers' reductions."""
+        from . import row_kernels as rk
+
         if len(tokens) != len(request_ids):
             raise ValueError("one token per request")
         if top_k is None or top_k < 1:
             raise ValueError("batched decode needs a positive Quest top_k")
+        cfg = self.config
         step = cache.decode_batch(request_ids)
+        fused = self._fused_projections()
+        B, D = len(tokens), cfg.head_dim
+        Hq, Hkv = cfg.num_attention_heads, cfg.num_key_value_heads
         positions = torch.tensor(step.lengths, device=self.device)
-        x = self.model.embed_tokens(torch.tensor(tokens, device=self.device))
+        inv_freq = cfg.rope_theta ** (-torch.arange(0, D, 2, device=self.device).float() / D)
+        angle = positions.float()[:, None] * inv_freq[None, :]
+        cos, sin = angle.cos().to(self.dtype).contiguous(), angle.sin().to(self.dtype).contiguous()
+        x = self.model.embed_tokens(torch.tensor(tokens, device=self.device)).contiguous()
+        delta = None
         for index, layer in enumerate(self.model.layers):
-            q, k, v = self._project_at(layer, x, positions)
+            qkv_w, qkv_b, gu_w = fused[index]
+            h = rk.add_rmsnorm(x, delta, layer.input_layernorm.weight, _eps(layer.input_layernorm, cfg))
+            qkv = F.linear(h, qkv_w, qkv_b)
+            rk.rope_(qkv, Hq + Hkv, D, cos, sin)
+            q = qkv[:, : Hq * D].view(B, Hq, D)
+            k = qkv[:, Hq * D: (Hq + Hkv) * D].view(B, Hkv, D)
+            v = qkv[:, (Hq + Hkv) * D:].view(B, Hkv, D)
             step.append(index, k, v)
             attention = step.attend(index, q, top_k)
-            x = self._finish(layer, x, attention)
+            o_proj = layer.self_attn.o_proj
+            o = F.linear(attention.reshape(B, -1), o_proj.weight, o_proj.bias)
+            norm2 = layer.post_attention_layernorm
+            h = rk.add_rmsnorm(x, o, norm2.weight, _eps(norm2, cfg))
+            down = layer.mlp.down_proj
+            delta = F.linear(rk.silu_mul(F.linear(h, gu_w)), down.weight, down.bias)
+        x = x + delta
         return self.lm_head(self.model.norm(x)).float()
+
+
+def _eps(norm, cfg):
+    return getattr(norm, "eps", getattr(norm, "variance_epsilon", cfg.rms_norm_eps))
+
+
+def _fuse(modules, name):
+    """Concatenate the modules' `name` parameters along dim 0 and make each
+    module's parameter a view of the result (None if any is missing)."""
+    params = [getattr(m, name) for m in modules]
+    if any(p is None for p in params):
+        return None
+    whole = torch.cat([p.detach() for p in params], 0)
+    row = 0
+    for m, p in zip(modules, params):
+        n = p.shape[0]
+        setattr(m, name, nn.Parameter(whole[row: row + n], requires_grad=p.requires_grad))
+        row += n
+    return whole

@@ -446,3 +446,50 @@ def resolve_items(positions, items, hot_rows, lengths, page_size, counts_total=N
     )
     _hip.check(status, "nhs_resolve_items")
     return physical, miss_host, miss_device, counts
+
+
+# ---- elementwise stages of the batched decode layer -------------------------------------
+
+
+def add_rmsnorm(x, delta, weight, eps, write_back=True):
+    """x [rows, width] (+ delta, written back into x when write_back) ->
+    RMSNorm(h) * weight, a new tensor."""
+    device = _require_gpu("add_rmsnorm", x, weight)
+    if x.ndim != 2 or not x.is_contiguous() or weight.shape != (x.shape[1],) or weight.dtype != x.dtype:
+        raise ValueError("add_rmsnorm: x [rows, width] contiguous, weight [width] of x's dtype")
+    if delta is not None and (delta.shape != x.shape or delta.dtype != x.dtype or not delta.is_contiguous()):
+        raise ValueError("add_rmsnorm: delta must match x")
+    out = torch.empty_like(x)
+    lib = _hip.load()
+    status = lib.nhs_add_rmsnorm(x.shape[0], x.shape[1], dtype_code(x.dtype), _ptr(x), _ptr(delta),
+                                 int(bool(write_back)), _ptr(weight), float(eps), _ptr(out), _stream(device))
+    _hip.check(status, "nhs_add_rmsnorm")
+    return out
+
+
+def rope_(t, heads, head_dim, cos, sin):
+    """Rotary embedding in place on t [rows, >= heads*head_dim] (row stride
+    t.stride(0)); cos/sin [rows, head_dim/2] in t's dtype."""
+    device = _require_gpu("rope", t, cos, sin)
+    rows = t.shape[0]
+    if t.stride(-1) != 1 or cos.shape != (rows, head_dim // 2) or sin.shape != cos.shape:
+        raise ValueError("rope: unit-stride rows and [rows, head_dim/2] cos/sin")
+    if cos.dtype != t.dtype or sin.dtype != t.dtype or not (cos.is_contiguous() and sin.is_contiguous()):
+        raise ValueError("rope: cos/sin must be contiguous in t's dtype")
+    lib = _hip.load()
+    status = lib.nhs_rope(rows, heads, head_dim, dtype_code(t.dtype), _ptr(t), t.stride(0), _ptr(cos), _ptr(sin),
+                          _stream(device))
+    _hip.check(status, "nhs_rope")
+
+
+def silu_mul(gate_up):
+    """gate_up [rows, 2*inter] -> silu(gate) * up [rows, inter]."""
+    device = _require_gpu("silu_mul", gate_up)
+    if gate_up.ndim != 2 or gate_up.shape[1] % 2 or not gate_up.is_contiguous():
+        raise ValueError("silu_mul: gate_up [rows, 2*inter] contiguous")
+    rows, inter = gate_up.shape[0], gate_up.shape[1] // 2
+    out = torch.empty(rows, inter, dtype=gate_up.dtype, device=device)
+    lib = _hip.load()
+    status = lib.nhs_silu_mul(rows, inter, dtype_code(gate_up.dtype), _ptr(gate_up), _ptr(out), _stream(device))
+    _hip.check(status, "nhs_silu_mul")
+    return out
