@@ -105,6 +105,15 @@ int nhs_gather_rows(const void* host_alias, void* pool,
                     void* stream);
 
 /*
+ * Caps the workgroups of every later nhs_gather_rows launch (process-wide;
+ * 0, the default, launches one workgroup per 16 plan entries). Each
+ * workgroup then loops over groups of entries. A few dozen workgroups reach
+ * the host link's rate; a cap leaves the other compute units to kernels that
+ * run beside the gather. No counterpart in the reference.
+ */
+int nhs_set_gather_workgroups(int32_t workgroups);
+
+/*
  * Physical-row GQA decode attention, split-K over rows with an online
  * softmax. For request b and query head h (kv head
  * h / (q_heads / kv_heads)):

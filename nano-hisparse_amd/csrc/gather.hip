@@ -4,17 +4,23 @@
 // the host and the pool layout a block is [2, page_size, kv_heads, head_dim],
 // so plane `pl` of row r starts at ((r/P)*2*P + pl*P + r%P) * plane_bytes.
 //
-// Each workgroup takes kRowsPerBlock consecutive plan entries. A thread owns
-// vector column c of every plane and issues the loads of all its rows before
-// the stores, so each lane keeps kRowsPerBlock 16-byte PCIe reads in flight.
-// Plan entries past a request's misses are -1; a workgroup whose entries are
-// all -1 returns after reading them.
+// A workgroup takes groups of kRowsPerBlock consecutive plan entries, group
+// blockIdx.x, blockIdx.x + gridDim.x, ... A thread owns vector column c of
+// every plane and issues the loads of all its rows before the stores, so
+// each lane keeps kRowsPerBlock 16-byte PCIe reads in flight. Plan entries
+// past a request's misses are -1; a group whose entries are all -1 costs
+// one read of them. The grid is capped (nhs_set_gather_workgroups): a few
+// dozen workgroups already saturate the host link, and waves that wait on
+// PCIe reads would otherwise hold compute units that concurrent kernels need.
+#include <atomic>
+
 #include "nhs_common.h"
 
 namespace nhs {
 
 constexpr int kGatherThreads = 256;
 constexpr int kRowsPerBlock = 16;  // 16 reads in flight per lane reach the copy engine's PCIe rate
+std::atomic<int> g_gather_workgroups{0};  // 0: one workgroup per group of entries
 
 template <typename V>
 __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char* __restrict__ host,
@@ -26,8 +32,11 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char*
   __shared__ int64_t src_base[kRowsPerBlock];
   __shared__ int64_t dst_base[kRowsPerBlock];
   __shared__ int live;
-  const int64_t first = (int64_t)blockIdx.x * kRowsPerBlock;
   const int64_t block_bytes = 2 * (int64_t)page_size * plane_bytes;
+  const int64_t groups = (n_entries + kRowsPerBlock - 1) / kRowsPerBlock;
+  for (int64_t group = blockIdx.x; group < groups; group += gridDim.x) {
+  const int64_t first = group * kRowsPerBlock;
+  __syncthreads();  // the previous group's bases have been read
   if (threadIdx.x == 0) live = 0;
   __syncthreads();
   if (threadIdx.x < kRowsPerBlock) {
@@ -47,7 +56,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char*
     }
   }
   __syncthreads();
-  if (live == 0) return;
+  if (live == 0) continue;  // uniform: `live` is shared
 
   int64_t sb[kRowsPerBlock], db[kRowsPerBlock];
 #pragma unroll
@@ -68,6 +77,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char*
     for (int r = 0; r < kRowsPerBlock; ++r)
       if (db[r] >= 0) *reinterpret_cast<V*>(pool + db[r] + off) = buf[r];
   }
+  }
 }
 
 }  // namespace nhs
@@ -84,8 +94,10 @@ extern "C" int nhs_gather_rows(const void* host_alias, void* pool, const int64_t
   if (n_entries == 0) return NHS_OK;
   if (plane_bytes / 4 > 0x3fffffff) return fail(NHS_ERR_UNSUPPORTED, "nhs_gather_rows: rows too wide");
   const uintptr_t align = (uintptr_t)host_alias | (uintptr_t)pool;
-  const int64_t blocks = (n_entries + kRowsPerBlock - 1) / kRowsPerBlock;
-  if (blocks > 0x7fffffff) return fail(NHS_ERR_UNSUPPORTED, "nhs_gather_rows: too many plan entries");
+  int64_t blocks = (n_entries + kRowsPerBlock - 1) / kRowsPerBlock;
+  const int cap = g_gather_workgroups.load(std::memory_order_relaxed);
+  if (cap > 0 && blocks > cap) blocks = cap;
+  if (blocks > 0x7fffffff) blocks = 0x7fffffff;
   hipStream_t s = (hipStream_t)stream;
   if (plane_bytes % 16 == 0 && align % 16 == 0) {
     launch(gather_rows_kernel<uint4>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s, ev.start, ev.stop,
@@ -99,4 +111,10 @@ extern "C" int nhs_gather_rows(const void* host_alias, void* pool, const int64_t
            (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes);
   }
   return launch_status("nhs_gather_rows");
+}
+
+extern "C" int nhs_set_gather_workgroups(int32_t workgroups) {
+  if (workgroups < 0) return nhs::fail(NHS_ERR_INVALID, "nhs_set_gather_workgroups: negative");
+  nhs::g_gather_workgroups.store(workgroups, std::memory_order_relaxed);
+  return NHS_OK;
 }

@@ -30,6 +30,7 @@ SIGNATURES = {
                          ctypes.c_int32, ctypes.c_int32, _p, ctypes.c_int64, _p, _p, _p, _p], ctypes.c_int),
     "nhs_host_device_ptr": ([_p, ctypes.POINTER(ctypes.c_void_p)], ctypes.c_int),
     "nhs_gather_rows": ([_p, _p, _p, _p, _i64, _i32, _i64, _p], ctypes.c_int),
+    "nhs_set_gather_workgroups": ([_i32], ctypes.c_int),
     "nhs_attend_workspace_bytes": ([_i32, _i32, _i32, _i32], ctypes.c_int64),
     "nhs_attend_rows": (
         [_p, _i32, _i64, _i64, _p, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64,

@@ -258,29 +258,35 @@ def test_allocation_revisits_a_group_published_late(cpu_kernels, monkeypatch):
     cache.assert_invariants()
 
 
-@pytest.mark.gpu
-def test_page_stays_pinned_until_its_mirror_event_completes(gpu):
-    cache = make("cuda:0", pages=8)
+class HeldMirror:
+    """A host mirror event that completes only when the test says so (the
+    policy only queries mirror events on this path)."""
+
+    def __init__(self):
+        self.done = False
+
+    def query(self):
+        return self.done
+
+
+def test_page_stays_pinned_until_its_mirror_event_completes(device):
+    cache = make(device, pages=8)
     cache.reserve("a", 64, 1)
     k = torch.randn(12, 1, 8, device=cache.device)
     v = torch.randn(12, 1, 8, device=cache.device)
     cache.write("a", 0, k, v)
     cache.storage.synchronize()
-    # the append kernel writes the host mirror on the compute stream; stand in
-    # for a mirror still in flight with an event held back on a side stream
+    # a mirror still in flight: its event has not completed yet
     page = cache.storage.pages["a", 0, 0]
-    side = torch.cuda.Stream()
-    with torch.cuda.stream(side):
-        torch.cuda._sleep(100_000_000)
-        pending = torch.cuda.Event()
-        pending.record(side)
-    page.host_ready, page.host_committed_version = pending, 0
+    held = HeldMirror()
+    page.host_ready, page.host_committed_version = held, 0
     cache.pending_clean.add(page.key)
     cache.transition_to_host("a", 0)
-    assert not page.host_ready.query()
     assert page.slot not in cache.allocator.reclaimable
+    assert cache.page_state(page.key)["residency"] == "dirty"
     assert cache.storage.stats["pressure_mirror_waits"] == 0
-    side.synchronize()
+    held.done = True
     cache.collect()
     assert cache.page_state(page.key)["residency"] == "clean_unpinned"
+    page.host_ready = None
     cache.assert_invariants()
