@@ -240,16 +240,17 @@ def cpu_baseline(w, steps):
     return float(np.median(times)), physical
 
 
-def traffic_from_profile(kernel_tag):
-    """HBM bytes per launch of a kernel from the committed rocprofv3 --pmc
-    summary (FETCH_SIZE and WRITE_SIZE scaled by a plain copy of known
-    size), or None when no summary is present."""
-    path = os.path.join(ROOT, "profiles", "sparse_decode_b16_ctx32k_pmc_traffic.txt")
+def traffic_from_profile(kernel_tag, name="sparse_decode_b16_ctx32k_pmc_traffic.txt", key="traffic_bytes"):
+    """Bytes per launch of a kernel from a committed rocprofv3 --pmc summary
+    (HBM bytes: FETCH_SIZE and WRITE_SIZE scaled by a plain copy of known
+    size; host-link bytes: TCC_EA0_RDREQ_IO_32B x 32), or None when no
+    summary is present."""
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             for line in f:
                 fields = line.split()
-                if len(fields) >= 3 and fields[0] == "traffic_bytes" and fields[1] == kernel_tag:
+                if len(fields) >= 3 and fields[0] == key and fields[1] == kernel_tag:
                     return int(fields[2])
     except OSError:
         pass
@@ -448,6 +449,10 @@ def main():
     # the committed PMC summary covers the default workload only
     default = (args.batch, args.context, args.seed, len(result.chunks)) == (16, 32768, 42, 1)
     traffic = traffic_from_profile("attend_kernel") if default else None
+    host_traffic = (
+        traffic_from_profile("gather_rows_kernel", "sparse_decode_b16_ctx32k_pmc_host_link.txt", "host_read_bytes")
+        if default else None
+    )
     result = {
         "metric": METRIC,
         "value": round(tokens_per_s, 1),
@@ -493,6 +498,7 @@ def main():
             "frac": round(gather_bytes / (kernel_us["gather"] * 1e-6) / PCIE_PEAK, 4),
             "measured_h2d_copy_gbs": round(max(h2d) / 1e9, 2),
             "algorithmic_bytes": gather_bytes,
+            "traffic": host_traffic,
         },
         "step_roofline": {"ideal_us": round(ideal_us, 1), "frac": round(ideal_us / (ms_per_step * 1e3), 4)},
         "quest_gbs": round(quest_bytes / (kernel_us["quest"] * 1e-6) / 1e9, 1),
