@@ -72,6 +72,8 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=32, help="model workload: decoder layers")
     ap.add_argument("--prompt", type=int, default=16384, help="model workload: prompt tokens per request")
     ap.add_argument("--requests", type=int, default=8, help="model workload: concurrent requests")
+    ap.add_argument("--micro-batches", type=int, default=1, choices=(1, 2),
+                    help="model workload: 2 pipelines two halves of the batch (gathers beside compute)")
     return ap.parse_args()
 
 
@@ -300,7 +302,7 @@ def run_model_decode(args):
     print(f"[bench] cache: {kv.gpu_pages} pool blocks ({kv.gpu_pages * kv.row_bytes * P / 2**30:.1f} GiB), "
           f"{kv.host_pages} host pages ({kv.host_pages * kv.row_bytes * P / 2**30:.1f} GiB pinned), "
           f"{time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
-    engine = Engine(model, cache, top_k=top, batch_decode=True)
+    engine = Engine(model, cache, top_k=top, batch_decode=True, micro_batches=args.micro_batches)
     gen = torch.Generator().manual_seed(args.seed)
     for b in range(B):
         engine.add_request(f"r{b}", torch.randint(0, cfg.vocab_size, (T,), generator=gen).tolist(), new_tokens)
@@ -352,6 +354,7 @@ def run_model_decode(args):
             "requests": B,
             "prompt": T,
             "layers": L,
+            "micro_batches": args.micro_batches,
             "parallelism": "single GPU",
         },
         "rows_per_step": {"resident_hits": resident_hits / K, "hot_hits": hot_hits / K, "misses": misses / K},

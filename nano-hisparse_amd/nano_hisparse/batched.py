@@ -10,12 +10,14 @@ transfer stream and one attention launch over all requests' rows. Each
 request keeps its own tables; the kernels read them through a device table
 of per-(request, layer) pointers built once per batch composition.
 
-Host bookkeeping stays per request but is O(1) per request and layer:
-page placement (and the residency policy) runs only for the requests whose
-token opens a new page; events are shared by the batch; the batch's reads
-are fenced per layer (HostStore.layer_reads) instead of by per-block
-reader references, since nothing else runs on the cache between a layer's
-resolve and its attention launch.
+Host bookkeeping stays per request but is O(1) per request and layer.
+Every layer's page for the new token is placed when the step starts (the
+residency policy, which may reclaim blocks, runs only then and once more at
+end()), so no block changes owner between a layer's resolve and its
+attention: the step's reads need no per-block reader references and are
+fenced per layer (HostStore.layer_reads) for later reuse. That also lets a
+caller interleave two steps over disjoint request sets layer by layer,
+each one's gather (transfer stream) running beside the other's compute.
 """
 
 from __future__ import annotations
@@ -29,8 +31,10 @@ class BatchDecode:
     """Appends and attends one decode token per request, layer by layer.
 
     Usage: step = cache.decode_batch(ids); for each layer l in order:
-    step.append(l, k, v); out = step.attend(l, q, top_pages). Every layer
-    must be appended before it is attended; lengths advance per layer.
+    step.append(l, k, v); out = step.attend(l, q, top_pages) (or
+    h = step.select(l, q, top_pages) ... out = step.finish(h), to run other
+    work while the gather is in flight); then step.end(). Every layer must
+    be appended before it is attended; lengths advance per layer.
     """
 
     def __init__(self, cache, request_ids):
@@ -62,36 +66,41 @@ class BatchDecode:
         both = torch.tensor([lengths, [n + 1 for n in lengths]], dtype=torch.int64)
         self.dev_lengths = both.pin_memory().to(cache.device, non_blocking=True)
         self._appended = set()
+        self._pages = self._place_all()
 
     # ---- append --------------------------------------------------------------------------
 
-    def _place(self, layer):
-        """Place each request's page for its new token; returns the pages.
-        A failure rolls back the pages this call opened."""
+    def _place_all(self):
+        """Place every layer's page for each request's new token (layer
+        major); returns pages[layer][b]. A failure rolls back the pages
+        opened here."""
         cache, store = self.cache, self.cache.storage
         P = cache.config.page_size
         pages, opened = [], []
         try:
-            for rid, length in zip(self.ids, self.lengths):
-                index = length // P
-                fresh = (rid, layer, index) not in store.pages
-                page = store.materialize(rid, layer, index)
-                if fresh:
-                    opened.append(page)
-                if page.valid_tokens:  # the active tail keeps its allocation reference
-                    if page.slot is None:
-                        raise RuntimeError("active append tail lost its resident lease")
-                    store.stats["resident_hits"] += 1
-                    store.stats["append_resident_hits"] += 1
-                else:
-                    try:
-                        cache._prepare_append(page)
-                    finally:
-                        cache._writing_key = None
-                for ev in (page.ready, page.last_use, page.host_ready):
-                    if ev is not None and getattr(ev, "stream", None) != store.compute:
-                        store.wait(store.compute, ev)
-                pages.append(page)
+            for layer in range(self.layers):
+                row = []
+                for rid, length in zip(self.ids, self.lengths):
+                    index = length // P
+                    fresh = (rid, layer, index) not in store.pages
+                    page = store.materialize(rid, layer, index)
+                    if fresh:
+                        opened.append(page)
+                    if page.valid_tokens:  # the active tail keeps its allocation reference
+                        if page.slot is None:
+                            raise RuntimeError("active append tail lost its resident lease")
+                        store.stats["resident_hits"] += 1
+                        store.stats["append_resident_hits"] += 1
+                    else:
+                        try:
+                            cache._prepare_append(page)
+                        finally:
+                            cache._writing_key = None
+                    for ev in (page.ready, page.last_use, page.host_ready):
+                        if ev is not None and getattr(ev, "stream", None) != store.compute:
+                            store.wait(store.compute, ev)
+                    row.append(page)
+                pages.append(row)
         except Exception:
             for page in reversed(opened):
                 if page.slot is not None:
@@ -114,7 +123,7 @@ class BatchDecode:
         if k.dtype != cfg.dtype or v.dtype != cfg.dtype or k.device != cache.pool.device:
             raise ValueError("K/V dtype/device must match the cache")
         k, v = k.contiguous(), v.contiguous()
-        pages = self._place(layer)
+        pages = self._pages[layer]
         rk.append_items(k, v, cache.pool, store.host_alias, self.items[layer], self.dev_lengths[0])
         written = store.event(store.compute)
         P = cfg.page_size
@@ -129,7 +138,11 @@ class BatchDecode:
             cache.pending_clean.add(page.key)
         store.stats["d2h_bytes"] += row_bytes * B
         self._appended.add(layer)
-        cache.update_residency()
+
+    def end(self):
+        """The step's residency policy tick (publishes the step's mirrors,
+        unpins clean history, serves hot-region demand)."""
+        self.cache.update_residency()
 
     # ---- attention -----------------------------------------------------------------------
 
@@ -138,6 +151,13 @@ class BatchDecode:
         """query [B, q_heads, head_dim] -> [B, q_heads, head_dim]: Quest
         top_pages selection, resolve, gather and row attention for every
         request of the batch."""
+        return self.finish(self.select(layer, query, top_pages, keep_sink))
+
+    @torch.inference_mode()
+    def select(self, layer, query, top_pages, keep_sink=True):
+        """Quest selection and resolve on the compute stream, the gather of
+        the misses enqueued on the transfer stream; returns the handle for
+        finish()."""
         cache, store = self.cache, self.cache.storage
         cfg = cache.config
         if layer not in self._appended:
@@ -168,11 +188,20 @@ class BatchDecode:
         miss_host.record_stream(store.transfer)
         miss_device.record_stream(store.transfer)
         gathered = store.event(store.transfer)
+        for t in tables:
+            t.ready = gathered
+        return layer, query, physical, gathered
+
+    @torch.inference_mode()
+    def finish(self, handle):
+        """Attention over the selected rows once their gather is done."""
+        layer, query, physical, gathered = handle
+        cache, store = self.cache, self.cache.storage
         store.wait(store.compute, gathered)
-        out = rk.attend_batched(query, cache.pool, physical, cfg.page_size)
+        out = rk.attend_batched(query, cache.pool, physical, cache.config.page_size)
         done = store.event(store.compute)
-        for rid, t in zip(self.ids, tables):
-            t.ready, t.last_use = gathered, done
+        for rid in self.ids:
+            cache.tables[rid, layer].last_use = done
             store.layer_reads[rid, layer] = done
         return out
 

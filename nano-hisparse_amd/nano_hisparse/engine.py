@@ -28,10 +28,11 @@ class Request:
 
 class Engine:
     def __init__(self, model: Model, cache, top_k=None, backend="auto", eos_token_id=None, selector="quest",
-                 batch_decode=False):
+                 batch_decode=False, micro_batches=1):
         """batch_decode=True gives all running requests their decode turn in
-        one Model.decode_batch call (GPU cache, Quest top_k); emission order
-        and admission are unchanged."""
+        one Model.decode_batch call (GPU cache, Quest top_k; micro_batches=2
+        pipelines two halves of the batch); emission order and admission are
+        unchanged."""
         cfg, kv = model.config, cache.config
         if (cfg.num_key_value_heads, cfg.head_dim) != (kv.kv_heads, kv.head_dim):
             raise ValueError("model/cache head dimensions differ")
@@ -45,6 +46,7 @@ class Engine:
         if batch_decode and (top_k is None or selector != "quest" or not cache.storage.cuda):
             raise ValueError("batched decode needs a GPU cache and the Quest selector with a top_k")
         self.batch_decode = batch_decode
+        self.micro_batches = micro_batches
         self.requests: dict = {}
         self.waiting: deque = deque()
         self.running: deque = deque()
@@ -110,7 +112,8 @@ class Engine:
             batch = list(self.running)
             self.running.clear()
             logits = self.model.decode_batch(
-                [r.generated[-1] for r in batch], [r.request_id for r in batch], self.cache, self.top_k
+                [r.generated[-1] for r in batch], [r.request_id for r in batch], self.cache, self.top_k,
+                micro_batches=self.micro_batches,
             )
             for request, token in zip(batch, logits.argmax(-1).tolist()):
                 request.decode_count += 1

@@ -235,52 +235,108 @@ class Model(nn.Module):
         return out
 
     @torch.inference_mode()
-    def decode_batch(self, tokens: list[int], request_ids: list, cache, top_k: int):
+    def decode_batch(self, tokens: list[int], request_ids: list, cache, top_k: int, micro_batches: int = 1):
         """One decode step for several requests at once (Quest top_k pages).
 
-        Dense layers run on the [B, hidden] batch with fused projections
-        (one q/k/v GEMM, one gate/up GEMM) and libnhs_hip.so's fused
-        residual-add + RMSNorm, RoPE (cos/sin computed once per step) and
-        SiLU * up kernels; the sparse stages run once per layer for all
-        requests (cache.decode_batch). Returns fp32 logits [B, vocab]; row b
-        equals decode(tokens[b], request_ids[b]) up to the order of the
-        dense layers' reductions."""
+        Dense layers run on the batch with fused projections (one q/k/v
+        GEMM, one gate/up GEMM) and libnhs_hip.so's fused residual-add +
+        RMSNorm, RoPE (cos/sin computed once per step) and SiLU * up
+        kernels; the sparse stages run once per layer for all requests
+        (cache.decode_batch). With micro_batches=2 the requests form two
+        groups that run half a layer apart, so each group's host-row gather
+        (transfer stream) runs beside the other group's layer compute; the
+        gather's grid is capped meanwhile to leave compute units to that
+        work. Returns fp32 logits [B, vocab]; row b equals decode(tokens[b],
+        request_ids[b]) up to the order of the dense layers' reductions."""
         from . import row_kernels as rk
 
         if len(tokens) != len(request_ids):
             raise ValueError("one token per request")
         if top_k is None or top_k < 1:
             raise ValueError("batched decode needs a positive Quest top_k")
-        cfg = self.config
-        step = cache.decode_batch(request_ids)
+        if micro_batches not in (1, 2):
+            raise ValueError("micro_batches must be 1 or 2")
+        n = len(tokens)
+        if n < 2:
+            micro_batches = 1
+        cuts = [0, n] if micro_batches == 1 else [0, (n + 1) // 2, n]
+        groups = [_Group(self, tokens[a:b], request_ids[a:b], cache) for a, b in zip(cuts, cuts[1:])]
         fused = self._fused_projections()
-        B, D = len(tokens), cfg.head_dim
-        Hq, Hkv = cfg.num_attention_heads, cfg.num_key_value_heads
-        positions = torch.tensor(step.lengths, device=self.device)
-        inv_freq = cfg.rope_theta ** (-torch.arange(0, D, 2, device=self.device).float() / D)
-        angle = positions.float()[:, None] * inv_freq[None, :]
-        cos, sin = angle.cos().to(self.dtype).contiguous(), angle.sin().to(self.dtype).contiguous()
-        x = self.model.embed_tokens(torch.tensor(tokens, device=self.device)).contiguous()
-        delta = None
-        for index, layer in enumerate(self.model.layers):
-            qkv_w, qkv_b, gu_w = fused[index]
-            h = rk.add_rmsnorm(x, delta, layer.input_layernorm.weight, _eps(layer.input_layernorm, cfg))
-            qkv = F.linear(h, qkv_w, qkv_b)
-            rk.rope_(qkv, Hq + Hkv, D, cos, sin)
-            q = qkv[:, : Hq * D].view(B, Hq, D)
-            k = qkv[:, Hq * D: (Hq + Hkv) * D].view(B, Hkv, D)
-            v = qkv[:, (Hq + Hkv) * D:].view(B, Hkv, D)
-            step.append(index, k, v)
-            attention = step.attend(index, q, top_k)
-            o_proj = layer.self_attn.o_proj
-            o = F.linear(attention.reshape(B, -1), o_proj.weight, o_proj.bias)
-            norm2 = layer.post_attention_layernorm
-            h = rk.add_rmsnorm(x, o, norm2.weight, _eps(norm2, cfg))
-            down = layer.mlp.down_proj
-            delta = F.linear(rk.silu_mul(F.linear(h, gu_w)), down.weight, down.bias)
-        x = x + delta
+        layers = self.model.layers
+        if len(groups) == 1:
+            g = groups[0]
+            for index, layer in enumerate(layers):
+                g.pre(index, layer, fused[index], top_k)
+                g.post(layer)
+        else:
+            a, b = groups
+            rk.set_gather_workgroups(32)
+            try:
+                a.pre(0, layers[0], fused[0], top_k)
+                b.pre(0, layers[0], fused[0], top_k)
+                for index, layer in enumerate(layers):
+                    following = index + 1 < len(layers)
+                    a.post(layer)
+                    if following:
+                        a.pre(index + 1, layers[index + 1], fused[index + 1], top_k)
+                    b.post(layer)
+                    if following:
+                        b.pre(index + 1, layers[index + 1], fused[index + 1], top_k)
+            finally:
+                rk.set_gather_workgroups(0)
+        for g in groups:
+            g.step.end()
+        x = torch.cat([g.x + g.delta for g in groups])
         return self.lm_head(self.model.norm(x)).float()
 
+
+class _Group:
+    """One batch group of decode_batch: its residual stream, RoPE tables,
+    cache step and the gather handle in flight."""
+
+    def __init__(self, model, tokens, request_ids, cache):
+        cfg = model.config
+        self.model, self.cfg = model, cfg
+        self.step = cache.decode_batch(request_ids)
+        D = cfg.head_dim
+        positions = torch.tensor(self.step.lengths, device=model.device)
+        inv_freq = cfg.rope_theta ** (-torch.arange(0, D, 2, device=model.device).float() / D)
+        angle = positions.float()[:, None] * inv_freq[None, :]
+        self.cos = angle.cos().to(model.dtype).contiguous()
+        self.sin = angle.sin().to(model.dtype).contiguous()
+        self.x = model.model.embed_tokens(torch.tensor(tokens, device=model.device)).contiguous()
+        self.delta = None
+        self.handle = None
+
+    def pre(self, index, layer, fused, top_k):
+        """Norm, projections, RoPE, append, selection; the gather is left in flight."""
+        from . import row_kernels as rk
+
+        cfg, B = self.cfg, len(self.x)
+        D, Hq, Hkv = cfg.head_dim, cfg.num_attention_heads, cfg.num_key_value_heads
+        qkv_w, qkv_b, _ = fused
+        self.gu_w = fused[2]
+        h = rk.add_rmsnorm(self.x, self.delta, layer.input_layernorm.weight, _eps(layer.input_layernorm, cfg))
+        qkv = F.linear(h, qkv_w, qkv_b)
+        rk.rope_(qkv, Hq + Hkv, D, self.cos, self.sin)
+        q = qkv[:, : Hq * D].view(B, Hq, D)
+        k = qkv[:, Hq * D: (Hq + Hkv) * D].view(B, Hkv, D)
+        v = qkv[:, (Hq + Hkv) * D:].view(B, Hkv, D)
+        self.step.append(index, k, v)
+        self.handle = self.step.select(index, q, top_k)
+
+    def post(self, layer):
+        """Attention once the gather is in, output projection, MLP."""
+        from . import row_kernels as rk
+
+        cfg, B = self.cfg, len(self.x)
+        attention = self.step.finish(self.handle)
+        o_proj = layer.self_attn.o_proj
+        o = F.linear(attention.reshape(B, -1), o_proj.weight, o_proj.bias)
+        norm2 = layer.post_attention_layernorm
+        h = rk.add_rmsnorm(self.x, o, norm2.weight, _eps(norm2, cfg))
+        down = layer.mlp.down_proj
+        self.delta = F.linear(rk.silu_mul(F.linear(h, self.gu_w)), down.weight, down.bias)
 
 def _eps(norm, cfg):
     return getattr(norm, "eps", getattr(norm, "variance_epsilon", cfg.rms_norm_eps))

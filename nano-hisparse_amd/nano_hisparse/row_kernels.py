@@ -134,6 +134,11 @@ def gather_plan(host: MappedHost, pool, miss_host, miss_device, page_size):
     _hip.check(status, "nhs_gather_rows")
 
 
+def set_gather_workgroups(workgroups):
+    """Cap the gather's grid (process-wide; 0 = uncapped)."""
+    _hip.check(_hip.load().nhs_set_gather_workgroups(int(workgroups)), "nhs_set_gather_workgroups")
+
+
 def gather_rows(host, pool, plan, config):
     """Reference signature (row_kernels.py:58-70): gather one RowPlan's misses."""
     gather_plan(host, pool, plan.miss_host_rows, plan.miss_device_rows, config.page_size)

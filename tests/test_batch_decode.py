@@ -150,6 +150,7 @@ def test_batch_decode_matches_the_per_request_cache_path(gpu, dtype, tol):
                 out_s = seq.attention(q[i], name, layer, sel)
                 err = (out_b[i].float() - out_s.float()).abs().max().item()
                 assert err <= tol, (step, layer, name, err)
+        step_b.end()
         for c in (seq, bat):
             c.assert_invariants()
     for name in names:
@@ -171,8 +172,9 @@ def test_batch_decode_matches_the_per_request_cache_path(gpu, dtype, tol):
 
 
 @pytest.mark.gpu
-def test_engine_batch_decode_generates_the_sequential_tokens(gpu):
-    log_case(test="engine-batch-decode")
+@pytest.mark.parametrize("micro_batches", [1, 2])
+def test_engine_batch_decode_generates_the_sequential_tokens(gpu, micro_batches):
+    log_case(test="engine-batch-decode", micro_batches=micro_batches)
     torch.manual_seed(31)
     cfg = ModelConfig(hidden_size=64, intermediate_size=128, num_hidden_layers=2, num_attention_heads=4,
                       num_key_value_heads=2, vocab_size=96)
@@ -184,7 +186,7 @@ def test_engine_batch_decode_generates_the_sequential_tokens(gpu):
             CacheConfig(gpu_pages=40, host_pages=256, page_size=4, kv_heads=2, head_dim=16, device=gpu),
             HotConfig(16, 24, resident_window_pages=4),
         )
-        engine = Engine(model, cache, top_k=4, batch_decode=batch_decode)
+        engine = Engine(model, cache, top_k=4, batch_decode=batch_decode, micro_batches=micro_batches)
         for name, prompt in prompts.items():
             engine.add_request(name, prompt, 12)
         results.append(engine.run())

@@ -81,8 +81,9 @@ def test_silu_mul_matches_torch(gpu, dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("micro_batches", [1, 2])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 0.15)])
-def test_fused_batched_step_matches_per_request_decode(gpu, dtype, tol):
+def test_fused_batched_step_matches_per_request_decode(gpu, dtype, tol, micro_batches):
     torch.manual_seed(7)
     cfg = ModelConfig(hidden_size=128, intermediate_size=256, num_hidden_layers=2, num_attention_heads=8,
                       num_key_value_heads=2, vocab_size=100)
@@ -99,7 +100,7 @@ def test_fused_batched_step_matches_per_request_decode(gpu, dtype, tol):
             c.reserve(name, len(prompt) + 16, cfg.num_hidden_layers)
             tokens[name] = int(model.prefill(prompt, c, name).argmax())
     for _ in range(6):
-        batch = model.decode_batch([tokens[n] for n in prompts], list(prompts), caches[1], 4)
+        batch = model.decode_batch([tokens[n] for n in prompts], list(prompts), caches[1], 4, micro_batches)
         for i, name in enumerate(prompts):
             single = model.decode(tokens[name], name, caches[0], top_k=4)
             scale = single.abs().max().item()
