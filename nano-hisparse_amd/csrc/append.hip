@@ -13,6 +13,7 @@
 namespace nhs {
 
 constexpr int kAppendThreads = 256;
+constexpr int kAppendBatch = 16;  // earlier rows loaded together for the page mean
 
 struct AppendArgs {
   const void* k;
@@ -38,7 +39,17 @@ __device__ __forceinline__ void append_element(const AppendArgs& a, int e) {
   float lo = load_elem(a.minimum, a.dtype, e);
   float hi = load_elem(a.maximum, a.dtype, e);
   double sum = 0.0;
-  for (int r = 0; r < a.within; ++r) sum += (double)load_elem(a.pool_block, a.dtype, (int64_t)r * a.row_elems + e);
+  // the earlier keys of the page, loaded kAppendBatch at a time before they
+  // are summed (in row order)
+  for (int r0 = 0; r0 < a.within; r0 += kAppendBatch) {
+    float keys[kAppendBatch];
+#pragma unroll
+    for (int j = 0; j < kAppendBatch; ++j)
+      keys[j] = r0 + j < a.within ? load_elem(a.pool_block, a.dtype, (int64_t)(r0 + j) * a.row_elems + e) : 0.f;
+#pragma unroll
+    for (int j = 0; j < kAppendBatch; ++j)
+      if (r0 + j < a.within) sum += (double)keys[j];
+  }
   for (int t = 0; t < a.count; ++t) {
     const int64_t src = (int64_t)t * a.token_stride + e;
     const int64_t row = (int64_t)(a.within + t) * a.row_elems + e;

@@ -9,6 +9,7 @@
 namespace nhs {
 
 constexpr int kNormThreads = 256;
+constexpr int kNormHeld = 32;  // elements per thread held in registers (rows up to 8192)
 
 template <typename T>
 __device__ __forceinline__ float rnd(float v) {
@@ -44,14 +45,44 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(typename T::B
   const int row = blockIdx.x;
   typename T::Bits* xr = x + (int64_t)row * width;
   const typename T::Bits* dr = delta ? delta + (int64_t)row * width : nullptr;
+  // rows of up to kNormThreads * kNormHeld elements are held in registers:
+  // every load is issued before the first store, which could alias them
+  float held[kNormHeld];
   float acc = 0.f;
-  for (int i = threadIdx.x; i < width; i += kNormThreads) {
-    float h = T::to_float(xr[i]);
-    if (dr) {
-      h = rnd<T>(h + T::to_float(dr[i]));
-      if (write_back) xr[i] = T::from_float(h);
+  const bool in_regs = width <= kNormThreads * kNormHeld;
+  if (in_regs) {
+#pragma unroll
+    for (int j = 0; j < kNormHeld; ++j) {
+      const int i = threadIdx.x + j * kNormThreads;
+      held[j] = i < width ? T::to_float(xr[i]) : 0.f;
     }
-    acc += h * h;
+    if (dr) {
+      float dv[kNormHeld];
+#pragma unroll
+      for (int j = 0; j < kNormHeld; ++j) {
+        const int i = threadIdx.x + j * kNormThreads;
+        dv[j] = i < width ? T::to_float(dr[i]) : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kNormHeld; ++j) held[j] = rnd<T>(held[j] + dv[j]);
+      if (write_back)
+#pragma unroll
+        for (int j = 0; j < kNormHeld; ++j) {
+          const int i = threadIdx.x + j * kNormThreads;
+          if (i < width) xr[i] = T::from_float(held[j]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kNormHeld; ++j) acc += held[j] * held[j];
+  } else {
+    for (int i = threadIdx.x; i < width; i += kNormThreads) {
+      float h = T::to_float(xr[i]);
+      if (dr) {
+        h = rnd<T>(h + T::to_float(dr[i]));
+        if (write_back) xr[i] = T::from_float(h);
+      }
+      acc += h * h;
+    }
   }
   acc = group_sum(acc, kWave);
   if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = acc;
@@ -61,10 +92,24 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(typename T::B
   for (int w = 0; w < kNormThreads / kWave; ++w) total += partial[w];
   const float r = rsqrtf(total / (float)width + eps);
   typename T::Bits* orow = out + (int64_t)row * width;
-  for (int i = threadIdx.x; i < width; i += kNormThreads) {
-    float h = T::to_float(xr[i]);
-    if (dr && !write_back) h = rnd<T>(h + T::to_float(dr[i]));
-    orow[i] = T::from_float(rnd<T>(h * r) * T::to_float(weight[i]));
+  if (in_regs) {
+    float wv[kNormHeld];
+#pragma unroll
+    for (int j = 0; j < kNormHeld; ++j) {
+      const int i = threadIdx.x + j * kNormThreads;
+      wv[j] = i < width ? T::to_float(weight[i]) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kNormHeld; ++j) {
+      const int i = threadIdx.x + j * kNormThreads;
+      if (i < width) orow[i] = T::from_float(rnd<T>(held[j] * r) * wv[j]);
+    }
+  } else {
+    for (int i = threadIdx.x; i < width; i += kNormThreads) {
+      float h = T::to_float(xr[i]);
+      if (dr && !write_back) h = rnd<T>(h + T::to_float(dr[i]));
+      orow[i] = T::from_float(rnd<T>(h * r) * T::to_float(weight[i]));
+    }
   }
 }
 

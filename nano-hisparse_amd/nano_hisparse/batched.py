@@ -37,7 +37,12 @@ class BatchDecode:
     be appended before it is attended; lengths advance per layer.
     """
 
-    def __init__(self, cache, request_ids):
+    def __init__(self, cache, request_ids, overlap=False):
+        """overlap=True puts each layer's gather on the cache's transfer
+        stream, ordered by events, for callers that run other work beside
+        it; by default it runs in order on the compute stream (a gather
+        that nothing runs beside gains nothing from a second queue and would
+        pay two cross-queue event hops per layer)."""
         store = cache.storage
         if not store.cuda:
             raise RuntimeError("batched decode runs on a GPU cache (libnhs_hip.so)")
@@ -60,12 +65,15 @@ class BatchDecode:
         if len({store.requests[r].layers for r in ids}) != 1:
             raise ValueError("requests of a batch must have the same layer count")
         self.cache, self.ids, self.lengths = cache, ids, lengths
+        self.overlap = overlap
+        self._written = []  # pages appended this step
         self.layers = store.requests[ids[0]].layers
         self.items = cache._layer_items(ids)
         self.max_pages = max(store.requests[r].page_count for r in ids)
         both = torch.tensor([lengths, [n + 1 for n in lengths]], dtype=torch.int64)
         self.dev_lengths = both.pin_memory().to(cache.device, non_blocking=True)
         self._appended = set()
+        self._attended = set()
         self._pages = self._place_all()
 
     # ---- append --------------------------------------------------------------------------
@@ -122,27 +130,40 @@ class BatchDecode:
             raise ValueError(f"expected [{B}, {cfg.kv_heads}, {cfg.head_dim}] K/V")
         if k.dtype != cfg.dtype or v.dtype != cfg.dtype or k.device != cache.pool.device:
             raise ValueError("K/V dtype/device must match the cache")
-        k, v = k.contiguous(), v.contiguous()
+        if not (k[0].is_contiguous() and v[0].is_contiguous() and k.stride() == v.stride()):
+            k, v = k.contiguous(), v.contiguous()  # rows may be views of a fused projection
         pages = self._pages[layer]
         rk.append_items(k, v, cache.pool, store.host_alias, self.items[layer], self.dev_lengths[0])
-        written = store.event(store.compute)
         P = cfg.page_size
         row_bytes = store.page_bytes // P
         for rid, length, page in zip(self.ids, self.lengths, pages):
             page.valid_tokens = length % P + 1
             page.content_version += 1
             page.sealed = page.valid_tokens == P
-            page.ready = page.host_ready = written
             page.host_enqueued_version = page.content_version
             store.requests[rid].lengths[layer] = length + 1
-            cache.pending_clean.add(page.key)
+        self._written.extend(pages)
         store.stats["d2h_bytes"] += row_bytes * B
         self._appended.add(layer)
 
     def end(self):
-        """The step's residency policy tick (publishes the step's mirrors,
-        unpins clean history, serves hot-region demand)."""
-        self.cache.update_residency()
+        """Close the step: one compute-stream event, recorded after every
+        launch of the step, becomes the appended pages' write and mirror
+        event and the read fence of every layer the step read (nothing
+        changes blocks mid-step, so per-layer events would only add queue
+        markers); then the residency policy tick (publishes mirrors, unpins
+        clean history, serves hot-region demand)."""
+        cache, store = self.cache, self.cache.storage
+        done = store.event(store.compute)
+        for page in self._written:
+            page.ready = page.host_ready = done
+            cache.pending_clean.add(page.key)
+        for rid in self.ids:
+            for layer in self._attended:
+                cache.tables[rid, layer].last_use = done
+                store.layer_reads[rid, layer] = done
+        self._written = []
+        cache.update_residency()
 
     # ---- attention -----------------------------------------------------------------------
 
@@ -155,9 +176,9 @@ class BatchDecode:
 
     @torch.inference_mode()
     def select(self, layer, query, top_pages, keep_sink=True):
-        """Quest selection and resolve on the compute stream, the gather of
-        the misses enqueued on the transfer stream; returns the handle for
-        finish()."""
+        """Quest selection and resolve on the compute stream, then the gather
+        of the misses (on the transfer stream with overlap); returns the
+        handle for finish()."""
         cache, store = self.cache, self.cache.storage
         cfg = cache.config
         if layer not in self._appended:
@@ -170,7 +191,8 @@ class BatchDecode:
             raise ValueError("top_pages must be positive")
         if top_pages * cfg.page_size > cache.hot_config.max_union_rows:
             raise ValueError("top-k width/union exceeds the admitted max_union_rows")
-        query = query.contiguous()
+        if query.stride(2) != 1:
+            query = query.contiguous()
         items, lengths = self.items[layer], self.dev_lengths[1]
         tables = [cache.tables[rid, layer] for rid in self.ids]
         _, positions, _ = rk.quest_items(
@@ -180,6 +202,11 @@ class BatchDecode:
         physical, miss_host, miss_device, _ = rk.resolve_items(
             positions, items, cache.hot_config.hot_rows, lengths, cfg.page_size, counts_total=cache.row_stats
         )
+        if not self.overlap:
+            rk.gather_plan(store.host_alias, cache.pool, miss_host.view(-1), miss_device.view(-1), cfg.page_size)
+            for t in tables:
+                t.ready = None  # in order on the compute stream
+            return layer, query, physical, None
         resolved = store.event(store.compute)
         store.wait(store.transfer, resolved)
         _wait_all(store, store.transfer, (t.last_use for t in tables))
@@ -199,10 +226,7 @@ class BatchDecode:
         cache, store = self.cache, self.cache.storage
         store.wait(store.compute, gathered)
         out = rk.attend_batched(query, cache.pool, physical, cache.config.page_size)
-        done = store.event(store.compute)
-        for rid in self.ids:
-            cache.tables[rid, layer].last_use = done
-            store.layer_reads[rid, layer] = done
+        self._attended.add(layer)
         return out
 
 

@@ -534,11 +534,11 @@ class HybridKVCache:
 
     # ---- batched decode ---------------------------------------------------------------------
 
-    def decode_batch(self, request_ids):
+    def decode_batch(self, request_ids, overlap=False):
         """A BatchDecode step over `request_ids` (one new token each)."""
         from .batched import BatchDecode
 
-        return BatchDecode(self, request_ids)
+        return BatchDecode(self, request_ids, overlap)
 
     def _layer_items(self, request_ids):
         """Device table [layers, B, nhs_layer_item] of the requests' tables,

@@ -260,7 +260,8 @@ class Model(nn.Module):
         if n < 2:
             micro_batches = 1
         cuts = [0, n] if micro_batches == 1 else [0, (n + 1) // 2, n]
-        groups = [_Group(self, tokens[a:b], request_ids[a:b], cache) for a, b in zip(cuts, cuts[1:])]
+        overlap = len(cuts) > 2
+        groups = [_Group(self, tokens[a:b], request_ids[a:b], cache, overlap) for a, b in zip(cuts, cuts[1:])]
         fused = self._fused_projections()
         layers = self.model.layers
         if len(groups) == 1:
@@ -294,17 +295,18 @@ class _Group:
     """One batch group of decode_batch: its residual stream, RoPE tables,
     cache step and the gather handle in flight."""
 
-    def __init__(self, model, tokens, request_ids, cache):
+    def __init__(self, model, tokens, request_ids, cache, overlap):
         cfg = model.config
         self.model, self.cfg = model, cfg
-        self.step = cache.decode_batch(request_ids)
+        self.step = cache.decode_batch(request_ids, overlap)
         D = cfg.head_dim
-        positions = torch.tensor(self.step.lengths, device=model.device)
+        positions = self.step.dev_lengths[0]  # already on the device
         inv_freq = cfg.rope_theta ** (-torch.arange(0, D, 2, device=model.device).float() / D)
         angle = positions.float()[:, None] * inv_freq[None, :]
         self.cos = angle.cos().to(model.dtype).contiguous()
         self.sin = angle.sin().to(model.dtype).contiguous()
-        self.x = model.model.embed_tokens(torch.tensor(tokens, device=model.device)).contiguous()
+        ids = torch.tensor(tokens, dtype=torch.int64).pin_memory().to(model.device, non_blocking=True)
+        self.x = model.model.embed_tokens(ids).contiguous()
         self.delta = None
         self.handle = None
 

@@ -125,9 +125,10 @@ def _prefill(caches, names, lengths, layers, g, device, dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("overlap", [False, True])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
-def test_batch_decode_matches_the_per_request_cache_path(gpu, dtype, tol):
-    log_case(test="batch-decode-vs-sequential", dtype=str(dtype))
+def test_batch_decode_matches_the_per_request_cache_path(gpu, dtype, tol, overlap):
+    log_case(test="batch-decode-vs-sequential", dtype=str(dtype), overlap=overlap)
     g = torch.Generator(device=gpu).manual_seed(11)
     seq, bat = make_cache(gpu, dtype), make_cache(gpu, dtype)
     names, lengths, layers, top = ["a", "b", "c"], [37, 70, 9], 2, 4
@@ -135,7 +136,7 @@ def test_batch_decode_matches_the_per_request_cache_path(gpu, dtype, tol):
     _prefill((seq, bat), names, lengths, layers, g, gpu, dtype)
     P = seq.config.page_size
     for step in range(40):  # crosses page boundaries, transitions and hot-row reuse
-        step_b = bat.decode_batch(names)
+        step_b = bat.decode_batch(names, overlap)
         for layer in range(layers):
             k = torch.randn(3, 2, 16, generator=g, device=gpu).to(dtype)
             v = torch.randn(3, 2, 16, generator=g, device=gpu).to(dtype)
