@@ -1,5 +1,15 @@
 """Full-size decode workloads on the GPU against the C oracle.
 
+- CPU plumbing config: a random-init 2-layer decoder (hidden 256, 4/2 heads
+  of 64, MLP 688, vocab 32000, fp32, seed 42), 3 prompts of 512 seeded
+  random tokens, pages of 16, Quest top-8 pages (sink and last page inside
+  the 8), 64 greedy tokens each, round robin. The configured hot buffer of
+  64 rows is below the 128-row selection and fails HotConfig, so hot rows =
+  128 (the reference's minimum legal value); a pool of exactly one hot
+  region + 2 tails per layer would admit one request at a time, so the pool
+  is 3x that. The GPU engine must generate the CPU (oracle) engine's tokens
+  and row counters.
+
 - Resolver stress: 64 requests with Qwen2-7B heads (28 query / 4 KV heads x
   128, bf16), contexts uniform in [4096, 65536], pages of 32, a 1024-row
   budget (32 pages), 2048 hot rows per request all occupied, 16 decode steps
@@ -23,6 +33,53 @@ from nano_hisparse import row_kernels as rk
 
 def log_case(**kw):
     print("case:", kw, flush=True)
+
+
+def run_plumbing_config(device):
+    from nano_hisparse.config import CacheConfig
+    from nano_hisparse.engine import Engine
+    from nano_hisparse.hybrid import HotConfig, HybridKVCache
+    from nano_hisparse.model import Model, ModelConfig
+
+    torch.manual_seed(42)
+    cfg = ModelConfig(vocab_size=32000, hidden_size=256, intermediate_size=688, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2)
+    model = Model(cfg).eval().to(device)  # initialised on the CPU: same weights everywhere
+    P, top, T, new = 16, 8, 512, 64
+    hot = HotConfig(top * P, top * P)
+    g = torch.Generator().manual_seed(42)
+    prompts = [torch.randint(0, cfg.vocab_size, (T,), generator=g).tolist() for _ in range(3)]
+    kv = CacheConfig(gpu_pages=3 * hot.admission_blocks(P, cfg.num_hidden_layers),
+                     host_pages=3 * cfg.num_hidden_layers * -(-(T + new) // P), page_size=P, kv_heads=2,
+                     head_dim=64, device=str(device))
+    cache = HybridKVCache(kv, hot)
+    engine = Engine(model, cache, top_k=top)
+    for i, prompt in enumerate(prompts):
+        engine.add_request(f"p{i}", prompt, new)
+    out = engine.run()
+    cache.assert_invariants()
+    return out, cache.snapshot()["row_stats"]
+
+
+def test_plumbing_config_runs_on_the_oracle(cpu_kernels):
+    out, stats = run_plumbing_config("cpu")
+    assert sorted(out) == ["p0", "p1", "p2"] and all(len(v) == 64 for v in out.values())
+    assert stats["misses"] > 0 and stats["hot_hits"] > 0
+
+
+@pytest.mark.gpu
+def test_plumbing_config_matches_the_oracle_engine(gpu):
+    log_case(test="plumbing-config")
+    import cpu_provider
+
+    cpu_provider.install()
+    try:
+        want, want_stats = run_plumbing_config("cpu")
+    finally:
+        cpu_provider.uninstall()
+    got, got_stats = run_plumbing_config(gpu)
+    assert got == want
+    assert got_stats == want_stats
 
 
 @pytest.mark.gpu
