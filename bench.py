@@ -67,8 +67,9 @@ def parse_args():
     ap.add_argument("--side-stream", action="store_true",
                     help="run the gather on a side stream ordered by events (the default with --chunks > 1)")
     ap.add_argument("--copy-calibration", action="store_true", help="run the PMC calibration copy and exit")
-    ap.add_argument("--workload", choices=("kernel", "model"), default="kernel",
-                    help="kernel: one-layer sparse decode step (default); model: whole-model batched decode")
+    ap.add_argument("--workload", choices=("kernel", "miss-heavy", "model"), default="kernel",
+                    help="kernel: one-layer sparse decode step (default); miss-heavy: the same step at batch 4, "
+                    "128K context, 4096-row budget, ~90%% of rows gathered; model: whole-model batched decode")
     ap.add_argument("--layers", type=int, default=32, help="model workload: decoder layers")
     ap.add_argument("--prompt", type=int, default=16384, help="model workload: prompt tokens per request")
     ap.add_argument("--requests", type=int, default=8, help="model workload: concurrent requests")
@@ -79,15 +80,18 @@ def parse_args():
 
 class Workload:
     q_heads, kv_heads, head_dim, page = 32, 8, 128, 64
-    top_pages = 32
-    resident_pages, hot_pages = 16, 8  # of the selected pages; the rest miss
 
-    def __init__(self, batch, context, seed, device):
+    def __init__(self, batch, context, seed, device, top_pages=32, resident_pages=16, hot_pages=8,
+                 page_offset_std=0.0):
+        """Selected pages: resident_pages resident (the last two among them),
+        hot_pages in the hot buffer, the rest missing. page_offset_std adds a
+        per-page N(0, std) offset to K and V so Quest scores spread out."""
         import torch
 
         from nano_hisparse import row_kernels as rk
         from nano_hisparse.batch_step import BatchTables
 
+        self.top_pages, self.resident_pages, self.hot_pages = top_pages, resident_pages, hot_pages
         self.batch, self.context, self.device = batch, context, device
         B, Hq, Hkv, D, P = batch, self.q_heads, self.kv_heads, self.head_dim, self.page
         n_pages = context // P
@@ -102,7 +106,10 @@ class Workload:
         mx = torch.empty_like(mn)
         chunk = 256
         for start in range(0, B * n_pages, chunk):
-            blk = torch.randn(min(chunk, B * n_pages - start), 2, P, Hkv, D, generator=gen, device=device).to(dtype)
+            blk = torch.randn(min(chunk, B * n_pages - start), 2, P, Hkv, D, generator=gen, device=device)
+            if page_offset_std:
+                blk += page_offset_std * torch.randn(blk.shape[0], 1, 1, 1, 1, generator=gen, device=device)
+            blk = blk.to(dtype)
             self.host[start : start + blk.shape[0]].copy_(blk)
             flat_mn = mn.view(B * n_pages, Hkv, D)
             flat_mx = mx.view(B * n_pages, Hkv, D)
@@ -389,8 +396,15 @@ def main():
     _hip.load()
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    miss_heavy = args.workload == "miss-heavy"
+    if miss_heavy:
+        args.batch, args.context = 4, 131072
     print(f"[bench] building workload batch={args.batch} context={args.context}", file=sys.stderr, flush=True)
-    w = Workload(args.batch, args.context, args.seed, device)
+    if miss_heavy:  # the two tail pages resident, 4 pages hot, 58 of 64 missing
+        w = Workload(args.batch, args.context, args.seed, device, top_pages=64, resident_pages=2, hot_pages=4,
+                     page_offset_std=0.5)
+    else:
+        w = Workload(args.batch, args.context, args.seed, device)
     compute = torch.cuda.current_stream(device)
     step = SparseDecodeBatch(w.pool, w.host, w.tables, w.page, w.top_pages, chunks=args.chunks, compute=compute,
                              transfer=torch.cuda.Stream(device=device) if args.side_stream else None)
@@ -450,7 +464,7 @@ def main():
     # ideal step: every HBM byte at the HBM peak, or every host byte at the PCIe peak
     ideal_us = 1e6 * max((attn_bytes + quest_bytes + gather_bytes) / HBM_PEAK, gather_bytes / PCIE_PEAK)
     # the committed PMC summary covers the default workload only
-    default = (args.batch, args.context, args.seed, len(result.chunks)) == (16, 32768, 42, 1)
+    default = not miss_heavy and (args.batch, args.context, args.seed, len(result.chunks)) == (16, 32768, 42, 1)
     traffic = traffic_from_profile("attend_kernel") if default else None
     host_traffic = (
         traffic_from_profile("gather_rows_kernel", "sparse_decode_b16_ctx32k_pmc_host_link.txt", "host_read_bytes")
@@ -470,9 +484,15 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "sparse decode step of one layer (quest select + resolve + host-row gather + attention), "
-            "Llama-3-8B heads 32q/8kv/128, bf16, page 64, 32 pages = 2048 rows selected of 32768, "
-            "selected pages 50% resident / 25% hot / 25% host misses, hot rows 4096 per request",
+            "workload": (
+                "sparse decode step of one layer (quest select + resolve + host-row gather + attention), "
+                "Llama-3-8B heads 32q/8kv/128, bf16, page 64, 32 pages = 2048 rows selected of 32768, "
+                "selected pages 50% resident / 25% hot / 25% host misses, hot rows 4096 per request"
+                if not miss_heavy else
+                "miss-heavy sparse decode step of one layer, Llama-3-8B heads 32q/8kv/128, bf16, page 64, "
+                "64 pages = 4096 rows selected of 131072, selected pages: 2 tail pages resident, 4 hot, 58 host "
+                "misses; K/V N(0,1) plus a per-page offset N(0, 0.5); hot rows 8192 per request"
+            ),
             "batch": w.batch,
             "context": w.context,
             "chunks": len(result.chunks),
