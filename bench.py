@@ -67,7 +67,7 @@ def parse_args():
     ap.add_argument("--side-stream", action="store_true",
                     help="run the gather on a side stream ordered by events (the default with --chunks > 1)")
     ap.add_argument("--copy-calibration", action="store_true", help="run the PMC calibration copy and exit")
-    ap.add_argument("--workload", choices=("kernel", "miss-heavy", "model"), default="kernel",
+    ap.add_argument("--workload", choices=("kernel", "miss-heavy", "model", "resolver-stress"), default="kernel",
                     help="kernel: one-layer sparse decode step (default); miss-heavy: the same step at batch 4, "
                     "128K context, 4096-row budget, ~90%% of rows gathered; model: whole-model batched decode")
     ap.add_argument("--layers", type=int, default=32, help="model workload: decoder layers")
@@ -266,6 +266,106 @@ def traffic_from_profile(kernel_tag, name="sparse_decode_b16_ctx32k_pmc_traffic.
     return None
 
 
+def run_resolver_stress(args):
+    """Quest selection + row resolution for 64 requests with Qwen2-7B heads
+    (28 query / 4 KV heads x 128, bf16), contexts uniform in [4096, 65536]
+    (seeded), pages of 32, 32 pages = 1024 rows selected, 2048 hot rows per
+    request all occupied (every step replaces LRU rows), fresh queries every
+    step; prints one JSON line (the step is selection + resolve only)."""
+    import numpy as np
+    import torch
+
+    from nano_hisparse import _hip
+    from nano_hisparse import row_kernels as rk
+
+    _hip.load()
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    B, Hq, Hkv, D, P, K, H = 64, 28, 4, 128, 32, 1024, 2048
+    top = K // P
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    rng = np.random.default_rng(args.seed)
+    lengths = rng.integers(4096, 65536 + 1, size=B)
+    n_pages = int(-(-lengths.max() // P))
+    counts = -(-lengths // P)
+    minimum = torch.empty(B, n_pages, Hkv, D, dtype=torch.bfloat16, device=device)
+    maximum = torch.empty_like(minimum)
+    for b in range(B):
+        keys = torch.randn(n_pages, P, Hkv, D, generator=g, device=device).to(torch.bfloat16)
+        minimum[b], maximum[b] = keys.amin(1), keys.amax(1)
+    source = np.full((B, n_pages), -1, np.int32)
+    resident = np.full((B, n_pages), -1, np.int32)
+    hot = np.zeros((B, H // P), np.int32)
+    tags = np.full((B, H), -1, np.int32)
+    next_host, next_block = 0, 0
+    for b in range(B):
+        c = int(counts[b])
+        source[b, :c] = np.arange(next_host, next_host + c)
+        next_host += c
+        hot[b] = np.arange(next_block, next_block + H // P)
+        next_block += H // P
+        res = rng.permutation(c)[: (3 * c) // 10]
+        resident[b, res] = np.arange(next_block, next_block + res.size)
+        next_block += res.size
+        nonres = np.flatnonzero(resident[b, :c] < 0)
+        cand = (source[b, nonres][:, None].astype(np.int64) * P + np.arange(P)).ravel()
+        tags[b] = rng.choice(cand, size=H, replace=False)
+    lru = np.stack([rng.permutation(H) for _ in range(B)])
+    to = lambda x: torch.from_numpy(x).to(device)  # noqa: E731
+    g_len, g_src, g_res, g_hot, g_tags, g_lru = (to(x) for x in (lengths, source, resident, hot, tags, lru))
+    queries = [torch.randn(B, Hq, D, generator=g, device=device).to(torch.bfloat16)
+               for _ in range(args.warmup + args.steps)]
+    totals = torch.zeros(3, dtype=torch.int64, device=device)
+    ev = [[rk.timing_events(), rk.timing_events()] for _ in range(args.steps)]
+
+    def step(i, events=None):
+        if events:
+            rk.set_launch_events(*events[0])
+        _, positions, _ = rk.quest_batched(queries[i], minimum, maximum, g_len, P, top)
+        if events:
+            rk.set_launch_events(*events[1])
+        rk.resolve_batched(positions, g_src, g_res, g_hot, g_tags, g_lru, g_len, P, counts_total=totals)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    totals.zero_()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        step(args.warmup + i, ev[i])
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    quest_us = 1e3 * sum(e[0][0].elapsed_time(e[0][1]) for e in ev) / args.steps
+    resolve_us = 1e3 * sum(e[1][0].elapsed_time(e[1][1]) for e in ev) / args.steps
+    resident_hits, hot_hits, misses = (t / args.steps for t in totals.tolist())
+    result = {
+        "metric": METRIC,
+        "value": round(B / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "resolver stress: Quest selection + row resolution (no gather/attention) for 64 requests, "
+            "Qwen2-7B heads 28q/4kv/128, bf16, contexts uniform in [4096, 65536], page 32, 1024 rows selected, "
+            "2048 hot rows per request fully occupied, fresh queries every step",
+            "batch": B,
+            "parallelism": "single GPU",
+        },
+        "kernel_us": {"quest": round(quest_us, 2), "resolve": round(resolve_us, 2)},
+        "rows_per_step": {"resident_hits": resident_hits, "hot_hits": hot_hits, "misses": misses},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def run_model_decode(args):
     """Whole-model batched decode; prints one JSON line."""
     from math import ceil
@@ -387,6 +487,9 @@ def main():
         return
     if args.workload == "model":
         run_model_decode(args)
+        return
+    if args.workload == "resolver-stress":
+        run_resolver_stress(args)
         return
     import torch
 

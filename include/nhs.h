@@ -171,13 +171,16 @@ int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t po
  * Quest page selection for `batch` requests. Request b scores each of its
  * count = ceil(lengths[b]/page_size) pages (count is clamped to max_pages):
  *   score[p] = (sum_h sum_d max(q[h,d]*min[p,h/g,d], q[h,d]*max[p,h/g,d])) / q_heads
- * in fp32 with a fixed summation order: a bound row is cut into chunks of
- * 32 bytes when it is a multiple of 32 bytes of at most 64 chunks, else of
- * 16 bytes when a multiple of 16 bytes, else of one element; each chunk is
- * summed from 0.0 in element order with t = fma(q, q > 0 ? max : min, t);
- * chunk sums (padded with +0.0 to a power of two) are added as a pairwise
- * tree; head sums are added sequentially h = 0..q_heads-1.
- * q_heads/kv_heads <= 8.
+ * in fp32 with a fixed summation order: per KV head j and dimension d the
+ * GQA group's terms are min*Qneg + max*Qpos (Qpos / Qneg: the sums, in head
+ * order from 0.0, of the group's positive / non-positive q[h,d]); a bound
+ * row is cut into chunks of 32 bytes when it is a multiple of 32 bytes of at
+ * most 64 chunks, else of 16 bytes when a multiple of 16 bytes, else of one
+ * element; each chunk is summed from 0.0 in element order with
+ * t = fma(nneg ? min : 0, Qneg, t), t = fma(npos ? max : 0, Qpos, t) (npos,
+ * nneg: whether any head contributed to Qpos, Qneg); chunk sums (padded with
+ * +0.0 to a power of two) are added as a pairwise tree; KV-head sums are
+ * added sequentially j = 0..kv_heads-1. q_heads/kv_heads <= 8.
  * Page count-1, and page 0 when keep_sink and
  * top_pages > 1 and count > 1, score +inf. The top_pages pages by (score
  * descending, page ascending) are written ascending to pages[b, :top_pages]

@@ -78,9 +78,58 @@ __device__ __forceinline__ int page_count(const int64_t* lengths, int64_t length
 
 // Quest bounds score: (sum_h sum_d max(q*min, q*max)) / q_heads.
 //
-// The term max(q*kmin, q*kmax) is q * (q > 0 ? kmax : kmin) (kmax >= kmin),
-// added to t with one fma: for 16-bit queries and bounds the product is
-// exact, so this adds the reference's term to t (up to the sign of a zero).
+// The heads of one KV head's GQA group contribute q*kmax where q > 0 and
+// q*kmin elsewhere (kmax >= kmin), so per (KV head, d) the group's terms are
+//   kmin[d] * Qneg[d] + kmax[d] * Qpos[d]
+// with Qpos / Qneg the group's positive / non-positive query sums (added in
+// head order from 0.0, once per request). A lane keeps them for its chunk
+// and scores a page with two fmas per element, t = fma(kmin', Qneg, t) then
+// t = fma(kmax', Qpos, t), where kmin' (kmax') is 0 when no head of the
+// group is non-positive (positive) at d, so a bound nobody selects is never
+// multiplied. Chunk sums are added as a pairwise tree over a KV head's
+// lanes, the KV-head sums sequentially; the CPU oracle sums in this order.
+//
+// The per-lane grouped sums (and the masks of which side has contributors).
+template <int E, int G>
+struct GroupedQuery {
+  float pos[E], neg[E];
+  bool has_pos[E], has_neg[E];
+  // qv: the lane's slices of the group's query heads; live: this lane holds
+  // data (padding lanes add exactly +0)
+  __device__ __forceinline__ void init(const float (&qv)[G][E], int group, bool live) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float p = 0.f, n = 0.f;
+      bool hp = false, hn = false;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if (g < group) {
+          const float q = qv[g][e];
+          if (q > 0.f) {
+            p = p + q;
+            hp = true;
+          } else {
+            n = n + q;
+            hn = true;
+          }
+        }
+      }
+      pos[e] = p, neg[e] = n;
+      has_pos[e] = hp && live, has_neg[e] = hn && live;
+    }
+  }
+  // this lane's chunk sum for one page's bounds
+  __device__ __forceinline__ float chunk(const float (&mn)[E], const float (&mx)[E]) const {
+    float x = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      x = __builtin_fmaf(has_neg[e] ? mn[e] : 0.f, neg[e], x);
+      x = __builtin_fmaf(has_pos[e] ? mx[e] : 0.f, pos[e], x);
+    }
+    return x;
+  }
+};
 //
 // General kernel, for pages wider than one wave: lanes are laid out as (page
 // of the step, kv head, chunk), so a lane keeps one kv head's query slices
@@ -92,7 +141,7 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
   extern __shared__ float smem[];
   const int pages_per_step = a.pages_per_step;
   float* qs = smem;                              // [q_heads * head_dim]
-  float* hs = smem + a.q_heads * a.head_dim;     // [pages_per_step][q_heads]
+  float* hs = smem + a.q_heads * a.head_dim;     // [pages_per_step][kv_heads]
   const int b = blockIdx.y;
   const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
   const int p_begin = blockIdx.x * a.pages_per_block;
@@ -116,6 +165,8 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < E; ++e) qv[g][e] = data && g < a.group ? qs[(kh * a.group + g) * a.head_dim + sub * E + e] : 0.f;
+  GroupedQuery<E, G> gq;
+  gq.init(qv, a.group, data);
   const char *lo, *hi;
   bounds_of<T>(a, b, lo, hi);
   const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
@@ -130,23 +181,13 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
   for (int base = p_begin; base < p_end; base += pages_per_step) {
     const int p = base + page_local;
     load(p + pages_per_step, mn2, mx2);
-    float t[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float x = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) x = __builtin_fmaf(qv[g][e], qv[g][e] > 0.f ? mx[e] : mn[e], x);
-      t[g] = group_sum(x, lpr);
-    }
-    if (active && sub == 0 && p < p_end)
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-        if (g < a.group) hs[page_local * a.q_heads + kh * a.group + g] = t[g];
+    const float t = group_sum(gq.chunk(mn, mx), lpr);
+    if (active && sub == 0 && p < p_end) hs[page_local * a.kv_heads + kh] = t;
     __syncthreads();
     if ((int)threadIdx.x < pages_per_step && base + (int)threadIdx.x < p_end) {
-      const float* row = hs + threadIdx.x * a.q_heads;
+      const float* row = hs + threadIdx.x * a.kv_heads;
       float total = row[0];
-      for (int h = 1; h < a.q_heads; ++h) total = total + row[h];
+      for (int h = 1; h < a.kv_heads; ++h) total = total + row[h];
       a.scores[(int64_t)b * a.max_pages + base + threadIdx.x] = total / (float)a.q_heads;
     }
     __syncthreads();
@@ -160,19 +201,17 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
 
 // Page kernel, for pages that fit one wave (kv_heads * lanes per head <=
 // 64, 32-byte chunks): lane = (page of the wave, kv head, chunk). A wave
-// loads its query slices straight into registers, issues the bounds of all
-// its kPageSlots page slots, then scores them one by one: per-lane chunk sum,
-// DPP tree over a head's lanes, and the sequential head sum through the
-// wave's own LDS rows, so no workgroup barrier is involved.
+// loads its query slices straight into registers, forms the grouped sums,
+// issues the bounds of all its kPageSlots page slots, then scores them one
+// by one: per-lane chunk sum, DPP tree over a KV head's lanes, and the
+// sequential KV-head sum read across lanes, with no barrier.
 constexpr int kPageThreads = 256;
 constexpr int kPageWaves = kPageThreads / kWave;
 constexpr int kPageSlots = 4;
-constexpr int kMaxHeadsPerWave = 512;  // pages per wave * q_heads rounded up to 4 (+ 16 read past the end)
 
 template <typename T, int E, int G>
 __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) float hsum[kPageWaves][kMaxHeadsPerWave + 16];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int b = blockIdx.y;
@@ -208,6 +247,8 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
     if (!(data && g < a.group))
 #pragma unroll
       for (int e = 0; e < E; ++e) qv[g][e] = 0.f;
+  GroupedQuery<E, G> gq;
+  gq.init(qv, a.group, data);
   const char *lo, *hi;
   bounds_of<T>(a, b, lo, hi);
   const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
@@ -220,49 +261,22 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
     load_vec<T, E>(lo, (int64_t)pc * page_elems + lane_off, mn[s]);
     load_vec<T, E>(hi, (int64_t)pc * page_elems + lane_off, mx[s]);
   }
-  float* hs = hsum[wave];
   const int lpr = 1 << a.lpr_log2;
+  const int page_lane0 = page_local * lanes_per_page;
 #pragma unroll
   for (int s = 0; s < kPageSlots; ++s) {
     const int p0 = wave_first + s * ppw;
     if (p0 >= count) break;
-    float t[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float x = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) x = __builtin_fmaf(qv[g][e], qv[g][e] > 0.f ? mx[s][e] : mn[s][e], x);
-      t[g] = group_sum(x, lpr);
+    const float t = group_sum(gq.chunk(mn[s], mx[s]), lpr);
+    // sequential sum over the page's KV heads (every lane takes part in the
+    // lane reads; the page's first lane stores)
+    float total = 0.f;
+    for (int h = 0; h < a.kv_heads; ++h) {
+      const float v = __shfl(t, page_lane0 + (h << a.lpr_log2));
+      total = h == 0 ? v : total + v;
     }
-    const int row_stride = (a.q_heads + 3) & ~3;  // 16-byte aligned rows
-    if (data && sub == 0)
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-        if (g < a.group) hs[page_local * row_stride + kh * a.group + g] = t[g];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane < ppw && p0 + lane < count) {
-      // sequential sum over the heads; 16 values are read per batch so the
-      // adds do not wait on one LDS round trip each
-      const float* row = hs + lane * row_stride;
-      float total = 0.f;
-      for (int h0 = 0; h0 < a.q_heads; h0 += 16) {
-        float v[16];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float4 w = *reinterpret_cast<const float4*>(row + h0 + 4 * j);
-          v[4 * j] = w.x, v[4 * j + 1] = w.y, v[4 * j + 2] = w.z, v[4 * j + 3] = w.w;
-        }
-#pragma unroll
-        for (int j = 0; j < 16; ++j)
-          if (h0 + j < a.q_heads) total = h0 + j == 0 ? v[j] : total + v[j];
-      }
-      a.scores[(int64_t)b * a.max_pages + p0 + lane] = total / (float)a.q_heads;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (within == 0 && page_local < ppw && p0 + page_local < count)
+      a.scores[(int64_t)b * a.max_pages + p0 + page_local] = total / (float)a.q_heads;
   }
 }
 
@@ -552,7 +566,7 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
   dim3 grid, block;
   size_t lds = 0;
   const int ppw = lanes_per_page <= kWave ? kWave / lanes_per_page : 0;
-  if (E * esize == 32 && ppw > 0 && ppw * ((q_heads + 3) & ~3) <= kMaxHeadsPerWave) {
+  if (E * esize == 32 && ppw > 0) {
     // a page fits one wave: the page kernel
     a.pages_per_step = ppw;
     a.pages_per_block = kPageWaves * kPageSlots * ppw;
@@ -575,7 +589,7 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
     a.pages_per_block = a.pages_per_step * ((kPagesPerBlock + a.pages_per_step - 1) / a.pages_per_step);
     grid = dim3((unsigned)((max_pages + a.pages_per_block - 1) / a.pages_per_block), (unsigned)batch);
     block = dim3(threads);
-    lds = ((size_t)q_heads * head_dim + (size_t)a.pages_per_step * q_heads) * sizeof(float);
+    lds = ((size_t)q_heads * head_dim + (size_t)a.pages_per_step * kv_heads) * sizeof(float);
     switch (bounds_dtype * 1024 + E * 16 + G) {
 #define NHS_QUEST_CASE(DT, TY, EE, GG) \
   case DT * 1024 + EE * 16 + GG: kernel = quest_score_kernel<TY, EE, GG>; break;

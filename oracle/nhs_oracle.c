@@ -21,13 +21,21 @@
  * bytes / element size when the row is a multiple of 16 bytes, else 1);
  * each chunk is summed sequentially from 0.0; the chunk sums, padded with
  * +0.0 to a power of two, are added as a pairwise tree in chunk order; the
- * per-head sums are added sequentially. The Quest term max(q*kmin, q*kmax)
- * (selection.py:84) is q * (q > 0 ? kmax : kmin), accumulated with one
- * fma: for 16-bit queries and bounds the product is exact, so each step
- * adds the reference's term (up to the sign of a zero); for fp32 inputs the
- * product is not rounded before the addition. The mean selector rounds
- * each product before adding it. Build with -ffp-contract=off so no other
- * product is fused.
+ * per-KV-head sums are added sequentially.
+ *
+ * Quest (selection.py:84-85) sums max(q*kmin, q*kmax) over the query heads
+ * and dimensions. For one KV head and dimension d the heads of its GQA group
+ * contribute q*kmax if q > 0 and q*kmin otherwise (kmin <= kmax), that is
+ *   kmin[d] * Qneg[d] + kmax[d] * Qpos[d],
+ * with Qpos / Qneg the sums of the group's positive / non-positive query
+ * values at d (added sequentially in head order from 0.0). Each chunk step
+ * is t = fma(nneg ? kmin : 0, Qneg, t) then t = fma(npos ? kmax : 0, Qpos, t),
+ * where npos / nneg say whether any head contributed to Qpos / Qneg: a
+ * bound that no head multiplies is never multiplied (so an infinite bound
+ * gives no 0 * inf), and NaN queries or bounds propagate as in the
+ * reference. The score is the sum over KV heads divided by q_heads. The mean
+ * selector rounds each product before adding it. Build with
+ * -ffp-contract=off so no other product is fused.
  */
 #include <math.h>
 #include <stdint.h>
@@ -171,37 +179,60 @@ static int page_count(int64_t len, int page_size, int max_pages) {
   return (int)(c < max_pages ? c : max_pages);
 }
 
-/* Quest score of every page p < count of one request. */
+/* Quest score of every page p < count of one request (order in the header). */
 static void quest_scores_one(const void* q, int q_dtype, int64_t q_hs, const void* lo, const void* hi, int bdt,
                              int q_heads, int kv_heads, int head_dim, int count, float* scores) {
   const int group = q_heads / kv_heads;
   const int E = quest_chunk_elems(head_dim, elem_size(bdt));
   const int used = head_dim / E, L = pow2_at_least(used);
+  const size_t n = (size_t)kv_heads * head_dim;
+  float* qpos = (float*)malloc(sizeof(float) * n);
+  float* qneg = (float*)malloc(sizeof(float) * n);
+  char* npos = (char*)malloc(n);
+  char* nneg = (char*)malloc(n);
   float* t = (float*)malloc(sizeof(float) * (size_t)L);
-  float* hs = (float*)malloc(sizeof(float) * (size_t)q_heads);
+  float* hs = (float*)malloc(sizeof(float) * (size_t)kv_heads);
+  for (int kh = 0; kh < kv_heads; ++kh)
+    for (int d = 0; d < head_dim; ++d) {
+      float pos = 0.0f, neg = 0.0f;
+      char np = 0, nn = 0;
+      for (int g = 0; g < group; ++g) {
+        float qd = load_elem(q, q_dtype, (int64_t)(kh * group + g) * q_hs + d);
+        if (qd > 0.0f) {
+          pos = pos + qd;
+          np = 1;
+        } else {
+          neg = neg + qd;
+          nn = 1;
+        }
+      }
+      qpos[kh * head_dim + d] = pos, qneg[kh * head_dim + d] = neg;
+      npos[kh * head_dim + d] = np, nneg[kh * head_dim + d] = nn;
+    }
   for (int p = 0; p < count; ++p) {
-    for (int h = 0; h < q_heads; ++h) {
-      const int kh = h / group;
+    for (int kh = 0; kh < kv_heads; ++kh) {
       const int64_t base = ((int64_t)p * kv_heads + kh) * head_dim;
       for (int l = 0; l < L; ++l) {
         t[l] = 0.0f;
         if (l >= used) continue;
         for (int e = 0; e < E; ++e) {
-          /* max(q*kmin, q*kmax) = q * (q > 0 ? kmax : kmin) for kmin <= kmax,
-             added to t with one fma: exact per step for 16-bit inputs, whose
-             products fit in fp32 */
-          int d = l * E + e;
-          float qd = load_elem(q, q_dtype, (int64_t)h * q_hs + d);
-          float k = qd > 0.0f ? load_elem(hi, bdt, base + d) : load_elem(lo, bdt, base + d);
-          t[l] = fmaf(qd, k, t[l]);
+          int d = l * E + e, i = kh * head_dim + d;
+          float kmin = nneg[i] ? load_elem(lo, bdt, base + d) : 0.0f;
+          float kmax = npos[i] ? load_elem(hi, bdt, base + d) : 0.0f;
+          t[l] = fmaf(kmin, qneg[i], t[l]);
+          t[l] = fmaf(kmax, qpos[i], t[l]);
         }
       }
-      hs[h] = tree_sum(t, L);
+      hs[kh] = tree_sum(t, L);
     }
     float total = hs[0];
-    for (int h = 1; h < q_heads; ++h) total = total + hs[h];
+    for (int kh = 1; kh < kv_heads; ++kh) total = total + hs[kh];
     scores[p] = total / (float)q_heads;
   }
+  free(qpos);
+  free(qneg);
+  free(npos);
+  free(nneg);
   free(t);
   free(hs);
 }

@@ -8,6 +8,8 @@ reference repository): tests/test_selection.py:18-50.
 import ctypes
 
 import numpy as np
+import math
+
 import pytest
 import torch
 
@@ -135,6 +137,36 @@ def test_quest_pages_agree_with_float64_scores_outside_ties():
         kth = ex.topk(top).values[-1].item()
         for p in got ^ want:  # any disagreement must be a near-tie at the k-th score
             assert abs(ex[p].item() - kth) < 1e-4
+
+
+def test_quest_infinite_and_nan_bounds_behave_as_the_reference_maximum():
+    """Bounds of +-inf (keys of inf) and NaN: the score is finite exactly where
+    the reference's sum of max(q*kmin, q*kmax) is, and NaN/inf where it is.
+    The grouped form never multiplies a bound that no head selects, so an
+    infinite bound on the unused side gives no 0 * inf."""
+    Hq, Hkv, D, P = 4, 2, 8, 4
+    q = torch.tensor([[1.0, -2.0, 0.5, 3.0, -1.0, 2.0, -0.5, 1.5]]).repeat(Hq, 1)
+    q[1] = -q[1].abs()  # KV head 0 serves heads 0 (mixed signs) and 1 (all negative)
+    q[2] = q[2].abs()  # KV head 1 serves heads 2 (all positive) and 3 (mixed signs)
+    mn = torch.full((1, 6, Hkv, D), -1.0)
+    mx = torch.full((1, 6, Hkv, D), 1.0)
+    mx[0, 1, 0, 1] = float("inf")  # d 1: both heads of KV head 0 are negative, kmax unused: finite
+    mn[0, 2, 1, 0] = float("-inf")  # d 0: both heads of KV head 1 are positive, kmin unused: finite
+    mx[0, 3, 0, :] = float("nan")  # NaN bounds: NaN score
+    mn[0, 4, 0, 2] = float("-inf")  # d 2: head 1 is negative and reads kmin: +inf
+    qe = q.double()
+    kmin = mn.double().repeat_interleave(2, 2)
+    kmax = mx.double().repeat_interleave(2, 2)
+    ref = torch.maximum(qe[None, None] * kmin, qe[None, None] * kmax).sum(-1).mean(-1)[0]
+    scores, _, _ = oracle.quest_select(q[None], mn, mx, [6 * P], P, 2)
+    for p in range(6):
+        r, s_ = ref[p].item(), scores[0, p].item()
+        if math.isnan(r):
+            assert math.isnan(s_), p
+        elif math.isinf(r):
+            assert s_ == r, p
+        else:
+            assert abs(s_ - r) < 1e-5, (p, s_, r)
 
 
 def test_mean_select_forces_first_and_last_page():
