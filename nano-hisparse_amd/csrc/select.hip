@@ -242,13 +242,9 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
 #pragma unroll
       for (int e = 0; e < E; ++e) qv[g][e] = load_elem(a.q, a.q_dtype, qi[g] + (data ? e : 0));
   }
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-    if (!(data && g < a.group))
-#pragma unroll
-      for (int e = 0; e < E; ++e) qv[g][e] = 0.f;
-  GroupedQuery<E, G> gq;
-  gq.init(qv, a.group, data);
+  // (GroupedQuery ignores heads past the group and lanes without data)
+  // the bounds of every slot are requested before the query slices are
+  // used, so the two memory latencies overlap
   const char *lo, *hi;
   bounds_of<T>(a, b, lo, hi);
   const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
@@ -261,6 +257,8 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
     load_vec<T, E>(lo, (int64_t)pc * page_elems + lane_off, mn[s]);
     load_vec<T, E>(hi, (int64_t)pc * page_elems + lane_off, mx[s]);
   }
+  GroupedQuery<E, G> gq;
+  gq.init(qv, a.group, data);
   const int lpr = 1 << a.lpr_log2;
   const int page_lane0 = page_local * lanes_per_page;
 #pragma unroll
@@ -352,17 +350,20 @@ struct SelectArgs {
   int32_t* positions;
 };
 
-__global__ __launch_bounds__(kSelectThreads) void select_topk_kernel(SelectArgs a) {
+// THREADS = 1024 covers NHS_MAX_SELECT_PAGES; a 256-thread workgroup (4
+// waves: cheaper barriers and histogram passes) covers up to 4096 pages.
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void select_topk_kernel(SelectArgs a) {
   __shared__ int32_t chosen[NHS_MAX_SELECT_PAGES];
   __shared__ int32_t hist[256];
-  __shared__ int32_t scan[kSelectThreads / 64 + 1];
+  __shared__ int32_t scan[THREADS / 64 + 1];
   __shared__ int32_t pick[2];
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
   const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
   const int64_t len = a.lengths ? a.lengths[b] : a.length;
   const int k = a.top_pages < count ? a.top_pages : count;
-  const int per = (count + kSelectThreads - 1) / kSelectThreads;  // <= 16
+  const int per = (count + THREADS - 1) / THREADS;  // <= 16
   const int p0 = tid * per;
 
   bool sel[kMaxSelectPerThread];
@@ -450,14 +451,14 @@ __global__ __launch_bounds__(kSelectThreads) void select_topk_kernel(SelectArgs 
 #pragma unroll
   for (int q = 0; q < kMaxSelectPerThread; ++q)
     if (sel[q]) chosen[out++] = p0 + q;
-  for (int i = n_sel + tid; i < a.top_pages; i += kSelectThreads) chosen[i] = -1;
+  for (int i = n_sel + tid; i < a.top_pages; i += THREADS) chosen[i] = -1;
   __syncthreads();
   int32_t* pages = a.pages + (int64_t)b * a.top_pages;
-  for (int i = tid; i < a.top_pages; i += kSelectThreads) pages[i] = chosen[i];
+  for (int i = tid; i < a.top_pages; i += THREADS) pages[i] = chosen[i];
   const int P = a.page_size;
   const int64_t n_pos = (int64_t)a.top_pages * P;
   int32_t* pos = a.positions + (int64_t)b * n_pos;
-  for (int64_t i = tid; i < n_pos; i += kSelectThreads) {
+  for (int64_t i = tid; i < n_pos; i += THREADS) {
     uint32_t j = a.page_div.div((uint32_t)i);
     int32_t p = chosen[j];
     int64_t t = (int64_t)p * P + (int64_t)((uint32_t)i - j * (uint32_t)P);
@@ -501,7 +502,10 @@ static int quest_chunk_elems(int head_dim, int esize) {
 
 static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, const char* who, hipEvent_t start,
                          hipEvent_t stop) {
-  launch(select_topk_kernel, dim3((unsigned)batch), dim3(kSelectThreads), 0, stream, start, stop, s);
+  if (s.max_pages <= 256 * kMaxSelectPerThread)
+    launch(select_topk_kernel<256>, dim3((unsigned)batch), dim3(256), 0, stream, start, stop, s);
+  else
+    launch(select_topk_kernel<kSelectThreads>, dim3((unsigned)batch), dim3(kSelectThreads), 0, stream, start, stop, s);
   return launch_status(who);
 }
 
