@@ -13,7 +13,7 @@
 namespace nhs {
 
 constexpr int kAppendThreads = 256;
-constexpr int kAppendBatch = 16;  // earlier rows loaded together for the page mean
+constexpr int kAppendBatch = 64;  // earlier rows loaded together for the page mean (one round for P <= 64)
 
 struct AppendArgs {
   const void* k;
@@ -33,19 +33,26 @@ struct AppendArgs {
 __device__ __forceinline__ float nan_min(float a, float b) { return (a != a || b != b) ? a + b : (b < a ? b : a); }
 __device__ __forceinline__ float nan_max(float a, float b) { return (a != a || b != b) ? a + b : (b > a ? b : a); }
 
-// Element e of every appended row of one page.
+// Element e of every appended row of one page (T: the KV storage type, so
+// every load below is a plain load of a known width).
+template <typename T>
 __device__ __forceinline__ void append_element(const AppendArgs& a, int e) {
-  const int esize = a.dtype == NHS_F32 ? 4 : 2;
-  float lo = load_elem(a.minimum, a.dtype, e);
-  float hi = load_elem(a.maximum, a.dtype, e);
+  constexpr int esize = T::bytes;
+  float lo = load_elem(a.minimum, T::dtype, e);
+  float hi = load_elem(a.maximum, T::dtype, e);
   double sum = 0.0;
   // the earlier keys of the page, loaded kAppendBatch at a time before they
   // are summed (in row order)
+  // Loads are unconditional (rows past `within` re-read the last earlier
+  // row, which is in bounds) so that no branch separates them; only the
+  // sum is masked.
   for (int r0 = 0; r0 < a.within; r0 += kAppendBatch) {
     float keys[kAppendBatch];
 #pragma unroll
-    for (int j = 0; j < kAppendBatch; ++j)
-      keys[j] = r0 + j < a.within ? load_elem(a.pool_block, a.dtype, (int64_t)(r0 + j) * a.row_elems + e) : 0.f;
+    for (int j = 0; j < kAppendBatch; ++j) {
+      const int r = min(r0 + j, a.within - 1);
+      keys[j] = load_elem(a.pool_block, T::dtype, (int64_t)r * a.row_elems + e);
+    }
 #pragma unroll
     for (int j = 0; j < kAppendBatch; ++j)
       if (r0 + j < a.within) sum += (double)keys[j];
@@ -71,19 +78,20 @@ __device__ __forceinline__ void append_element(const AppendArgs& a, int e) {
         reinterpret_cast<uint16_t*>(a.host_block)[a.plane_elems + row] = vb;
       }
     }
-    const float key = load_elem(a.k, a.dtype, src);
+    const float key = load_elem(a.k, T::dtype, src);
     lo = nan_min(lo, key);
     hi = nan_max(hi, key);
     sum += (double)key;
   }
-  store_elem(a.minimum, a.dtype, e, lo);
-  store_elem(a.maximum, a.dtype, e, hi);
+  store_elem(a.minimum, T::dtype, e, lo);
+  store_elem(a.maximum, T::dtype, e, hi);
   a.summary[e] = (float)(sum / (double)(a.within + a.count));
 }
 
+template <typename T>
 __global__ __launch_bounds__(kAppendThreads) void append_page_kernel(AppendArgs a) {
   const int e = blockIdx.x * kAppendThreads + threadIdx.x;
-  if (e < a.row_elems) append_element(a, e);
+  if (e < a.row_elems) append_element<T>(a, e);
 }
 
 struct AppendItemsArgs {
@@ -99,6 +107,7 @@ struct AppendItemsArgs {
 
 // Item blockIdx.y appends its one token; its page and row follow from its
 // length and its page tables.
+template <typename T>
 __global__ __launch_bounds__(kAppendThreads) void append_items_kernel(AppendItemsArgs g) {
   const int e = blockIdx.x * kAppendThreads + threadIdx.x;
   if (e >= g.row_elems) return;
@@ -106,7 +115,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_items_kernel(AppendItem
   const nhs_layer_item& item = g.items[b];
   const int64_t length = g.lengths[b];
   const int64_t page = length / g.page_size;
-  const int esize = g.dtype == NHS_F32 ? 4 : 2;
+  constexpr int esize = T::bytes;
   const int64_t plane = (int64_t)g.page_size * g.row_elems;
   const int64_t block_bytes = 2 * plane * esize;
   const int64_t page_offset = page * g.row_elems;
@@ -124,7 +133,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_items_kernel(AppendItem
   a.summary = item.summaries + page_offset;
   a.minimum = static_cast<char*>(item.minimum) + page_offset * esize;
   a.maximum = static_cast<char*>(item.maximum) + page_offset * esize;
-  append_element(a, e);
+  append_element<T>(a, e);
 }
 
 }  // namespace nhs
@@ -155,8 +164,13 @@ extern "C" int nhs_append_page(const void* k, const void* v, int64_t token_strid
   a.summary = summary;
   a.minimum = minimum;
   a.maximum = maximum;
-  launch(append_page_kernel, dim3((unsigned)((row_elems + kAppendThreads - 1) / kAppendThreads)),
-         dim3(kAppendThreads), 0, (hipStream_t)stream, ev.start, ev.stop, a);
+  const dim3 grid((unsigned)((row_elems + kAppendThreads - 1) / kAppendThreads)), threads(kAppendThreads);
+  if (kv_dtype == NHS_BF16)
+    launch(append_page_kernel<BF16>, grid, threads, 0, (hipStream_t)stream, ev.start, ev.stop, a);
+  else if (kv_dtype == NHS_F16)
+    launch(append_page_kernel<F16>, grid, threads, 0, (hipStream_t)stream, ev.start, ev.stop, a);
+  else
+    launch(append_page_kernel<F32>, grid, threads, 0, (hipStream_t)stream, ev.start, ev.stop, a);
   return launch_status("nhs_append_page");
 }
 
@@ -181,7 +195,12 @@ extern "C" int nhs_append_items(int32_t batch, const void* k, const void* v, int
   g.host = static_cast<char*>(host_alias);
   g.items = items;
   g.lengths = lengths;
-  launch(append_items_kernel, dim3((unsigned)((row_elems + kAppendThreads - 1) / kAppendThreads), (unsigned)batch),
-         dim3(kAppendThreads), 0, (hipStream_t)stream, ev.start, ev.stop, g);
+  const dim3 grid((unsigned)((row_elems + kAppendThreads - 1) / kAppendThreads), (unsigned)batch), block(kAppendThreads);
+  if (kv_dtype == NHS_BF16)
+    launch(append_items_kernel<BF16>, grid, block, 0, (hipStream_t)stream, ev.start, ev.stop, g);
+  else if (kv_dtype == NHS_F16)
+    launch(append_items_kernel<F16>, grid, block, 0, (hipStream_t)stream, ev.start, ev.stop, g);
+  else
+    launch(append_items_kernel<F32>, grid, block, 0, (hipStream_t)stream, ev.start, ev.stop, g);
   return launch_status("nhs_append_items");
 }

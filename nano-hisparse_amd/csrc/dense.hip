@@ -47,14 +47,16 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(typename T::B
   const typename T::Bits* dr = delta ? delta + (int64_t)row * width : nullptr;
   // rows of up to kNormThreads * kNormHeld elements are held in registers:
   // every load is issued before the first store, which could alias them
-  float held[kNormHeld];
+  float held[kNormHeld], wv[kNormHeld];
   float acc = 0.f;
   const bool in_regs = width <= kNormThreads * kNormHeld;
   if (in_regs) {
+    // x, delta and the weights are all requested before the first use
 #pragma unroll
     for (int j = 0; j < kNormHeld; ++j) {
       const int i = threadIdx.x + j * kNormThreads;
       held[j] = i < width ? T::to_float(xr[i]) : 0.f;
+      wv[j] = i < width ? T::to_float(weight[i]) : 0.f;
     }
     if (dr) {
       float dv[kNormHeld];
@@ -93,12 +95,6 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(typename T::B
   const float r = rsqrtf(total / (float)width + eps);
   typename T::Bits* orow = out + (int64_t)row * width;
   if (in_regs) {
-    float wv[kNormHeld];
-#pragma unroll
-    for (int j = 0; j < kNormHeld; ++j) {
-      const int i = threadIdx.x + j * kNormThreads;
-      wv[j] = i < width ? T::to_float(weight[i]) : 0.f;
-    }
 #pragma unroll
     for (int j = 0; j < kNormHeld; ++j) {
       const int i = threadIdx.x + j * kNormThreads;
@@ -110,6 +106,66 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(typename T::B
       if (dr && !write_back) h = rnd<T>(h + T::to_float(dr[i]));
       orow[i] = T::from_float(rnd<T>(h * r) * T::to_float(weight[i]));
     }
+  }
+}
+
+// add_rmsnorm for 16-bit rows of V * kNormThreads * 8 elements: thread t
+// owns the 8-element chunks t, t + kNormThreads, ... and moves them with
+// 16-byte loads and stores. Same arithmetic as add_rmsnorm_kernel.
+template <typename T, int V>
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_vec_kernel(uint16_t* x, const uint16_t* delta,
+                                                                       const uint16_t* weight, uint16_t* out,
+                                                                       int width, float eps, int write_back) {
+#pragma clang fp contract(off)
+  __shared__ float partial[kNormThreads / kWave];
+  const int row = blockIdx.x;
+  uint4* xr = reinterpret_cast<uint4*>(x + (int64_t)row * width);
+  const uint4* dr = delta ? reinterpret_cast<const uint4*>(delta + (int64_t)row * width) : nullptr;
+  const uint4* wr = reinterpret_cast<const uint4*>(weight);
+  uint4 xv[V], dv[V], wv[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    xv[j] = xr[threadIdx.x + j * kNormThreads];
+    wv[j] = wr[threadIdx.x + j * kNormThreads];
+    if (dr) dv[j] = dr[threadIdx.x + j * kNormThreads];
+  }
+  float h[V][8];
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const uint32_t xw[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+    const uint32_t dw[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = T::to_float((uint16_t)(xw[e >> 1] >> ((e & 1) * 16)));
+      if (dr) v = rnd<T>(v + T::to_float((uint16_t)(dw[e >> 1] >> ((e & 1) * 16))));
+      h[j][e] = v;
+      acc += v * v;
+      const uint32_t bits = T::from_float(v);
+      o[e >> 1] = (e & 1) ? (o[e >> 1] | (bits << 16)) : bits;
+    }
+    if (dr && write_back) xr[threadIdx.x + j * kNormThreads] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  acc = group_sum(acc, kWave);
+  if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = acc;
+  __syncthreads();
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) total += partial[w];
+  const float r = rsqrtf(total / (float)width + eps);
+  uint4* orow = reinterpret_cast<uint4*>(out + (int64_t)row * width);
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const uint32_t ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float w = T::to_float((uint16_t)(ww[e >> 1] >> ((e & 1) * 16)));
+      const uint32_t bits = T::from_float(rnd<T>(h[j][e] * r) * w);
+      o[e >> 1] = (e & 1) ? (o[e >> 1] | (bits << 16)) : bits;
+    }
+    orow[threadIdx.x + j * kNormThreads] = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -163,6 +219,26 @@ extern "C" int nhs_add_rmsnorm(int32_t rows, int32_t width, int32_t dtype, void*
   const int wb = delta && write_back ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)rows), block(kNormThreads);
+  const int chunk = kNormThreads * 8;
+  const bool aligned = (((uintptr_t)x | (uintptr_t)delta | (uintptr_t)weight | (uintptr_t)out) % 16) == 0;
+  if (dtype != NHS_F32 && aligned && width % chunk == 0 && width / chunk <= 4) {
+    const int v = width / chunk;
+    auto* xp = static_cast<uint16_t*>(x);
+    auto* dp = static_cast<const uint16_t*>(delta);
+    auto* wp = static_cast<const uint16_t*>(weight);
+    auto* op = static_cast<uint16_t*>(out);
+#define NHS_NORM_VEC(TT, VV) \
+  launch(add_rmsnorm_vec_kernel<TT, VV>, grid, block, 0, s, ev.start, ev.stop, xp, dp, wp, op, width, eps, wb)
+    if (dtype == NHS_BF16) {
+      if (v == 1) NHS_NORM_VEC(BF16T, 1); else if (v == 2) NHS_NORM_VEC(BF16T, 2);
+      else if (v == 3) NHS_NORM_VEC(BF16T, 3); else NHS_NORM_VEC(BF16T, 4);
+    } else {
+      if (v == 1) NHS_NORM_VEC(F16T, 1); else if (v == 2) NHS_NORM_VEC(F16T, 2);
+      else if (v == 3) NHS_NORM_VEC(F16T, 3); else NHS_NORM_VEC(F16T, 4);
+    }
+#undef NHS_NORM_VEC
+    return launch_status("nhs_add_rmsnorm");
+  }
   if (dtype == NHS_BF16)
     launch(add_rmsnorm_kernel<BF16T>, grid, block, 0, s, ev.start, ev.stop, static_cast<uint16_t*>(x),
            static_cast<const uint16_t*>(delta), static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(out),
