@@ -303,6 +303,23 @@ int nhs_rope(int32_t rows, int32_t heads, int32_t head_dim, int32_t dtype, void*
 int nhs_silu_mul(int32_t rows, int32_t inter, int32_t dtype, const void* gate_up, void* out, void* stream);
 
 /*
+ * Causal GQA self-attention over one prompt (prefill), flash-attention style
+ * on MFMA: out[s, h] = softmax_{t <= s}(q[s, h] . k[t, h / g] * D^-1/2) .
+ * v[t, h / g] for s < seq, g = q_heads / kv_heads, fp32 accumulation. bf16 or
+ * fp16, head_dim 64 or 128, strides in elements (multiples of 8, dims
+ * contiguous), 16-byte aligned tensors. Replaces the dense causal
+ * F.scaled_dot_product_attention of Model.prefill (model.py:170-180 of the
+ * reference), whose flash and memory-efficient backends this PyTorch build
+ * does not provide on gfx950 (its math fallback materialises seq x seq
+ * scores per head).
+ */
+int nhs_prefill_attention(const void* q, int64_t q_seq_stride, int64_t q_head_stride, const void* k,
+                          int64_t k_seq_stride, int64_t k_head_stride, const void* v, int64_t v_seq_stride,
+                          int64_t v_head_stride, int32_t dtype, int32_t seq, int32_t q_heads, int32_t kv_heads,
+                          int32_t head_dim, void* out, int64_t out_seq_stride, int64_t out_head_stride,
+                          void* stream);
+
+/*
  * Legacy per-head selections: out[h, c] = columns[h, c] in [0, n) ?
  * shared_rows[columns[h, c]] : -1 for h < heads, c < width.
  * Replaces the head_columns branch of resolve_rows,

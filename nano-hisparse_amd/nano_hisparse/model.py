@@ -1,7 +1,8 @@
 """A small Qwen2-shaped decoder that drives the sparse decode path.
 
 Reference: nano_hisparse/model.py:19-221. Dense layers (projections, RoPE,
-RMSNorm, SwiGLU, the prefill's causal attention) are torch operations; each
+RMSNorm, SwiGLU) are torch operations, the prefill's causal attention of a
+bf16/fp16 GPU model is the MFMA flash kernel (nhs_prefill_attention); each
 decode step appends K/V through the cache, selects pages with Quest on the
 GPU and attends over the selected rows with the HIP kernels. The module tree
 (names and construction order) is the reference's, which is HF Qwen2's, so
@@ -167,17 +168,28 @@ class Model(nn.Module):
             raise ValueError("prefill is allowed exactly once per request")
         cfg = self.config
         groups = cfg.num_attention_heads // cfg.num_key_value_heads
+        # bf16/fp16 models on a GPU run the causal attention as the MFMA
+        # flash kernel (nhs_prefill_attention): O(S) memory where the dense
+        # path materialises S x S scores per head; fp32 and CPU models keep
+        # the dense causal attention.
+        flash = (self.device.type == "cuda" and self.dtype in (torch.bfloat16, torch.float16)
+                 and cfg.head_dim in (64, 128))
+        if flash:
+            from . import row_kernels as rk
         x = self.model.embed_tokens(torch.tensor(tokens, device=self.device))
         for index, layer in enumerate(self.model.layers):
             q, k, v = self._project(layer, x, 0)
             if cache is not None:
                 cache.write(request_id, index, k, v)
-            attention = F.scaled_dot_product_attention(
-                q.transpose(0, 1),
-                k.repeat_interleave(groups, 1).transpose(0, 1),
-                v.repeat_interleave(groups, 1).transpose(0, 1),
-                is_causal=True,
-            ).transpose(0, 1)
+            if flash:
+                attention = rk.prefill_attention(q, k, v)
+            else:
+                attention = F.scaled_dot_product_attention(
+                    q.transpose(0, 1),
+                    k.repeat_interleave(groups, 1).transpose(0, 1),
+                    v.repeat_interleave(groups, 1).transpose(0, 1),
+                    is_causal=True,
+                ).transpose(0, 1)
             x = self._finish(layer, x, attention)
         return self.lm_head(self.model.norm(x[-1])).float()
 

@@ -498,3 +498,28 @@ def silu_mul(gate_up):
     status = lib.nhs_silu_mul(rows, inter, dtype_code(gate_up.dtype), _ptr(gate_up), _ptr(out), _stream(device))
     _hip.check(status, "nhs_silu_mul")
     return out
+
+
+# ---- prefill attention ---------------------------------------------------------------------
+
+
+def prefill_attention(q, k, v, out=None):
+    """Causal GQA attention of one prompt: q [S, Hq, D], k/v [S, Hkv, D]
+    (bf16 or fp16, rows may be views of a fused projection) -> [S, Hq, D]."""
+    device = _require_gpu("prefill_attention", q, k, v)
+    if q.ndim != 3 or k.ndim != 3 or k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError("prefill_attention: q [S, Hq, D], k and v [S, Hkv, D]")
+    if q.dtype != k.dtype or q.dtype != v.dtype or q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("prefill_attention: bf16 or fp16 q/k/v of one dtype")
+    if any(t.stride(2) != 1 for t in (q, k, v)):
+        raise ValueError("prefill_attention: head dims must be contiguous")
+    S, Hq, D = q.shape
+    if out is None:
+        out = torch.empty(S, Hq, D, dtype=q.dtype, device=device)
+    lib = _hip.load()
+    status = lib.nhs_prefill_attention(
+        _ptr(q), q.stride(0), q.stride(1), _ptr(k), k.stride(0), k.stride(1), _ptr(v), v.stride(0), v.stride(1),
+        dtype_code(q.dtype), S, Hq, k.shape[1], D, _ptr(out), out.stride(0), out.stride(1), _stream(device),
+    )
+    _hip.check(status, "nhs_prefill_attention")
+    return out
