@@ -419,6 +419,7 @@ def run_model_decode(args):
         torch.cuda.synchronize()
         print(f"[bench] admitted {B - len(engine.waiting)}/{B} at {time.perf_counter() - t0:.1f} s",
               file=sys.stderr, flush=True)
+    admit_s = time.perf_counter() - t0
     for _ in range(W):
         engine.step()
     torch.cuda.synchronize()
@@ -469,6 +470,7 @@ def run_model_decode(args):
         "step_roofline": {"ideal_ms": round(ideal_ms, 3), "frac": round(ideal_ms / ms_per_step, 4),
                           "hbm_bytes": hbm_bytes, "pcie_bytes": round(pcie_bytes)},
         "wall_s_timed": round(wall, 3),
+        "admit_s": round(admit_s, 2),  # untimed: every prompt prefilled, admitted requests decoding meanwhile
     }
     print(json.dumps(result), flush=True)
 

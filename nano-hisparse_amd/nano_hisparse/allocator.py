@@ -10,10 +10,12 @@ bytes may be overwritten.
 
 Besides the reference's structures the allocator keeps indexes that make the
 residency policy independent of the pool size: the bound blocks of each
-(request, layer) in binding order, a min-heap of empty blocks (stale entries
-are skipped lazily) and the number of unpinned blocks that readers still
-reference, so "allocatable blocks" is counted and enumerated in order
-without a scan.
+(request, layer) in binding order, the KV-page blocks of each (request,
+layer) that still hold their allocation reference, a min-heap of empty
+blocks (stale entries are skipped lazily) and the number of unpinned blocks
+that readers still reference, so "allocatable blocks" is counted and
+enumerated in order, and a layer's unpin candidates are found, without a
+scan.
 """
 
 from __future__ import annotations
@@ -49,6 +51,8 @@ class DeviceAllocator:
         self.occupancy: Counter = Counter()
         # (request, layer) -> {owner key: slot} in binding order
         self.group_blocks: dict[tuple, OrderedDict] = {}
+        # (request, layer) -> {owner key: slot} of KV pages (key[2] >= 0) not unpinned
+        self.group_pinned: dict[tuple, dict] = {}
         self._empty_heap = list(range(config.gpu_pages))
         self.referenced_unpinned = 0  # reclaimable blocks with reader references
 
@@ -64,6 +68,8 @@ class DeviceAllocator:
         self.lru[key] = slot
         self.occupancy[key[0]] += 1
         self.group_blocks.setdefault(key[:2], OrderedDict())[key] = slot
+        if key[2] >= 0:
+            self.group_pinned.setdefault(key[:2], {})[key] = slot
 
     def release(self, slot, fence):
         frame = self.slots[slot]
@@ -78,6 +84,7 @@ class DeviceAllocator:
         del group[owner]
         if not group:
             del self.group_blocks[owner[:2]]
+        self._drop_pinned(owner)
         frame.owner, frame.ref_cnt, frame.fence = None, 0, fence
         self.free.add(slot)
         heapq.heappush(self._empty_heap, slot)
@@ -93,8 +100,14 @@ class DeviceAllocator:
         assert frame.ref_cnt > 0
         frame.ref_cnt -= 1
         self.reclaimable[slot] = on_reuse
+        self._drop_pinned(frame.owner)
         if frame.ref_cnt:
             self.referenced_unpinned += 1
+
+    def _drop_pinned(self, key):
+        pinned = self.group_pinned.get(key[:2])
+        if pinned is not None and pinned.pop(key, None) is not None and not pinned:
+            del self.group_pinned[key[:2]]
 
     def reclaim(self, slot):
         """Take an unpinned block: its owner callback detaches the old mapping."""
@@ -155,6 +168,11 @@ class DeviceAllocator:
         if self.budget >= len(self.slots):
             return len(self.free) + len(self.reclaimable) - self.referenced_unpinned
         return len(self.available())
+
+    def pinned_pages(self, group):
+        """{owner key: slot} of the layer's KV-page blocks that still hold
+        their allocation reference (unordered)."""
+        return self.group_pinned.get(group, {})
 
     def group_keys(self, group):
         """Owner keys bound for one (request, layer), in binding order."""

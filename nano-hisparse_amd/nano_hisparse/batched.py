@@ -25,6 +25,7 @@ from __future__ import annotations
 import torch
 
 from . import row_kernels as rk
+from .hybrid import store_entry
 
 
 class BatchDecode:
@@ -113,7 +114,7 @@ class BatchDecode:
             for page in reversed(opened):
                 if page.slot is not None:
                     cache._detach(page)
-                    cache.tables[page.key[:2]].source[page.key[2]] = -1
+                    store_entry(cache.tables[page.key[:2]].source, page.key[2], -1)
                 store._unmaterialize(page)
             raise
         return pages

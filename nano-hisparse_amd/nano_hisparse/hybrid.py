@@ -25,6 +25,7 @@ of each stream.
 
 from __future__ import annotations
 
+import bisect
 import heapq
 from collections import Counter
 from contextlib import suppress
@@ -36,7 +37,7 @@ import torch
 from .allocator import DeviceAllocator
 from .config import CapacityError
 from .row_index import LogicalTopK, resolve_rows
-from .storage import HostStore, Location, PageLease
+from .storage import HostStore, Location, PageLease, upload
 
 ACTIVE_TAIL_PAGES = 2
 
@@ -119,6 +120,13 @@ class _OrderedKeys(dict):
         self.pop(key, None)
 
 
+def store_entry(table, index, value):
+    """Write one entry of a device table on the current stream as a
+    one-element fill (the value travels as a kernel argument; indexed
+    assignment of a Python number costs about three times the host time)."""
+    table[index : index + 1].fill_(value)
+
+
 class HybridKVCache:
     def __init__(self, config, hot: HotConfig):
         if config.host_pages * config.page_size >= 2**31:
@@ -133,6 +141,12 @@ class HybridKVCache:
         self._next_rank = 0
         self._dirty: set = set()  # layers that may hold unpinnable clean history
         self._awaiting: set = set()  # layers without a hot region
+        # awaiting layers holding resident pages: "active" ones may act at any
+        # tick (hot region demanded, or the resident window reached);
+        # "dormant" ones act only while allocatable blocks are below the
+        # transition watermark
+        self._awaiting_active: set = set()
+        self._dormant: set = set()
         self._sweep = None  # (heap, rank cursor, group filter) while a tick runs
         self._item_tables: dict = {}  # batch composition -> device nhs_layer_item table
         self.allocator = DeviceAllocator(config)
@@ -259,18 +273,37 @@ class HybridKVCache:
             self.storage.stats["append_resident_hits"] += 1
             return PageLease(self.storage, [page])
         slot = self._slot()
-        self.tables[page.key[:2]].source[page.key[2]] = page.host_slot
+        store_entry(self.tables[page.key[:2]].source, page.key[2], page.host_slot)
         self.storage.wait(self.storage.compute, self.allocator.slots[slot].fence)
         self._bind(page, slot, Location.RESIDENT)
         return None
 
     def _bind(self, page, slot, location):
         self.storage.bind(page, slot, location)
-        self.tables[page.key[:2]].resident[page.key[2]] = slot
+        group = page.key[:2]
+        store_entry(self.tables[group].resident, page.key[2], slot)
+        if group in self._awaiting:
+            self._file(group)
 
     def _detach(self, page):
         self.storage.detach(page)
-        self.tables[page.key[:2]].resident[page.key[2]] = -1
+        group = page.key[:2]
+        store_entry(self.tables[group].resident, page.key[2], -1)
+        if group in self._awaiting:
+            self._file(group)
+
+    def _file(self, group):
+        """Re-file an awaiting layer as active, dormant or neither (no
+        resident pages) after its residents or hot-region demand changed."""
+        self._awaiting_active.discard(group)
+        self._dormant.discard(group)
+        residents = self.storage.resident_pages[group]
+        if group not in self._awaiting or not residents:
+            return
+        if self.tables[group].hot_required or residents >= self.hot_config.resident_window_pages:
+            self._awaiting_active.add(group)
+        else:
+            self._dormant.add(group)
 
     def _tail_index(self, group):
         """Last page of a layer's history (the page being written, if any)."""
@@ -323,49 +356,93 @@ class HybridKVCache:
 
     def _unpin_clean_pages(self, group):
         """Once a layer has its hot region, its clean history gives up the
-        allocation reference (newest page first) and stays readable."""
+        allocation reference (newest page first) and stays readable. Only
+        the layer's still-pinned pages can qualify (historical, clean, not
+        yet unpinned), so only those are checked."""
         self._dirty.discard(group)
         if not self.tables[group].blocks:
             return
-        for page in sorted(self._historical_pages(group), key=lambda p: -p.key[2]):
-            if page.host_committed_version == page.content_version and page.slot not in self.allocator.reclaimable:
-                self.allocator.unpin(page.slot, self._on_block_reused)
-                self.storage.stats["clean_page_unpins"] += 1
+        pinned = self.allocator.pinned_pages(group)
+        if not pinned:
+            return
+        pages, slots = self.storage.pages, self.allocator.slots
+        last = self._tail_index(group) - ACTIVE_TAIL_PAGES
+        ready = []
+        for key, slot in pinned.items():
+            page = pages[key]
+            if (key[2] <= last and page.sealed and slots[slot].ref_cnt == 1
+                    and page.host_committed_version == page.content_version):
+                ready.append(page)
+        ready.sort(key=lambda p: -p.key[2])
+        for page in ready:
+            self.allocator.unpin(page.slot, self._on_block_reused)
+            self.storage.stats["clean_page_unpins"] += 1
 
     def _require_hot(self, group, reason):
         tables = self.tables[group]
         if not tables.hot_required:
             tables.hot_required, tables.trigger = True, reason
             self.storage.stats[f"hot_trigger_{reason}"] += 1
+            if group in self._awaiting:
+                self._file(group)
 
     def update_residency(self, request_id=None, layer=None, *, upcoming_allocation=False):
         """Publish finished mirrors and raise or serve hot-region demand,
         without blocking (reference hybrid.py:256-294): first every selected
         layer unpins its clean history, then, layer by layer in admission
         order, hot-region demand is raised and served and the layer unpins
-        again. Layers neither dirty nor awaiting a hot region are skipped
-        (both steps are no-ops for them); a layer that a later layer's
-        transition makes dirty is still visited in this tick if it comes
-        after the one being served, as in a full sweep."""
+        again. Only layers that can act are visited, in the same order as a
+        full sweep: dirty layers and active awaiting ones from a heap;
+        dormant layers (awaiting, below the resident window, no demand yet)
+        only where allocatable blocks are below the watermark when the sweep
+        reaches them, since elsewhere serving one is a no-op. Layers neither
+        dirty nor awaiting, or without resident pages, are no-ops too. A
+        layer that a later layer's transition makes dirty is still visited
+        in this tick if it comes after the one being served."""
         self.storage.check_stream()
         self._publish_clean()
         selected = self._selector(request_id, layer)
         for group in self._in_order([g for g in self._dirty if selected(g)]):
             self._unpin_clean_pages(group)
-        heap = [(self._rank[g], g) for g in self._awaiting | self._dirty if selected(g)]
+        rank_of = self._rank
+        heap = [(rank_of[g], g) for g in self._awaiting_active | self._dirty if selected(g)]
         heapq.heapify(heap)
         visited = set()
+        dormant, at = None, 0  # selected dormant layers in rank order, built on first need
         outer, self._sweep = self._sweep, [heap, -1, selected]
         try:
-            while heap:
+            while True:
+                # dormant layers ranked before the next heap layer (a serve
+                # may push one), visited while the sweep is below the watermark
+                while self._dormant and self._below_watermark(upcoming_allocation):
+                    if dormant is None:
+                        dormant = sorted((rank_of[g], g) for g in self._dormant if selected(g))
+                        at = bisect.bisect_right(dormant, (self._sweep[1], ()))
+                    while at < len(dormant) and dormant[at][1] in visited:
+                        at += 1
+                    if at == len(dormant) or (heap and dormant[at][0] > heap[0][0]):
+                        break
+                    rank, group = dormant[at]
+                    at += 1
+                    if group in self.tables:
+                        visited.add(group)
+                        self._sweep[1] = rank
+                        self._serve(group, upcoming_allocation)
+                if not heap:
+                    break
                 rank, group = heapq.heappop(heap)
                 if group in visited or group not in self.tables:
                     continue
                 visited.add(group)
                 self._sweep[1] = rank
+                if dormant is not None:
+                    at = bisect.bisect_right(dormant, (rank, ()), at)
                 self._serve(group, upcoming_allocation)
         finally:
             self._sweep = outer
+
+    def _below_watermark(self, upcoming_allocation):
+        return self.allocator.available_count() - int(upcoming_allocation) < self.transition_watermark
 
     def _serve(self, group, upcoming_allocation):
         tables = self.tables[group]
@@ -416,7 +493,8 @@ class HybridKVCache:
             self.allocator.bind(block, (request_id, layer, -i - 1))
         tables.blocks = blocks
         self._awaiting.discard(group)
-        tables.hot.copy_(torch.tensor(blocks, dtype=torch.int32, device=self.device))
+        self._file(group)
+        tables.hot.copy_(upload(blocks, torch.int32, self.device))
         tables.ready = self.storage.event(self.storage.transfer)
         self.storage.stats["hot_region_allocations"] += 1
         self._mark(group)
@@ -593,6 +671,8 @@ class HybridKVCache:
             del self._rank[key]
             self._dirty.discard(key)
             self._awaiting.discard(key)
+            self._awaiting_active.discard(key)
+            self._dormant.discard(key)
         self.collect(wait=wait)
 
     def collect(self, wait=False):
@@ -665,6 +745,17 @@ class HybridKVCache:
         store.assert_invariants()
         assert alloc.available_count() == len(self._available_blocks())
         assert self._awaiting == {g for g, t in self.tables.items() if not t.blocks}
+        window = self.hot_config.resident_window_pages
+        live = {g for g in self._awaiting if store.resident_pages[g]}
+        assert self._awaiting_active == {
+            g for g in live if self.tables[g].hot_required or store.resident_pages[g] >= window
+        }
+        assert self._dormant == live - self._awaiting_active
+        assert alloc.group_pinned == {
+            g: {k: s for k, s in b.items() if k[2] >= 0 and s not in alloc.reclaimable}
+            for g, b in alloc.group_blocks.items()
+            if any(k[2] >= 0 and s not in alloc.reclaimable for k, s in b.items())
+        }
         assert set(self._rank) == set(self.tables)
         for name, request in store.requests.items():
             assert request.extra_index_bytes == sum(t.nbytes for g, t in self.tables.items() if g[0] == name)

@@ -18,6 +18,7 @@ from torch import nn
 from torch.nn import functional as F
 
 from .selection import Selection, quest_selection, select_pages
+from .storage import upload
 
 
 @dataclass
@@ -176,7 +177,7 @@ class Model(nn.Module):
                  and cfg.head_dim in (64, 128))
         if flash:
             from . import row_kernels as rk
-        x = self.model.embed_tokens(torch.tensor(tokens, device=self.device))
+        x = self.model.embed_tokens(upload(tokens, torch.int64, self.device))
         for index, layer in enumerate(self.model.layers):
             q, k, v = self._project(layer, x, 0)
             if cache is not None:
@@ -203,7 +204,7 @@ class Model(nn.Module):
             raise ValueError("all layers must have the same nonempty history")
         position = lengths[0]
         P = cache.config.page_size
-        x = self.model.embed_tokens(torch.tensor([token], device=self.device))
+        x = self.model.embed_tokens(upload([token], torch.int64, self.device))
         for index, layer in enumerate(self.model.layers):
             q, k, v = self._project(layer, x, position)
             cache.write(request_id, index, k, v)

@@ -23,6 +23,16 @@ import torch
 from .allocator import DeviceAllocator
 from .config import CacheConfig, CapacityError
 
+
+def upload(values, dtype, device):
+    """A host list as a tensor on `device`, enqueued on the current stream
+    from pinned memory: a copy from pageable memory would block the host
+    until the device's queue drains."""
+    host = torch.tensor(values, dtype=dtype)
+    if torch.device(device).type != "cuda":
+        return host.to(device)
+    return host.pin_memory().to(device, non_blocking=True)
+
 PageKey = tuple  # (request_id, layer, page index)
 
 

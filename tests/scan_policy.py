@@ -111,6 +111,7 @@ class ScanningCache(HybridKVCache):
             self.allocator.bind(block, (request_id, layer, -i - 1))
         tables.blocks = blocks
         self._awaiting.discard(group)
+        self._file(group)  # bookkeeping only; the sweeps here ignore it
         tables.hot.copy_(torch.tensor(blocks, dtype=torch.int32, device=self.device))
         tables.ready = self.storage.event(self.storage.transfer)
         self.storage.stats["hot_region_allocations"] += 1

@@ -80,22 +80,28 @@ def _comparable(result):
     return result
 
 
-def run(seed, ops=70):
+def run(seed, ops=None):
     rng = random.Random(seed)
-    hot_rows = rng.choice([4, 8])
-    # from seed 40: no window, watermark 0 (transitions only when the last
-    # block goes) and no explicit transitions, so the pool runs full
-    pressure_only = seed >= 40
-    hot = HotConfig(
-        4,
-        hot_rows,
-        resident_window_pages=64 if pressure_only else rng.choice([2, 3, 4, 6, 64]),
-        transition_watermark=0 if pressure_only else rng.choice([None, 0, 1, 3]),
-    )
-    layers_max = 2
+    hot_rows = 4 if seed >= 60 else rng.choice([4, 8])
+    # seeds 40-59: no window, watermark 0 (transitions only when the last
+    # block goes) and no explicit transitions, so the pool runs full;
+    # from seed 60: many short requests below a window they never reach and
+    # a watermark of several blocks, so most layers wait without demand
+    # until the pool runs low mid-sweep
+    pressure_only = 40 <= seed < 60
+    dormant = seed >= 60
+    if dormant:
+        window, watermark = 64, rng.choice([2, 4, 6])
+    elif pressure_only:
+        window, watermark = 64, 0
+    else:
+        window, watermark = rng.choice([2, 3, 4, 6, 64]), rng.choice([None, 0, 1, 3])
+    hot = HotConfig(4, hot_rows, resident_window_pages=window, transition_watermark=watermark)
+    layers_max = 4 if dormant else 2
+    ops = ops or (140 if dormant else 70)
     admission = hot.admission_blocks(P, layers_max)
     cfg = CacheConfig(
-        gpu_pages=admission + rng.randrange(0, 10),
+        gpu_pages=admission + rng.randrange(0, 10) + (rng.randrange(0, 8) if dormant else 0),
         host_pages=96,
         page_size=P,
         kv_heads=1,
@@ -108,7 +114,7 @@ def run(seed, ops=70):
     for step in range(ops):
         op = rng.random()
         live = [n for n in names if n in twin.caches[0].storage.requests]
-        if op < 0.12 or not live:
+        if op < (0.25 if dormant else 0.12) or not live:
             name = f"r{step}"
             layers = rng.randint(1, layers_max)
             max_tokens = rng.randint(8, 48)
@@ -121,7 +127,8 @@ def run(seed, ops=70):
         layer = rng.randrange(request.layers)
         if op < 0.45:
             room = request.max_tokens - request.lengths[layer]
-            count = min(room, rng.choice([1, 1, 2, 3, P, 2 * P + 1])) if room else 1
+            sizes = [1, P, 2 * P + 1, 3 * P] if dormant else [1, 1, 2, 3, P, 2 * P + 1]
+            count = min(room, rng.choice(sizes)) if room else 1
             k = torch.randn(count, 1, 8, generator=gen)
             v = torch.randn(count, 1, 8, generator=gen)
             twin.do(f"{step} write {name}/{layer} x{count}", lambda c: c.write(name, layer, k.clone(), v.clone()))
@@ -147,7 +154,7 @@ def run(seed, ops=70):
                 res = twin.do(f"{step} hold lease {key}", lambda c: held.append(c.resolve(name, layer, topk)))
                 if res[0] == "ok":
                     twin.leases[key] = held
-        elif op < 0.86 and pressure_only:  # no explicit transitions: more appends instead
+        elif op < 0.86 and (pressure_only or dormant):  # no explicit transitions: more appends instead
             k = torch.randn(P, 1, 8, generator=gen)
             v = torch.randn(P, 1, 8, generator=gen)
             if request.lengths[layer] + P <= request.max_tokens:
@@ -171,7 +178,7 @@ def run(seed, ops=70):
     return twin
 
 
-@pytest.mark.parametrize("seed", range(60))
+@pytest.mark.parametrize("seed", range(80))
 def test_indexed_policy_matches_full_sweeps(cpu_kernels, seed):
     twin = run(seed)
     stats = twin.caches[0].storage.stats
@@ -181,7 +188,7 @@ def test_indexed_policy_matches_full_sweeps(cpu_kernels, seed):
 def test_random_sequences_reach_every_policy_path(cpu_kernels):
     """The seeds above exercise transitions, unpins, reuse and every trigger."""
     totals = {}
-    for seed in range(60):
+    for seed in range(80):
         stats = run(seed).caches[0].storage.stats
         for key, value in stats.items():
             totals[key] = totals.get(key, 0) + value

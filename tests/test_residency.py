@@ -244,6 +244,7 @@ def test_allocation_revisits_a_group_published_late(cpu_kernels, monkeypatch):
     slot = page.slot
     cache.allocator.reclaimable.pop(slot)
     cache.allocator.incref(slot)  # put the allocation reference back
+    cache.allocator.group_pinned.setdefault(page.key[:2], {})[page.key] = slot  # and its index entry
     page.host_committed_version = 0
     assert not cache.allocator.free
 
