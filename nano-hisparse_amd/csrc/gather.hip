@@ -12,6 +12,10 @@
 // one read of them. The grid is capped (nhs_set_gather_workgroups): a few
 // dozen workgroups already saturate the host link, and waves that wait on
 // PCIe reads would otherwise hold compute units that concurrent kernels need.
+// 16-byte rows are stored non-temporally: the gathered bytes go to HBM while
+// the kernel waits on PCIe anyway, instead of as dirty cache lines that the
+// next kernel's memory traffic would have to write back (the gather itself
+// also runs ~2% faster that way).
 #include <atomic>
 
 #include "nhs_common.h"
@@ -21,6 +25,8 @@ namespace nhs {
 constexpr int kGatherThreads = 256;
 constexpr int kRowsPerBlock = 16;  // 16 reads in flight per lane reach the copy engine's PCIe rate
 std::atomic<int> g_gather_workgroups{0};  // 0: one workgroup per group of entries
+
+typedef unsigned int gather_u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename V>
 __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char* __restrict__ host,
@@ -75,7 +81,13 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char*
       if (sb[r] >= 0) buf[r] = *reinterpret_cast<const V*>(host + sb[r] + off);
 #pragma unroll
     for (int r = 0; r < kRowsPerBlock; ++r)
-      if (db[r] >= 0) *reinterpret_cast<V*>(pool + db[r] + off) = buf[r];
+      if (db[r] >= 0) {
+        if constexpr (sizeof(V) == 16)
+          __builtin_nontemporal_store(__builtin_bit_cast(gather_u32x4, buf[r]),
+                                      reinterpret_cast<gather_u32x4*>(pool + db[r] + off));
+        else
+          *reinterpret_cast<V*>(pool + db[r] + off) = buf[r];
+      }
   }
   }
 }
