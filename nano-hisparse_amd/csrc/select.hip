@@ -89,43 +89,101 @@ __device__ __forceinline__ int page_count(const int64_t* lengths, int64_t length
 // multiplied. Chunk sums are added as a pairwise tree over a KV head's
 // lanes, the KV-head sums sequentially; the CPU oracle sums in this order.
 //
+// element e of E packed elements of T (raw 32-bit words), widened exactly to fp32
+template <typename T, int E>
+__device__ __forceinline__ float packed_elem(const uint32_t (&w)[E * T::bytes / 4], int e) {
+  if constexpr (T::bytes == 4) {
+    return __uint_as_float(w[e]);
+  } else {
+    const uint32_t word = w[e >> 1];
+    if constexpr (T::dtype == NHS_BF16)
+      return __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+    else
+      return f16_bits_to_f32((e & 1) ? (word >> 16) : (word & 0xffffu));
+  }
+}
+
 // The per-lane grouped sums (and the masks of which side has contributors).
+// Branch-free: a query value adds +0.0 to the other side's sum, which leaves
+// it unchanged (the positive sum starts at +0.0 and only grows, the
+// non-positive one starts at +0.0 and never becomes -0.0); the side flags
+// are bit e of two per-lane masks.
 template <int E, int G>
 struct GroupedQuery {
+  static_assert(E <= 32, "side masks hold one bit per element");
   float pos[E], neg[E];
-  bool has_pos[E], has_neg[E];
+  uint32_t has_pos = 0, has_neg = 0;  // bit e: a head of the group is > 0 (<= 0) at element e
   // qv: the lane's slices of the group's query heads; live: this lane holds
   // data (padding lanes add exactly +0)
   __device__ __forceinline__ void init(const float (&qv)[G][E], int group, bool live) {
 #pragma clang fp contract(off)
+    uint32_t hp_bits = 0, hn_bits = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       float p = 0.f, n = 0.f;
-      bool hp = false, hn = false;
+      uint32_t hp = 0, hn = 0;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        if (g < group) {
-          const float q = qv[g][e];
-          if (q > 0.f) {
-            p = p + q;
-            hp = true;
-          } else {
-            n = n + q;
-            hn = true;
-          }
-        }
+        const float q = qv[g][e];
+        const bool in_group = g < group;
+        const bool up = q > 0.f;
+        p = p + (in_group && up ? q : 0.f);
+        n = n + (in_group && !up ? q : 0.f);
+        hp |= (uint32_t)(in_group && up);
+        hn |= (uint32_t)(in_group && !up);
       }
       pos[e] = p, neg[e] = n;
-      has_pos[e] = hp && live, has_neg[e] = hn && live;
+      hp_bits |= hp << e;
+      hn_bits |= hn << e;
     }
+    has_pos = live ? hp_bits : 0u;
+    has_neg = live ? hn_bits : 0u;
+  }
+  // init() from the heads' slices kept packed in T (widened element by element)
+  // (all G heads are in the group)
+  template <typename T>
+  __device__ __forceinline__ void init_packed(const uint32_t (&qw)[G][E * T::bytes / 4], bool live) {
+#pragma clang fp contract(off)
+    uint32_t hp_bits = 0, hn_bits = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      float p = 0.f, n = 0.f;
+      uint32_t hp = 0, hn = 0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float q = packed_elem<T, E>(qw[g], e);
+        const bool up = q > 0.f;
+        p = p + (up ? q : 0.f);
+        n = n + (up ? 0.f : q);
+        hp |= (uint32_t)up;
+        hn |= (uint32_t)!up;
+      }
+      pos[e] = p, neg[e] = n;
+      hp_bits |= hp << e;
+      hn_bits |= hn << e;
+    }
+    has_pos = live ? hp_bits : 0u;
+    has_neg = live ? hn_bits : 0u;
+  }
+  // chunk() of bounds kept packed in T
+  template <typename T>
+  __device__ __forceinline__ float chunk_packed(const uint32_t (&mn)[E * T::bytes / 4],
+                                                const uint32_t (&mx)[E * T::bytes / 4]) const {
+    float x = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      x = __builtin_fmaf((has_neg >> e) & 1u ? packed_elem<T, E>(mn, e) : 0.f, neg[e], x);
+      x = __builtin_fmaf((has_pos >> e) & 1u ? packed_elem<T, E>(mx, e) : 0.f, pos[e], x);
+    }
+    return x;
   }
   // this lane's chunk sum for one page's bounds
   __device__ __forceinline__ float chunk(const float (&mn)[E], const float (&mx)[E]) const {
     float x = 0.f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      x = __builtin_fmaf(has_neg[e] ? mn[e] : 0.f, neg[e], x);
-      x = __builtin_fmaf(has_pos[e] ? mx[e] : 0.f, pos[e], x);
+      x = __builtin_fmaf((has_neg >> e) & 1u ? mn[e] : 0.f, neg[e], x);
+      x = __builtin_fmaf((has_pos >> e) & 1u ? mx[e] : 0.f, pos[e], x);
     }
     return x;
   }
@@ -201,10 +259,11 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
 
 // Page kernel, for pages that fit one wave (kv_heads * lanes per head <=
 // 64, 32-byte chunks): lane = (page of the wave, kv head, chunk). A wave
-// loads its query slices straight into registers, forms the grouped sums,
-// issues the bounds of all its kPageSlots page slots, then scores them one
-// by one: per-lane chunk sum, DPP tree over a KV head's lanes, and the
-// sequential KV-head sum read across lanes, with no barrier.
+// loads its query slices straight into registers, issues the bounds of all
+// its kPageSlots page slots, forms the grouped sums, then scores the slots
+// one by one: per-lane chunk sum, DPP tree over a KV head's lanes, and the
+// sequential KV-head sum read across lanes, with no barrier. It is
+// instantiated for each group size G (1..8), so no head is masked.
 constexpr int kPageThreads = 256;
 constexpr int kPageWaves = kPageThreads / kWave;
 constexpr int kPageSlots = 4;
@@ -226,46 +285,65 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   const int sub = within & ((1 << a.lpr_log2) - 1);
   const bool data = page_local < ppw && sub < a.lanes_used;
 
-  // query slices: with the bounds' dtype and 16-byte rows, every head's
-  // vector loads are issued before the first is used
-  float qv[G][E];
+  // Query slices and bounds stay packed in their dtype until folded or
+  // scored (widening them at load time doubled the registers and halved
+  // the waves a SIMD holds). The bounds of every slot are requested before
+  // the query slices are used, so the two memory latencies overlap.
+  constexpr int W = E * T::bytes / 4;  // 32-bit words of a lane's 32-byte chunk
   int64_t qi[G];
 #pragma unroll
   for (int g = 0; g < G; ++g)
-    qi[g] = (int64_t)b * a.q_bs + (data && g < a.group ? (int64_t)(kh * a.group + g) * a.q_hs + sub * E : 0);
-  if (a.q_vec && a.q_dtype == T::dtype) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) load_vec<T, E>(a.q, qi[g], qv[g]);
-  } else {
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < E; ++e) qv[g][e] = load_elem(a.q, a.q_dtype, qi[g] + (data ? e : 0));
-  }
-  // (GroupedQuery ignores heads past the group and lanes without data)
-  // the bounds of every slot are requested before the query slices are
-  // used, so the two memory latencies overlap
+    qi[g] = (int64_t)b * a.q_bs + (data ? (int64_t)(kh * G + g) * a.q_hs + sub * E : 0);
   const char *lo, *hi;
   bounds_of<T>(a, b, lo, hi);
   const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
   const int64_t lane_off = data ? (int64_t)kh * a.head_dim + sub * E : 0;
-  float mn[kPageSlots][E], mx[kPageSlots][E];
+  uint32_t mn[kPageSlots][W], mx[kPageSlots][W];
+  auto load_bounds = [&]() {
 #pragma unroll
-  for (int s = 0; s < kPageSlots; ++s) {
-    const int p = wave_first + s * ppw + page_local;
-    const int pc = p < count ? p : wave_first;  // lanes past the end reread a live page
-    load_vec<T, E>(lo, (int64_t)pc * page_elems + lane_off, mn[s]);
-    load_vec<T, E>(hi, (int64_t)pc * page_elems + lane_off, mx[s]);
+    for (int s = 0; s < kPageSlots; ++s) {
+      const int p = wave_first + s * ppw + page_local;
+      const int pc = p < count ? p : wave_first;  // lanes past the end reread a live page
+      const uint4* lp = reinterpret_cast<const uint4*>(lo + ((int64_t)pc * page_elems + lane_off) * T::bytes);
+      const uint4* hp = reinterpret_cast<const uint4*>(hi + ((int64_t)pc * page_elems + lane_off) * T::bytes);
+#pragma unroll
+      for (int v = 0; v < W / 4; ++v) {
+        const uint4 x = lp[v], y = hp[v];
+        mn[s][4 * v] = x.x, mn[s][4 * v + 1] = x.y, mn[s][4 * v + 2] = x.z, mn[s][4 * v + 3] = x.w;
+        mx[s][4 * v] = y.x, mx[s][4 * v + 1] = y.y, mx[s][4 * v + 2] = y.z, mx[s][4 * v + 3] = y.w;
+      }
+    }
+  };
+  GroupedQuery<E, G> gq;  // G is the group size here: nothing to mask
+  if (a.q_vec && a.q_dtype == T::dtype) {
+    uint32_t qw[G][W];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint4* qp = reinterpret_cast<const uint4*>(static_cast<const char*>(a.q) + qi[g] * T::bytes);
+#pragma unroll
+      for (int v = 0; v < W / 4; ++v) {
+        const uint4 x = qp[v];
+        qw[g][4 * v] = x.x, qw[g][4 * v + 1] = x.y, qw[g][4 * v + 2] = x.z, qw[g][4 * v + 3] = x.w;
+      }
+    }
+    load_bounds();
+    gq.template init_packed<T>(qw, data);
+  } else {
+    float qv[G][E];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < E; ++e) qv[g][e] = load_elem(a.q, a.q_dtype, qi[g] + (data ? e : 0));
+    load_bounds();
+    gq.init(qv, G, data);
   }
-  GroupedQuery<E, G> gq;
-  gq.init(qv, a.group, data);
   const int lpr = 1 << a.lpr_log2;
   const int page_lane0 = page_local * lanes_per_page;
 #pragma unroll
   for (int s = 0; s < kPageSlots; ++s) {
     const int p0 = wave_first + s * ppw;
     if (p0 >= count) break;
-    const float t = group_sum(gq.chunk(mn[s], mx[s]), lpr);
+    const float t = group_sum(gq.template chunk_packed<T>(mn[s], mx[s]), lpr);
     // sequential sum over the page's KV heads (every lane takes part in the
     // lane reads; the page's first lane stores)
     float total = 0.f;
@@ -576,11 +654,12 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
     a.pages_per_block = kPageWaves * kPageSlots * ppw;
     grid = dim3((unsigned)((max_pages + a.pages_per_block - 1) / a.pages_per_block), (unsigned)batch);
     block = dim3(kPageThreads);
-    switch (bounds_dtype * 8 + G) {
+    switch (bounds_dtype * 16 + a.group) {  // instantiated for every group size: no masked heads
 #define NHS_PAGE_CASE(DT, TY, EE, GG) \
-  case DT * 8 + GG: kernel = quest_page_kernel<TY, EE, GG>; break;
-#define NHS_PAGE_GS(DT, TY, EE) \
-  NHS_PAGE_CASE(DT, TY, EE, 1) NHS_PAGE_CASE(DT, TY, EE, 2) NHS_PAGE_CASE(DT, TY, EE, 4) NHS_PAGE_CASE(DT, TY, EE, 8)
+  case DT * 16 + GG: kernel = quest_page_kernel<TY, EE, GG>; break;
+#define NHS_PAGE_GS(DT, TY, EE)                                                                         \
+  NHS_PAGE_CASE(DT, TY, EE, 1) NHS_PAGE_CASE(DT, TY, EE, 2) NHS_PAGE_CASE(DT, TY, EE, 3) NHS_PAGE_CASE(DT, TY, EE, 4) \
+  NHS_PAGE_CASE(DT, TY, EE, 5) NHS_PAGE_CASE(DT, TY, EE, 6) NHS_PAGE_CASE(DT, TY, EE, 7) NHS_PAGE_CASE(DT, TY, EE, 8)
       NHS_PAGE_GS(NHS_F32, F32, 8)
       NHS_PAGE_GS(NHS_F16, F16, 16)
       NHS_PAGE_GS(NHS_BF16, BF16, 16)

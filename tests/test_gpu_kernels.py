@@ -287,6 +287,47 @@ def test_quest_select_bit_exact(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, n_pages, 
             assert torch.equal(scores[b, :count].view(torch.int32), e_scores[b, :count].view(torch.int32))
 
 
+@pytest.mark.parametrize(
+    "dtype,B,Hq,Hkv,D,P,n_pages,top",
+    [
+        (torch.bfloat16, 3, 32, 8, 128, 64, 96, 8),  # 4 query heads per KV head
+        (torch.bfloat16, 3, 28, 4, 128, 32, 96, 8),  # 7 per KV head
+        (torch.float32, 2, 8, 2, 64, 16, 50, 6),
+        (torch.float16, 2, 6, 2, 128, 16, 50, 6),  # 3 per KV head
+    ],
+)
+def test_quest_scores_with_special_values_bit_exact(gpu, dtype, B, Hq, Hkv, D, P, n_pages, top):
+    """Queries and bounds holding +-inf, NaN, +-0 and exact ties: every score
+    (NaN where the oracle's is NaN) and every selection equal the oracle's."""
+    log_case(test="quest-special", dtype=dtype, B=B, Hq=Hq, Hkv=Hkv, D=D, n_pages=n_pages)
+    g = torch.Generator().manual_seed(D + Hq)
+    q = torch.randn(B, Hq, D, generator=g)
+    pick = torch.randint(0, 8, q.shape, generator=g)
+    q[pick == 0] = 0.0
+    q[pick == 1] = -0.0
+    q[0, 1, 3], q[0, 2, 5], q[1, 0, 7] = float("inf"), float("-inf"), float("nan")
+    q = q.to(dtype)
+    mn, mx = _bounds(g, B, n_pages, Hkv, D, dtype, offsets=False)
+    mn, mx = mn.float(), mx.float()
+    mn[:, 5], mx[:, 5] = mn[:, 4], mx[:, 4]  # an exact tie between pages 4 and 5
+    mx[0, 7, 0, 1] = float("inf")
+    mn[0, 8, 1, 2] = float("-inf")
+    mx[1, 9, 0, :] = float("nan")
+    mn[2 % B, 10, Hkv - 1, D - 1] = float("-inf")
+    mn[:, 11], mx[:, 11] = 0.0, -0.0
+    mn, mx = mn.to(dtype), mx.to(dtype)
+    lengths = torch.full((B,), n_pages * P)
+    e_scores, e_pages, e_pos = oracle.quest_select(q, mn, mx, lengths, P, top)
+    pages, pos, scores = rk.quest_batched(q.to(gpu), mn.to(gpu), mx.to(gpu), lengths.to(gpu), P, top)
+    scores = scores.cpu()[:, :n_pages]
+    nan = torch.isnan(e_scores[:, :n_pages])
+    assert torch.equal(torch.isnan(scores), nan)
+    assert torch.equal(scores[~nan].view(torch.int32), e_scores[:, :n_pages][~nan].view(torch.int32))
+    assert nan.any() and torch.isinf(e_scores[:, :n_pages]).any()
+    assert torch.equal(pages.cpu(), e_pages)
+    assert torch.equal(pos.cpu(), e_pos)
+
+
 def test_quest_known_answers(gpu):
     """tests/test_selection.py:18-33 of the reference."""
     log_case(test="quest-kat")
