@@ -303,6 +303,18 @@ int nhs_rope(int32_t rows, int32_t heads, int32_t head_dim, int32_t dtype, void*
 int nhs_silu_mul(int32_t rows, int32_t inter, int32_t dtype, const void* gate_up, void* out, void* stream);
 
 /*
+ * Linear layer for up to 16 token rows (decode): y[m, n] = sum_k x[m, k] *
+ * w[n, k] (+ bias[n]), bf16 or fp16 (dtype), fp32 accumulation, one
+ * rounding. w is [n, k] row-major (torch Linear weight layout); n a multiple
+ * of 16, k of 256; strides in elements (x and w rows 16-byte aligned); bias
+ * may be NULL. Replaces the decode projections of the reference's layers
+ * (model.py:43-71, nn.Linear q/k/v/o and gate/up/down, and the lm_head at
+ * model.py:221), which at decode batch sizes stream the weights.
+ */
+int nhs_linear_small_m(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, const void* bias,
+                       int32_t dtype, int32_t m, int32_t n, int32_t k, void* y, int64_t y_row_stride, void* stream);
+
+/*
  * Causal GQA self-attention over one prompt (prefill), flash-attention style
  * on MFMA: out[s, h] = softmax_{t <= s}(q[s, h] . k[t, h / g] * D^-1/2) .
  * v[t, h / g] for s < seq, g = q_heads / kv_heads, fp32 accumulation. bf16 or

@@ -1,0 +1,140 @@
+// Linear layer for a handful of token rows (decode): y[m, n] = sum_k x[m, k]
+// * w[n, k] (+ bias[n]), m < 16, bf16 or fp16 in and out, fp32 accumulation.
+//
+// At decode batch sizes the product is a stream of the weight matrix (2
+// bytes per weight, 16 flops or fewer), so the kernel is built to read the
+// weights at the HBM rate: a workgroup of 8 waves owns RT tiles of 16
+// weight rows and the full K; wave w takes the K slice [w K/8, (w+1) K/8)
+// and walks it in 32-wide k steps with v_mfma_f32_16x16x32, the weight
+// rows as the A operand (lane l: row l % 16, elements (l / 16) * 8 .. +7 of
+// the step) and the token rows as the B operand (lane l: token l % 16, the
+// same elements; tokens past m read as zero). Each wave keeps kUnroll steps
+// of weight loads in flight. The 8 partial tiles are added through LDS in
+// wave order, the bias is added in fp32 and the sum is rounded once.
+#include "nhs_common.h"
+
+namespace nhs {
+
+constexpr int kLinWaves = 8;
+constexpr int kLinThreads = kLinWaves * kWave;
+constexpr int kLinUnroll = 8;  // k steps of weight loads in flight per wave
+
+typedef __bf16 lin_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 lin_f16x8 __attribute__((ext_vector_type(8)));
+typedef float lin_f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ lin_f32x4 lin_mfma(uint4 a, uint4 b, lin_f32x4 c) {
+  if constexpr (T::dtype == NHS_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(lin_bf16x8, a), __builtin_bit_cast(lin_bf16x8, b),
+                                                  c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(lin_f16x8, a), __builtin_bit_cast(lin_f16x8, b), c,
+                                                 0, 0, 0);
+}
+
+struct LinearArgs {
+  const char* x;
+  const char* w;
+  const char* bias;  // may be null
+  char* y;
+  int64_t ldx, ldw, ldy;  // row strides in elements
+  int m, n, k;
+};
+
+template <typename T, int RT>
+__global__ __launch_bounds__(kLinThreads) void linear_small_m_kernel(LinearArgs a) {
+  __shared__ __attribute__((aligned(16))) float red[kLinWaves][RT][kWave * 4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n0 = blockIdx.x * RT * 16;
+  const int row = lane & 15, kq = (lane >> 4) * 8;  // MFMA operand row and element offset
+  const int slice = a.k / kLinWaves;
+  const int k_begin = wave * slice;
+  const int steps = slice / 32;
+  // tokens past m read row 0 and are zeroed (no branch between load and use)
+  const bool live_tok = row < a.m;
+  const char* xp = a.x + ((int64_t)(live_tok ? row : 0) * a.ldx + k_begin + kq) * T::bytes;
+  const char* wp[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) wp[rt] = a.w + ((int64_t)(n0 + rt * 16 + row) * a.ldw + k_begin + kq) * T::bytes;
+  lin_f32x4 acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) acc[rt] = (lin_f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < steps; s0 += kLinUnroll) {
+    const int n_steps = min(kLinUnroll, steps - s0);  // uniform
+    uint4 wv[kLinUnroll][RT], xv[kLinUnroll];
+#pragma unroll
+    for (int u = 0; u < kLinUnroll; ++u) {
+      const int s = s0 + (u < n_steps ? u : 0);  // past the slice: reread a live step, unused
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) wv[u][rt] = *reinterpret_cast<const uint4*>(wp[rt] + (int64_t)s * 32 * T::bytes);
+      xv[u] = *reinterpret_cast<const uint4*>(xp + (int64_t)s * 32 * T::bytes);
+    }
+#pragma unroll
+    for (int u = 0; u < kLinUnroll; ++u) {
+      if (u < n_steps) {
+        const uint4 xb = live_tok ? xv[u] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt] = lin_mfma<T>(wv[u][rt], xb, acc[rt]);
+      }
+    }
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+    *reinterpret_cast<float4*>(&red[wave][rt][lane * 4]) = make_float4(acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]);
+  __syncthreads();
+  // D lane l holds weight rows (l / 16) * 4 + i of the tile, token l % 16
+  for (int t = threadIdx.x; t < RT * kWave * 4; t += kLinThreads) {
+    const int rt = t / (kWave * 4), r = t - rt * kWave * 4;
+    const int l = r >> 2, i = r & 3;
+    const int tok = l & 15;
+    if (tok >= a.m) continue;
+    float v = red[0][rt][r];
+#pragma unroll
+    for (int w = 1; w < kLinWaves; ++w) v += red[w][rt][r];
+    const int n = n0 + rt * 16 + (l >> 4) * 4 + i;
+    if (a.bias) v += load_elem(a.bias, T::dtype, n);
+    store_elem(a.y, T::dtype, (int64_t)tok * a.ldy + n, v);
+  }
+}
+
+}  // namespace nhs
+
+extern "C" int nhs_linear_small_m(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride,
+                                  const void* bias, int32_t dtype, int32_t m, int32_t n, int32_t k, void* y,
+                                  int64_t y_row_stride, void* stream) {
+  using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
+  const char* who = "nhs_linear_small_m";
+  if (!x || !w || !y) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
+  if (dtype != NHS_BF16 && dtype != NHS_F16) return fail(NHS_ERR_UNSUPPORTED, "%s: bf16 or fp16 only", who);
+  if (m < 1 || m > 16 || n < 16 || k < 1) return fail(NHS_ERR_INVALID, "%s: needs 1 <= m <= 16, n >= 16", who);
+  if (n % 16 || k % (kLinWaves * 32))
+    return fail(NHS_ERR_UNSUPPORTED, "%s: n must be a multiple of 16 and k of %d", who, kLinWaves * 32);
+  if (x_row_stride < k || w_row_stride < k || y_row_stride < n || x_row_stride % 8 || w_row_stride % 8)
+    return fail(NHS_ERR_INVALID, "%s: bad row strides", who);
+  if (((uintptr_t)x | (uintptr_t)w) % 16) return fail(NHS_ERR_INVALID, "%s: x and w must be 16-byte aligned", who);
+  LinearArgs a;
+  a.x = static_cast<const char*>(x);
+  a.w = static_cast<const char*>(w);
+  a.bias = static_cast<const char*>(bias);
+  a.y = static_cast<char*>(y);
+  a.ldx = x_row_stride, a.ldw = w_row_stride, a.ldy = y_row_stride;
+  a.m = m, a.n = n, a.k = k;
+  hipStream_t s = (hipStream_t)stream;
+  // two 16-row tiles per workgroup once that still gives two workgroups per CU
+  const bool wide = n % 32 == 0 && n / 32 >= 512;
+  const dim3 grid((unsigned)(wide ? n / 32 : n / 16)), block(kLinThreads);
+  if (dtype == NHS_BF16) {
+    if (wide)
+      launch(linear_small_m_kernel<BF16, 2>, grid, block, 0, s, ev.start, ev.stop, a);
+    else
+      launch(linear_small_m_kernel<BF16, 1>, grid, block, 0, s, ev.start, ev.stop, a);
+  } else {
+    if (wide)
+      launch(linear_small_m_kernel<F16, 2>, grid, block, 0, s, ev.start, ev.stop, a);
+    else
+      launch(linear_small_m_kernel<F16, 1>, grid, block, 0, s, ev.start, ev.stop, a);
+  }
+  return launch_status(who);
+}

@@ -63,6 +63,7 @@ SIGNATURES = {
     "nhs_add_rmsnorm": ([_i32, _i32, _i32, _p, _p, _i32, _p, ctypes.c_float, _p, _p], ctypes.c_int),
     "nhs_rope": ([_i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p], ctypes.c_int),
     "nhs_silu_mul": ([_i32, _i32, _i32, _p, _p, _p], ctypes.c_int),
+    "nhs_linear_small_m": ([_p, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _p, _i64, _p], ctypes.c_int),
     "nhs_prefill_attention": (
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i64, _p],
         ctypes.c_int,

@@ -332,7 +332,7 @@ class _Group:
         qkv_w, qkv_b, _ = fused
         self.gu_w = fused[2]
         h = rk.add_rmsnorm(self.x, self.delta, layer.input_layernorm.weight, _eps(layer.input_layernorm, cfg))
-        qkv = F.linear(h, qkv_w, qkv_b)
+        qkv = _linear(h, qkv_w, qkv_b)
         rk.rope_(qkv, Hq + Hkv, D, self.cos, self.sin)
         q = qkv[:, : Hq * D].view(B, Hq, D)
         k = qkv[:, Hq * D: (Hq + Hkv) * D].view(B, Hkv, D)
@@ -347,11 +347,31 @@ class _Group:
         cfg, B = self.cfg, len(self.x)
         attention = self.step.finish(self.handle)
         o_proj = layer.self_attn.o_proj
-        o = F.linear(attention.reshape(B, -1), o_proj.weight, o_proj.bias)
+        o = _linear(attention.reshape(B, -1), o_proj.weight, o_proj.bias)
         norm2 = layer.post_attention_layernorm
         h = rk.add_rmsnorm(self.x, o, norm2.weight, _eps(norm2, cfg))
         down = layer.mlp.down_proj
         self.delta = F.linear(rk.silu_mul(F.linear(h, self.gu_w)), down.weight, down.bias)
+
+# weight matrices up to this many elements take nhs_linear_small_m at decode
+# batch sizes (q/k/v and o of an 8B-class layer: 12-25 M); hipBLASLt's
+# kernels are faster on the larger gate/up, down and lm_head matrices
+_SMALL_M_MAX_WEIGHTS = 32 << 20
+
+
+def _linear(x, weight, bias):
+    """x @ weight.T + bias for a decode batch: the MFMA weight-stream kernel
+    where it is the faster one, else torch."""
+    from . import row_kernels as rk
+
+    m, k = x.shape
+    n = weight.shape[0]
+    if (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and weight.dtype == x.dtype and m <= 16
+            and n % 16 == 0 and k % 256 == 0 and n * k <= _SMALL_M_MAX_WEIGHTS and x.stride(1) == 1
+            and weight.is_contiguous() and (bias is None or bias.is_contiguous())):
+        return rk.linear_small_m(x, weight, bias)
+    return F.linear(x, weight, bias)
+
 
 def _eps(norm, cfg):
     return getattr(norm, "eps", getattr(norm, "variance_epsilon", cfg.rms_norm_eps))

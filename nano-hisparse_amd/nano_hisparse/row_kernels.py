@@ -523,3 +523,33 @@ def prefill_attention(q, k, v, out=None):
     )
     _hip.check(status, "nhs_prefill_attention")
     return out
+
+
+# ---- decode linear layers --------------------------------------------------------------------
+
+
+def linear_small_m(x, weight, bias=None, out=None):
+    """y = x @ weight.T (+ bias) for x [m <= 16, k], weight [n, k] (bf16 or
+    fp16, one dtype); the weight stream of a decode projection."""
+    device = _require_gpu("linear_small_m", x, weight)
+    if x.ndim != 2 or weight.ndim != 2 or x.shape[1] != weight.shape[1]:
+        raise ValueError("linear_small_m: x [m, k], weight [n, k]")
+    if x.dtype != weight.dtype or x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("linear_small_m: bf16 or fp16 x and weight of one dtype")
+    if x.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError("linear_small_m: rows must be contiguous")
+    m, k = x.shape
+    n = weight.shape[0]
+    if bias is not None and (bias.shape != (n,) or bias.dtype != x.dtype or not bias.is_contiguous()):
+        raise ValueError("linear_small_m: bias must be a contiguous [n] vector of the same dtype")
+    if out is None:
+        out = torch.empty(m, n, dtype=x.dtype, device=device)
+    elif out.shape != (m, n) or out.dtype != x.dtype or out.stride(1) != 1:
+        raise ValueError("linear_small_m: out must be [m, n] with contiguous rows")
+    lib = _hip.load()
+    status = lib.nhs_linear_small_m(
+        _ptr(x), x.stride(0), _ptr(weight), weight.stride(0), _ptr(bias),
+        dtype_code(x.dtype), m, n, k, _ptr(out), out.stride(0), _stream(device),
+    )
+    _hip.check(status, "nhs_linear_small_m")
+    return out

@@ -1,0 +1,61 @@
+"""Decode linear layers (nhs_linear_small_m) against an fp32 reference of
+torch's nn.Linear on the same bf16/fp16 inputs: within 2 units in the last
+place of the output dtype relative to the largest output magnitude of the row
+(the kernel rounds one fp32 sum once; the order of the K sum differs), at the
+Llama-3-8B decode shapes (q/k/v fused with bias, o, gate/up fused, down,
+lm_head) and ragged token counts."""
+
+import pytest
+import torch
+
+from nano_hisparse import row_kernels as rk
+
+
+def log_case(**kw):
+    print("case:", kw, flush=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,n,k,bias", [(8, 6144, 4096, True), (8, 4096, 4096, False), (8, 28672, 4096, False),
+                                        (8, 4096, 14336, False), (3, 4096, 256, True), (1, 16, 256, False),
+                                        (16, 512, 512, True), (13, 2048, 1024, False)])
+def test_linear_small_m_matches_fp32_reference(gpu, dtype, m, n, k, bias):
+    log_case(test="linear", dtype=str(dtype), m=m, n=n, k=k, bias=bias)
+    g = torch.Generator(device=gpu).manual_seed(n + k + m)
+    x = torch.randn(m, k, generator=g, device=gpu).to(dtype)
+    w = (torch.randn(n, k, generator=g, device=gpu) / k ** 0.5).to(dtype)
+    b = torch.randn(n, generator=g, device=gpu).to(dtype) if bias else None
+    y = rk.linear_small_m(x, w, b)
+    ref = x.float() @ w.float().t().contiguous()
+    if bias:
+        ref = ref + b.float()
+    eps = torch.finfo(dtype).eps
+    scale = ref.abs().amax(1, keepdim=True).clamp_min(1e-3)
+    assert ((y.float() - ref).abs() / scale).max().item() <= 2 * eps
+
+
+@pytest.mark.gpu
+def test_linear_small_m_strided_rows_and_out(gpu):
+    """x and out as row slices of wider buffers (the fused projection layout)."""
+    log_case(test="linear-strided")
+    g = torch.Generator(device=gpu).manual_seed(1)
+    big = torch.randn(5, 1024 + 64, generator=g, device=gpu).to(torch.bfloat16)
+    x = big[:, 32:32 + 1024]
+    w = (torch.randn(256, 1024, generator=g, device=gpu) / 32).to(torch.bfloat16)
+    out_big = torch.zeros(5, 256 + 16, device=gpu, dtype=torch.bfloat16)
+    out = out_big[:, 16:]
+    rk.linear_small_m(x, w, out=out)
+    ref = x.float() @ w.float().t().contiguous()
+    assert ((out.float() - ref).abs() / ref.abs().amax(1, keepdim=True)).max().item() <= 2 * torch.finfo(torch.bfloat16).eps
+    assert torch.equal(out_big[:, :16], torch.zeros_like(out_big[:, :16]))
+
+
+@pytest.mark.gpu
+def test_linear_small_m_rejects_unsupported_shapes(gpu):
+    x = torch.zeros(17, 256, device=gpu, dtype=torch.bfloat16)
+    w = torch.zeros(16, 256, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="m <= 16"):
+        rk.linear_small_m(x, w)
+    with pytest.raises(RuntimeError, match="multiple"):
+        rk.linear_small_m(x[:4, :200], w[:, :200])
