@@ -306,7 +306,7 @@ int nhs_silu_mul(int32_t rows, int32_t inter, int32_t dtype, const void* gate_up
  * Linear layer for up to 16 token rows (decode): y[m, n] = sum_k x[m, k] *
  * w[n, k] (+ bias[n]), bf16 or fp16 (dtype), fp32 accumulation, one
  * rounding. w is [n, k] row-major (torch Linear weight layout); n a multiple
- * of 16, k of 256; strides in elements (x and w rows 16-byte aligned); bias
+ * of 16, k of 2048; strides in elements (x and w rows 16-byte aligned); bias
  * may be NULL. Replaces the decode projections of the reference's layers
  * (model.py:43-71, nn.Linear q/k/v/o and gate/up/down, and the lm_head at
  * model.py:221), which at decode batch sizes stream the weights.

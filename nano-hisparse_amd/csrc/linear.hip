@@ -3,21 +3,20 @@
 //
 // At decode batch sizes the product is a stream of the weight matrix (2
 // bytes per weight, 16 flops or fewer), so the kernel is built to read the
-// weights at the HBM rate: a workgroup of 8 waves owns RT tiles of 16
-// weight rows and the full K; wave w takes the K slice [w K/8, (w+1) K/8)
-// and walks it in 32-wide k steps with v_mfma_f32_16x16x32, the weight
-// rows as the A operand (lane l: row l % 16, elements (l / 16) * 8 .. +7 of
-// the step) and the token rows as the B operand (lane l: token l % 16, the
-// same elements; tokens past m read as zero). Each wave keeps kUnroll steps
-// of weight loads in flight. The 8 partial tiles are added through LDS in
-// wave order, the bias is added in fp32 and the sum is rounded once.
+// weights at the HBM rate: a workgroup of 8 waves owns a tile of 16 weight
+// rows and the full K; wave w takes the K slice [w K/8, (w+1) K/8) and walks
+// it in windows of 256 k, 32-wide steps with v_mfma_f32_16x16x32, the
+// weight rows as the A operand (lane l: row l % 16, elements (l / 16) * 8
+// .. +7 of the step) and the token rows as the B operand (lane l: token
+// l % 16, the same elements; tokens past m read as zero). The 8 partial
+// tiles are added through LDS in wave order, the bias is added in fp32 and
+// the sum is rounded once.
 #include "nhs_common.h"
 
 namespace nhs {
 
 constexpr int kLinWaves = 8;
 constexpr int kLinThreads = kLinWaves * kWave;
-constexpr int kLinUnroll = 8;  // k steps of weight loads in flight per wave
 
 typedef __bf16 lin_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 lin_f16x8 __attribute__((ext_vector_type(8)));
@@ -42,40 +41,54 @@ struct LinearArgs {
   int m, n, k;
 };
 
+// Weight rows are read as 512-byte row segments (two rows per load
+// instruction, whole cache lines), written to the wave's own LDS region and
+// read back in the MFMA operand layout: loaded straight in that layout a
+// load instruction would cover 16 rows x 64 bytes, which streams at ~4.3
+// TB/s against ~5.6 TB/s for long row segments. The region is private to
+// the wave and LDS executes a wave's operations in order, so no barrier is
+// needed between the writes and the reads.
+constexpr int kLinWindow = 256;                       // k elements staged per window (512 bytes of a row)
+constexpr int kLinRowBytes = kLinWindow * 2 + 16;     // staged row pitch (padded)
+
 template <typename T, int RT>
 __global__ __launch_bounds__(kLinThreads) void linear_small_m_kernel(LinearArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char lin_lds[];
   __shared__ __attribute__((aligned(16))) float red[kLinWaves][RT][kWave * 4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  char* stage = lin_lds + (size_t)wave * RT * 16 * kLinRowBytes;  // this wave's [RT * 16 rows][512 B]
   const int n0 = blockIdx.x * RT * 16;
   const int row = lane & 15, kq = (lane >> 4) * 8;  // MFMA operand row and element offset
-  const int slice = a.k / kLinWaves;
+  const int slice = a.k / kLinWaves;                 // a multiple of kLinWindow
   const int k_begin = wave * slice;
-  const int steps = slice / 32;
   // tokens past m read row 0 and are zeroed (no branch between load and use)
   const bool live_tok = row < a.m;
   const char* xp = a.x + ((int64_t)(live_tok ? row : 0) * a.ldx + k_begin + kq) * T::bytes;
-  const char* wp[RT];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) wp[rt] = a.w + ((int64_t)(n0 + rt * 16 + row) * a.ldw + k_begin + kq) * T::bytes;
+  // load mapping: instruction j covers tile rows 2j, 2j + 1 (lanes 0-31, 32-63), 16 bytes per lane
+  const int lrow = lane >> 5, lcol = (lane & 31) * 16;
+  const char* wrow = a.w + ((int64_t)(n0 + lrow) * a.ldw + k_begin) * T::bytes + lcol;
   lin_f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = (lin_f32x4){0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < steps; s0 += kLinUnroll) {
-    const int n_steps = min(kLinUnroll, steps - s0);  // uniform
-    uint4 wv[kLinUnroll][RT], xv[kLinUnroll];
+  constexpr int kLoads = RT * 8;  // 16 rows per tile, two per instruction
+  for (int w0 = 0; w0 < slice; w0 += kLinWindow) {
+    uint4 wv[kLoads], xv[kLinWindow / 32];
 #pragma unroll
-    for (int u = 0; u < kLinUnroll; ++u) {
-      const int s = s0 + (u < n_steps ? u : 0);  // past the slice: reread a live step, unused
+    for (int j = 0; j < kLoads; ++j)
+      wv[j] = *reinterpret_cast<const uint4*>(wrow + ((int64_t)(2 * j) * a.ldw + w0) * T::bytes);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) wv[u][rt] = *reinterpret_cast<const uint4*>(wp[rt] + (int64_t)s * 32 * T::bytes);
-      xv[u] = *reinterpret_cast<const uint4*>(xp + (int64_t)s * 32 * T::bytes);
-    }
+    for (int s = 0; s < kLinWindow / 32; ++s)
+      xv[s] = *reinterpret_cast<const uint4*>(xp + (int64_t)(w0 + s * 32) * T::bytes);
 #pragma unroll
-    for (int u = 0; u < kLinUnroll; ++u) {
-      if (u < n_steps) {
-        const uint4 xb = live_tok ? xv[u] : make_uint4(0u, 0u, 0u, 0u);
+    for (int j = 0; j < kLoads; ++j)
+      *reinterpret_cast<uint4*>(stage + (2 * j + lrow) * kLinRowBytes + lcol) = wv[j];
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) acc[rt] = lin_mfma<T>(wv[u][rt], xb, acc[rt]);
+    for (int s = 0; s < kLinWindow / 32; ++s) {
+      const uint4 xb = live_tok ? xv[s] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const uint4 wa = *reinterpret_cast<const uint4*>(stage + (rt * 16 + row) * kLinRowBytes + (s * 32 + kq) * 2);
+        acc[rt] = lin_mfma<T>(wa, xb, acc[rt]);
       }
     }
   }
@@ -109,8 +122,8 @@ extern "C" int nhs_linear_small_m(const void* x, int64_t x_row_stride, const voi
   if (!x || !w || !y) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
   if (dtype != NHS_BF16 && dtype != NHS_F16) return fail(NHS_ERR_UNSUPPORTED, "%s: bf16 or fp16 only", who);
   if (m < 1 || m > 16 || n < 16 || k < 1) return fail(NHS_ERR_INVALID, "%s: needs 1 <= m <= 16, n >= 16", who);
-  if (n % 16 || k % (kLinWaves * 32))
-    return fail(NHS_ERR_UNSUPPORTED, "%s: n must be a multiple of 16 and k of %d", who, kLinWaves * 32);
+  if (n % 16 || k % (kLinWaves * kLinWindow))
+    return fail(NHS_ERR_UNSUPPORTED, "%s: n must be a multiple of 16 and k of %d", who, kLinWaves * kLinWindow);
   if (x_row_stride < k || w_row_stride < k || y_row_stride < n || x_row_stride % 8 || w_row_stride % 8)
     return fail(NHS_ERR_INVALID, "%s: bad row strides", who);
   if (((uintptr_t)x | (uintptr_t)w) % 16) return fail(NHS_ERR_INVALID, "%s: x and w must be 16-byte aligned", who);
@@ -122,19 +135,11 @@ extern "C" int nhs_linear_small_m(const void* x, int64_t x_row_stride, const voi
   a.ldx = x_row_stride, a.ldw = w_row_stride, a.ldy = y_row_stride;
   a.m = m, a.n = n, a.k = k;
   hipStream_t s = (hipStream_t)stream;
-  // two 16-row tiles per workgroup once that still gives two workgroups per CU
-  const bool wide = n % 32 == 0 && n / 32 >= 512;
-  const dim3 grid((unsigned)(wide ? n / 32 : n / 16)), block(kLinThreads);
-  if (dtype == NHS_BF16) {
-    if (wide)
-      launch(linear_small_m_kernel<BF16, 2>, grid, block, 0, s, ev.start, ev.stop, a);
-    else
-      launch(linear_small_m_kernel<BF16, 1>, grid, block, 0, s, ev.start, ev.stop, a);
-  } else {
-    if (wide)
-      launch(linear_small_m_kernel<F16, 2>, grid, block, 0, s, ev.start, ev.stop, a);
-    else
-      launch(linear_small_m_kernel<F16, 1>, grid, block, 0, s, ev.start, ev.stop, a);
-  }
+  const dim3 grid((unsigned)(n / 16)), block(kLinThreads);
+  const size_t lds = (size_t)kLinWaves * 16 * kLinRowBytes;  // 8 waves x 16 staged rows
+  if (dtype == NHS_BF16)
+    launch(linear_small_m_kernel<BF16, 1>, grid, block, lds, s, ev.start, ev.stop, a);
+  else
+    launch(linear_small_m_kernel<F16, 1>, grid, block, lds, s, ev.start, ev.stop, a);
   return launch_status(who);
 }

@@ -301,7 +301,7 @@ class Model(nn.Module):
         for g in groups:
             g.step.end()
         x = torch.cat([g.x + g.delta for g in groups])
-        return self.lm_head(self.model.norm(x)).float()
+        return _linear(self.model.norm(x), self.lm_head.weight, self.lm_head.bias).float()
 
 
 class _Group:
@@ -351,24 +351,19 @@ class _Group:
         norm2 = layer.post_attention_layernorm
         h = rk.add_rmsnorm(self.x, o, norm2.weight, _eps(norm2, cfg))
         down = layer.mlp.down_proj
-        self.delta = F.linear(rk.silu_mul(F.linear(h, self.gu_w)), down.weight, down.bias)
-
-# weight matrices up to this many elements take nhs_linear_small_m at decode
-# batch sizes (q/k/v and o of an 8B-class layer: 12-25 M); hipBLASLt's
-# kernels are faster on the larger gate/up, down and lm_head matrices
-_SMALL_M_MAX_WEIGHTS = 32 << 20
-
+        self.delta = _linear(rk.silu_mul(_linear(h, self.gu_w, None)), down.weight, down.bias)
 
 def _linear(x, weight, bias):
     """x @ weight.T + bias for a decode batch: the MFMA weight-stream kernel
-    where it is the faster one, else torch."""
+    (nhs_linear_small_m) for bf16/fp16 batches of up to 16 rows whose shapes
+    it takes, else torch."""
     from . import row_kernels as rk
 
     m, k = x.shape
     n = weight.shape[0]
     if (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and weight.dtype == x.dtype and m <= 16
-            and n % 16 == 0 and k % 256 == 0 and n * k <= _SMALL_M_MAX_WEIGHTS and x.stride(1) == 1
-            and weight.is_contiguous() and (bias is None or bias.is_contiguous())):
+            and n % 16 == 0 and k % 2048 == 0 and x.stride(1) == 1 and weight.is_contiguous()
+            and (bias is None or bias.is_contiguous())):
         return rk.linear_small_m(x, weight, bias)
     return F.linear(x, weight, bias)
 

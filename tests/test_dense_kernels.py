@@ -81,18 +81,20 @@ def test_silu_mul_matches_torch(gpu, dtype):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("hidden", [128, 256])  # 256: q/k/v and o take nhs_linear_small_m in bf16
+# (2048, 16, 4): q/k/v and o take nhs_linear_small_m in bf16
+@pytest.mark.parametrize("hidden,heads,kv_heads", [(128, 8, 2), (2048, 16, 4)])
 @pytest.mark.parametrize("micro_batches", [1, 2])
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 0.15)])
-def test_fused_batched_step_matches_per_request_decode(gpu, dtype, tol, micro_batches, hidden):
+def test_fused_batched_step_matches_per_request_decode(gpu, dtype, tol, micro_batches, hidden, heads, kv_heads):
     print("case:", dict(dtype=str(dtype), micro_batches=micro_batches, hidden=hidden), flush=True)
     torch.manual_seed(7)
-    cfg = ModelConfig(hidden_size=hidden, intermediate_size=2 * hidden, num_hidden_layers=2, num_attention_heads=8,
-                      num_key_value_heads=2, vocab_size=100)
+    cfg = ModelConfig(hidden_size=hidden, intermediate_size=2 * hidden, num_hidden_layers=2,
+                      num_attention_heads=heads, num_key_value_heads=kv_heads, vocab_size=100)
     model = Model(cfg).eval().to(gpu).to(dtype)
     caches = [
-        HybridKVCache(CacheConfig(gpu_pages=64, host_pages=256, page_size=4, kv_heads=2, head_dim=hidden // 8,
-                                  dtype=dtype, device=gpu), HotConfig(16, 32, resident_window_pages=4))
+        HybridKVCache(CacheConfig(gpu_pages=64, host_pages=256, page_size=4, kv_heads=kv_heads,
+                                  head_dim=hidden // heads, dtype=dtype, device=gpu),
+                      HotConfig(16, 32, resident_window_pages=4))
         for _ in range(2)
     ]
     prompts = {"a": list(range(3, 40)), "b": list(range(1, 23)), "c": list(range(9, 60))}

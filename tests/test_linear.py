@@ -18,8 +18,8 @@ def log_case(**kw):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,n,k,bias", [(8, 6144, 4096, True), (8, 4096, 4096, False), (8, 28672, 4096, False),
-                                        (8, 4096, 14336, False), (3, 4096, 256, True), (1, 16, 256, False),
-                                        (16, 512, 512, True), (13, 2048, 1024, False)])
+                                        (8, 4096, 14336, False), (3, 4096, 2048, True), (1, 16, 2048, False),
+                                        (16, 512, 6144, True), (13, 2064, 4096, False)])
 def test_linear_small_m_matches_fp32_reference(gpu, dtype, m, n, k, bias):
     log_case(test="linear", dtype=str(dtype), m=m, n=n, k=k, bias=bias)
     g = torch.Generator(device=gpu).manual_seed(n + k + m)
@@ -40,9 +40,9 @@ def test_linear_small_m_strided_rows_and_out(gpu):
     """x and out as row slices of wider buffers (the fused projection layout)."""
     log_case(test="linear-strided")
     g = torch.Generator(device=gpu).manual_seed(1)
-    big = torch.randn(5, 1024 + 64, generator=g, device=gpu).to(torch.bfloat16)
-    x = big[:, 32:32 + 1024]
-    w = (torch.randn(256, 1024, generator=g, device=gpu) / 32).to(torch.bfloat16)
+    big = torch.randn(5, 2048 + 64, generator=g, device=gpu).to(torch.bfloat16)
+    x = big[:, 32:32 + 2048]
+    w = (torch.randn(256, 2048, generator=g, device=gpu) / 45).to(torch.bfloat16)
     out_big = torch.zeros(5, 256 + 16, device=gpu, dtype=torch.bfloat16)
     out = out_big[:, 16:]
     rk.linear_small_m(x, w, out=out)
@@ -53,9 +53,9 @@ def test_linear_small_m_strided_rows_and_out(gpu):
 
 @pytest.mark.gpu
 def test_linear_small_m_rejects_unsupported_shapes(gpu):
-    x = torch.zeros(17, 256, device=gpu, dtype=torch.bfloat16)
-    w = torch.zeros(16, 256, device=gpu, dtype=torch.bfloat16)
+    x = torch.zeros(17, 2048, device=gpu, dtype=torch.bfloat16)
+    w = torch.zeros(16, 2048, device=gpu, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="m <= 16"):
         rk.linear_small_m(x, w)
     with pytest.raises(RuntimeError, match="multiple"):
-        rk.linear_small_m(x[:4, :200], w[:, :200])
+        rk.linear_small_m(x[:4, :1024], w[:, :1024])
