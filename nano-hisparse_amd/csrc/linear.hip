@@ -3,20 +3,19 @@
 //
 // At decode batch sizes the product is a stream of the weight matrix (2
 // bytes per weight, 16 flops or fewer), so the kernel is built to read the
-// weights at the HBM rate: a workgroup of 8 waves owns a tile of 16 weight
-// rows and the full K; wave w takes the K slice [w K/8, (w+1) K/8) and walks
+// weights at the HBM rate: a workgroup of W waves (8..16) owns a tile of 16
+// weight rows and the full K; wave w takes the K slice [w K/W, (w+1) K/W) and walks
 // it in windows of 256 k, 32-wide steps with v_mfma_f32_16x16x32, the
 // weight rows as the A operand (lane l: row l % 16, elements (l / 16) * 8
 // .. +7 of the step) and the token rows as the B operand (lane l: token
-// l % 16, the same elements; tokens past m read as zero). The 8 partial
+// l % 16, the same elements; tokens past m read as zero). The W partial
 // tiles are added through LDS in wave order, the bias is added in fp32 and
 // the sum is rounded once.
 #include "nhs_common.h"
 
 namespace nhs {
 
-constexpr int kLinWaves = 8;
-constexpr int kLinThreads = kLinWaves * kWave;
+constexpr int kLinMinWaves = 8, kLinMaxWaves = 16;  // waves per workgroup: K slices
 
 typedef __bf16 lin_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 lin_f16x8 __attribute__((ext_vector_type(8)));
@@ -52,14 +51,16 @@ constexpr int kLinWindow = 256;                       // k elements staged per w
 constexpr int kLinRowBytes = kLinWindow * 2 + 16;     // staged row pitch (padded)
 
 template <typename T, int RT>
-__global__ __launch_bounds__(kLinThreads) void linear_small_m_kernel(LinearArgs a) {
+__global__ __launch_bounds__(kLinMaxWaves * kWave) void linear_small_m_kernel(LinearArgs a) {
+  // dynamic LDS: each wave's staged rows, then the partial tiles [waves][RT][64 * 4]
   extern __shared__ __attribute__((aligned(16))) char lin_lds[];
-  __shared__ __attribute__((aligned(16))) float red[kLinWaves][RT][kWave * 4];
+  const int waves = (int)(blockDim.x >> 6);
+  float* red = reinterpret_cast<float*>(lin_lds + (size_t)waves * RT * 16 * kLinRowBytes);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   char* stage = lin_lds + (size_t)wave * RT * 16 * kLinRowBytes;  // this wave's [RT * 16 rows][512 B]
   const int n0 = blockIdx.x * RT * 16;
   const int row = lane & 15, kq = (lane >> 4) * 8;  // MFMA operand row and element offset
-  const int slice = a.k / kLinWaves;                 // a multiple of kLinWindow
+  const int slice = a.k / waves;                     // a multiple of kLinWindow
   const int k_begin = wave * slice;
   // tokens past m read row 0 and are zeroed (no branch between load and use)
   const bool live_tok = row < a.m;
@@ -92,19 +93,20 @@ __global__ __launch_bounds__(kLinThreads) void linear_small_m_kernel(LinearArgs 
       }
     }
   }
+  constexpr int kTile = kWave * 4;  // partial tile floats per wave and row tile
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
-    *reinterpret_cast<float4*>(&red[wave][rt][lane * 4]) = make_float4(acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]);
+    *reinterpret_cast<float4*>(&red[(wave * RT + rt) * kTile + lane * 4]) =
+        make_float4(acc[rt][0], acc[rt][1], acc[rt][2], acc[rt][3]);
   __syncthreads();
   // D lane l holds weight rows (l / 16) * 4 + i of the tile, token l % 16
-  for (int t = threadIdx.x; t < RT * kWave * 4; t += kLinThreads) {
-    const int rt = t / (kWave * 4), r = t - rt * kWave * 4;
+  for (int t = threadIdx.x; t < RT * kTile; t += (int)blockDim.x) {
+    const int rt = t / kTile, r = t - rt * kTile;
     const int l = r >> 2, i = r & 3;
     const int tok = l & 15;
     if (tok >= a.m) continue;
-    float v = red[0][rt][r];
-#pragma unroll
-    for (int w = 1; w < kLinWaves; ++w) v += red[w][rt][r];
+    float v = red[rt * kTile + r];
+    for (int w = 1; w < waves; ++w) v += red[(w * RT + rt) * kTile + r];
     const int n = n0 + rt * 16 + (l >> 4) * 4 + i;
     if (a.bias) v += load_elem(a.bias, T::dtype, n);
     store_elem(a.y, T::dtype, (int64_t)tok * a.ldy + n, v);
@@ -122,8 +124,8 @@ extern "C" int nhs_linear_small_m(const void* x, int64_t x_row_stride, const voi
   if (!x || !w || !y) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
   if (dtype != NHS_BF16 && dtype != NHS_F16) return fail(NHS_ERR_UNSUPPORTED, "%s: bf16 or fp16 only", who);
   if (m < 1 || m > 16 || n < 16 || k < 1) return fail(NHS_ERR_INVALID, "%s: needs 1 <= m <= 16, n >= 16", who);
-  if (n % 16 || k % (kLinWaves * kLinWindow))
-    return fail(NHS_ERR_UNSUPPORTED, "%s: n must be a multiple of 16 and k of %d", who, kLinWaves * kLinWindow);
+  if (n % 16 || k % (kLinMinWaves * kLinWindow))
+    return fail(NHS_ERR_UNSUPPORTED, "%s: n must be a multiple of 16 and k of %d", who, kLinMinWaves * kLinWindow);
   if (x_row_stride < k || w_row_stride < k || y_row_stride < n || x_row_stride % 8 || w_row_stride % 8)
     return fail(NHS_ERR_INVALID, "%s: bad row strides", who);
   if (((uintptr_t)x | (uintptr_t)w) % 16) return fail(NHS_ERR_INVALID, "%s: x and w must be 16-byte aligned", who);
@@ -135,8 +137,18 @@ extern "C" int nhs_linear_small_m(const void* x, int64_t x_row_stride, const voi
   a.ldx = x_row_stride, a.ldw = w_row_stride, a.ldy = y_row_stride;
   a.m = m, a.n = n, a.k = k;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)(n / 16)), block(kLinThreads);
-  const size_t lds = (size_t)kLinWaves * 16 * kLinRowBytes;  // 8 waves x 16 staged rows
+  // waves per workgroup: the most K slices (8..16) that divide the windows
+  // and leave every wave at least two (more loads in flight when the grid
+  // is small, e.g. 14 for k = 14336)
+  const int windows = k / kLinWindow;
+  int waves = kLinMinWaves;
+  for (int w = kLinMaxWaves; w > kLinMinWaves; --w)
+    if (windows % w == 0 && windows / w >= 2) {
+      waves = w;
+      break;
+    }
+  const dim3 grid((unsigned)(n / 16)), block((unsigned)(waves * kWave));
+  const size_t lds = (size_t)waves * 16 * kLinRowBytes + (size_t)waves * kWave * 4 * sizeof(float);
   if (dtype == NHS_BF16)
     launch(linear_small_m_kernel<BF16, 1>, grid, block, lds, s, ev.start, ev.stop, a);
   else
