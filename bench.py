@@ -20,8 +20,9 @@ gather; with one chunk everything runs in order on one stream (--side-stream
 moves the gather to a second stream ordered by events). Every timed step
 resolves against its own copy of the resolver's starting tags/LRU, made
 before the timed region, so every step has the same 25% misses. In the timed
-region only the attention launches stamp timing events (the roofline's
-launch time); per-stage times come from a second, fully stamped pass.
+region the gather and attention launches stamp timing events (the two
+roofline kernels' launch times); the Quest and resolver times come from a
+second, fully stamped pass.
 Prints one JSON line.
 
 `--copy-calibration` instead runs a plain 256 MiB device-to-device copy three
@@ -541,12 +542,18 @@ def main():
     print(f"[bench] counts resident/hot/miss = {counts_sum}, valid rows {valid_rows}, chunks {chunk_requests}",
           file=sys.stderr, flush=True)
 
-    # timed region: K steps, synchronized on both sides. Only the attention
-    # launches (the roofline kernel) stamp timing events here: a stamped
-    # launch costs a few microseconds more, so the per-stage breakdown comes
-    # from a second pass of K steps below, stamped at every launch.
+    # timed region: K steps, synchronized on both sides. The launches of the
+    # two roofline kernels, gather and attention, stamp timing events here
+    # (measured: with the gather unstamped, the attention's own stamps read
+    # ~1.7 us longer, and neither an idle delay nor a small kernel between
+    # the two changes that). A stamped launch costs a few microseconds, so
+    # the Quest and resolver times come from a second pass of K steps below,
+    # stamped at every launch.
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    attn_events = [{"attention": step.timing_events()["attention"]} for _ in range(args.steps)]
+    attn_events = []
+    for _ in range(args.steps):
+        full = step.timing_events()
+        attn_events.append({"gather": full["gather"], "attention": full["attention"]})
     states = fresh_states(w, args.steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -561,6 +568,7 @@ def main():
     # per stage: summed over the launches (chunks) of a step, then averaged over steps
     attn_launch_us = (1e3 * sum(a.elapsed_time(b) for ev in attn_events for a, b in ev["attention"])
                       / args.steps / len(result.chunks))
+    gather_us = 1e3 * sum(a.elapsed_time(b) for ev in attn_events for a, b in ev["gather"]) / args.steps
     step_events = [step.timing_events() for _ in range(args.steps)]
     states = fresh_states(w, args.steps)
     torch.cuda.synchronize()
@@ -573,6 +581,7 @@ def main():
     stamped_ms = p0.elapsed_time(p1) / args.steps
     kernel_us = {n: 1e3 * sum(a.elapsed_time(b) for ev in step_events for a, b in ev[n]) / args.steps
                  for n in names}
+    kernel_us["gather"] = gather_us  # from the timed pass, like the attention's launch time
     del states
 
     # measured pinned H2D copy ceiling (copy engine), for reference
@@ -634,8 +643,9 @@ def main():
             "parallelism": "single GPU",
         },
         "step_us": round(ms_per_step * 1e3, 2),
-        # per-stage launch times from a second pass of K steps that stamps
-        # every launch (that pass's step time: stamped_step_us)
+        # per-stage launch times: gather from the timed pass, the others from a
+        # second pass of K steps that stamps every launch (its step time:
+        # stamped_step_us)
         "kernel_us": {n: round(v, 2) for n, v in kernel_us.items()},
         "stamped_step_us": round(stamped_ms * 1e3, 2),
         "roofline": {
