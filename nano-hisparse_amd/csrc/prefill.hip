@@ -2,7 +2,7 @@
 //
 // out[s, h] = softmax_{t <= s}(q[s, h] . k[t, h/g] * D^-1/2) . v[t, h/g] for
 // one prompt of `seq` tokens, bf16 or fp16 in, fp32 accumulation. A
-// workgroup of 4 waves owns 64 queries of one query head (16 per wave) and
+// workgroup of 8 waves owns 128 queries of one query head (16 per wave) and
 // walks the key tiles of 64 up to the diagonal with an online softmax.
 //
 // MFMA v_mfma_f32_16x16x32 (bf16 / f16): lane l supplies row l%16 of A and
@@ -25,7 +25,7 @@
 
 namespace nhs {
 
-constexpr int kPfWaves = 4;
+constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kPfBM = 16 * kPfWaves;  // queries per workgroup
 constexpr int kPfBN = 64;             // keys per tile
@@ -44,13 +44,18 @@ __device__ __forceinline__ pf_f32x4 mfma16x16x32(uint4 a, uint4 b, pf_f32x4 c) {
                                                  0, 0, 0);
 }
 
-// two fp32 weights as a packed pair of the input dtype (round to nearest even)
+typedef float pf_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 pf_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 pf_f16x2 __attribute__((ext_vector_type(2)));
+
+// two fp32 weights as a packed pair of the input dtype (round to nearest
+// even, by the hardware conversions)
 template <typename T>
 __device__ __forceinline__ uint32_t pf_pack(float lo, float hi) {
   if constexpr (T::dtype == NHS_BF16)
-    return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((pf_f32x2){lo, hi}, pf_bf16x2));
   else
-    return (uint32_t)f32_to_f16_bits(lo) | ((uint32_t)f32_to_f16_bits(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((pf_f32x2){lo, hi}, pf_f16x2));
 }
 template <typename T>
 __device__ __forceinline__ float pf_unpack(uint32_t v, int half) {
@@ -81,8 +86,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_kernel(PrefillAr
   constexpr int DB = D / 16;   // 16-wide dim blocks of the output
   constexpr int KROW = D * 2 + 16;       // bytes per K row in LDS (padded)
   constexpr int VROW = kPfBN * 2 + 16;   // bytes per V^T row in LDS (padded)
-  __shared__ __attribute__((aligned(16))) char ks_lds[kPfBN * KROW];
-  __shared__ __attribute__((aligned(16))) char vt_lds[D * VROW];
+  // two buffers per tile: tile t+1 is stored while tile t is read, one barrier per tile
+  __shared__ __attribute__((aligned(16))) char ks_buf[2][kPfBN * KROW];
+  __shared__ __attribute__((aligned(16))) char vt_buf[2][D * VROW];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, n = lane & 15;
@@ -108,16 +114,19 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_kernel(PrefillAr
 #pragma unroll
   for (int b = 0; b < DB; ++b) o[b] = (pf_f32x4){0.f, 0.f, 0.f, 0.f};
 
-  // tile staging: thread t loads K row t/4's dims [(t%4)*D/4, +D/4) and the
-  // 4 V rows 4*(t/16) .. +3 at dims 8*(t%16) .. +7 (D = 128; D = 64 uses the
+  // tile staging: thread t loads K row t/KT's dims [(t%KT)*D/KT, +D/KT) and
+  // the VR V rows VR*(t/16) .. +VR-1 at dims 8*(t%16) .. +7 (D = 64 uses the
   // first half of the threads for V)
-  constexpr int KCH = D * 2 / 4 / 16;  // 16-byte chunks of K per thread (D/4 elements)
-  const int krow = tid >> 2, kcol = (tid & 3) * (D / 4);
+  constexpr int KT = kPfThreads / kPfBN;        // threads per K row
+  constexpr int KCH = D * 2 / KT / 16;          // 16-byte chunks of K per thread
+  constexpr int VR = kPfBN * 16 / kPfThreads;   // V rows per thread (16 groups of 8 dims)
+  static_assert(KCH >= 1 && (VR == 2 || VR == 4), "tile staging layout");
+  const int krow = tid / KT, kcol = (tid % KT) * (D / KT);
   const int vkg = tid >> 4, vdg = tid & 15;
   const bool v_thread = vdg * 8 < D;
   const int last_key = min(a.seq, q0 + kPfBM) - 1;
   const int n_tiles = last_key / kPfBN + 1;
-  uint4 kreg[KCH], vreg[4];
+  uint4 kreg[KCH], vreg[VR];
   auto load_tile = [&](int t0) {
     const int kr = min(t0 + krow, a.seq - 1);  // rows past the end re-read the last key (masked below)
     const char* kp = a.k + ((int64_t)kr * a.k_s + (int64_t)kvh * a.k_h + kcol) * T::bytes;
@@ -125,33 +134,46 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_kernel(PrefillAr
     for (int c = 0; c < KCH; ++c) kreg[c] = *reinterpret_cast<const uint4*>(kp + c * 16);
     if (v_thread)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int vr = min(t0 + vkg * 4 + r, a.seq - 1);
+      for (int r = 0; r < VR; ++r) {
+        const int vr = min(t0 + vkg * VR + r, a.seq - 1);
         vreg[r] = *reinterpret_cast<const uint4*>(a.v + ((int64_t)vr * a.v_s + (int64_t)kvh * a.v_h + vdg * 8) * T::bytes);
       }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](int buf) {
+    char* ks_lds = ks_buf[buf];
+    char* vt_lds = vt_buf[buf];
 #pragma unroll
     for (int c = 0; c < KCH; ++c)
       *reinterpret_cast<uint4*>(ks_lds + krow * KROW + kcol * T::bytes + c * 16) = kreg[c];
     if (v_thread)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {  // V^T[dim 8*vdg + j][keys 4*vkg .. +3]
+      for (int j = 0; j < 8; ++j) {  // V^T[dim 8*vdg + j][keys VR*vkg .. +VR-1]
         const int half = j & 1, w = j >> 1;
         const uint32_t e0 = pf_get16(vreg[0], w, half), e1 = pf_get16(vreg[1], w, half);
-        const uint32_t e2 = pf_get16(vreg[2], w, half), e3 = pf_get16(vreg[3], w, half);
-        *reinterpret_cast<uint2*>(vt_lds + (vdg * 8 + j) * VROW + vkg * 4 * 2) =
-            make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+        char* dst = vt_lds + (vdg * 8 + j) * VROW + vkg * VR * 2;
+        if constexpr (VR == 4) {
+          const uint32_t e2 = pf_get16(vreg[2], w, half), e3 = pf_get16(vreg[3], w, half);
+          *reinterpret_cast<uint2*>(dst) = make_uint2(e0 | (e1 << 16), e2 | (e3 << 16));
+        } else {
+          *reinterpret_cast<uint32_t*>(dst) = e0 | (e1 << 16);
+        }
       }
   };
 
   load_tile(0);
+  store_tile(0);
+  if (n_tiles > 1) load_tile(kPfBN);
   for (int t = 0; t < n_tiles; ++t) {
     const int t0 = t * kPfBN;
-    __syncthreads();  // the previous tile's LDS reads are done
-    store_tile();
+    // tile t's buffer is complete and every wave is done with tile t-1's
+    // buffer, which now takes tile t+1 (loaded during tile t-1's math)
     __syncthreads();
-    if (t + 1 < n_tiles) load_tile(t0 + kPfBN);  // in flight during this tile's math
+    if (t + 1 < n_tiles) {
+      store_tile((t + 1) & 1);
+      if (t + 2 < n_tiles) load_tile(t0 + 2 * kPfBN);  // in flight during this tile's math
+    }
+    const char* ks_lds = ks_buf[t & 1];
+    const char* vt_lds = vt_buf[t & 1];
 
     // S^T for 4 key blocks of 16: s[kb] holds keys t0 + kb*16 + g4*4 + i
     pf_f32x4 s[4];
@@ -164,17 +186,28 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attention_kernel(PrefillAr
         s[kb] = mfma16x16x32<T>(kf, qf[st], s[kb]);
       }
     }
-    // scale, mask (causal and past the end), running max
+    // scale, mask (causal and past the end; a tile wholly below the wave's
+    // diagonal and inside the prompt needs none), running max
     float mx = m;
+    if (t0 + kPfBN - 1 <= q0 + wave * 16 && t0 + kPfBN <= a.seq) {  // uniform over the wave
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = t0 + kb * 16 + g4 * 4 + i;
-        const float x = (key <= query && key < a.seq) ? s[kb][i] * a.scale_log2 : -INFINITY;
-        s[kb][i] = x;
-        mx = fmaxf(mx, x);
-      }
+        for (int i = 0; i < 4; ++i) {
+          s[kb][i] = s[kb][i] * a.scale_log2;
+          mx = fmaxf(mx, s[kb][i]);
+        }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = t0 + kb * 16 + g4 * 4 + i;
+          const float x = (key <= query && key < a.seq) ? s[kb][i] * a.scale_log2 : -INFINITY;
+          s[kb][i] = x;
+          mx = fmaxf(mx, x);
+        }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float ref = mx == -INFINITY ? 0.f : mx;
