@@ -339,7 +339,7 @@ def run_resolver_stress(args):
         _, positions, _ = rk.quest_batched(queries[i], minimum, maximum, g_len, P, top)
         if events:
             rk.set_launch_events(*events[1])
-        rk.resolve_batched(positions, g_src, g_res, g_hot, g_tags, g_lru, g_len, P, counts_total=totals)
+        return rk.resolve_batched(positions, g_src, g_res, g_hot, g_tags, g_lru, g_len, P, counts_total=totals)[0]
 
     for i in range(args.warmup):
         step(i)
@@ -348,13 +348,31 @@ def run_resolver_stress(args):
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(args.steps):
-        step(args.warmup + i, ev[i])
+        physical = step(args.warmup + i, ev[i])
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     quest_us = 1e3 * sum(e[0][0].elapsed_time(e[0][1]) for e in ev) / args.steps
     resolve_us = 1e3 * sum(e[1][0].elapsed_time(e[1][1]) for e in ev) / args.steps
     resident_hits, hot_hits, misses = (t / args.steps for t in totals.tolist())
+
+    # attention at the same shape (untimed by the step above): the last
+    # step's rows over a pool of random bf16 K/V, per-launch time from events
+    pool = torch.randn(next_block, 2, P, Hkv, D, generator=g, device=device).to(torch.bfloat16)
+    out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=device)
+    attn_q = queries[-1]
+    for _ in range(3):
+        rk.attend_batched(attn_q, pool, physical, P, out=out)
+    attn_ev = [rk.timing_events() for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for e in attn_ev:
+        rk.set_launch_events(*e)
+        rk.attend_batched(attn_q, pool, physical, P, out=out)
+    torch.cuda.synchronize()
+    attn_us = 1e3 * sum(a.elapsed_time(b) for a, b in attn_ev) / args.steps
+    valid_rows = int((physical >= 0).sum())
+    attn_bytes = valid_rows * 2 * Hkv * D * 2 + B * (2 * Hq * D * 2 + 8 * K)
+    del pool
     result = {
         "metric": METRIC,
         "value": round(B / (ms * 1e-3), 1),
@@ -377,6 +395,10 @@ def run_resolver_stress(args):
         },
         "kernel_us": {"quest": round(quest_us, 2), "resolve": round(resolve_us, 2)},
         "rows_per_step": {"resident_hits": resident_hits, "hot_hits": hot_hits, "misses": misses},
+        # attention over the same selections, timed separately (not part of value)
+        "attention": {"launch_us": round(attn_us, 2), "algorithmic_bytes": attn_bytes,
+                      "achieved_gbs": round(attn_bytes / (attn_us * 1e-6) / 1e9, 1),
+                      "frac_of_hbm_peak": round(attn_bytes / (attn_us * 1e-6) / HBM_PEAK, 4)},
     }
     print(json.dumps(result), flush=True)
 
