@@ -133,23 +133,6 @@ def test_attend_rows_masking_edge_cases(gpu):
 # ---- resolver -----------------------------------------------------------------------
 
 
-def test_resolver_known_answer(gpu):
-    """tests/test_selection.py:36-50 of the reference, plus the LRU post-state."""
-    log_case(test="resolve-kat")
-    t32 = lambda v: torch.tensor([v], dtype=torch.int32, device=gpu)  # noqa: E731
-    source, resident, hot = t32([5, 2, 9, 4]), t32([-1, 7, -1, 3]), t32([6, 1])
-    tags = t32([-1, -1, -1, -1, -1, 22, -1, -1])
-    lru = torch.tensor([[0, 1, 2, 3, 4, 6, 7, 5]], dtype=torch.int64, device=gpu)
-    positions = torch.tensor([[9, 2, 6, 9, 14, -1]], dtype=torch.int64, device=gpu)
-    phys, mh, md, counts = rk.resolve_batched(positions, source, resident, hot, tags, lru, 16, 4)
-    assert phys[0].tolist() == [24, 5, 30, -1, 14, -1]
-    assert counts[0].tolist() == [2, 1, 1]
-    assert mh[0].tolist() == [37, -1, -1, -1, -1, -1]
-    assert md[0].tolist() == [24, -1, -1, -1, -1, -1]
-    assert tags[0].tolist() == [37, -1, -1, -1, -1, 22, -1, -1]
-    assert lru[0].tolist() == [1, 2, 3, 4, 6, 7, 0, 5]
-
-
 def make_resolver_state(rng, B, H, P, n_pages, host_pages, pool_blocks, resident_frac, tag_frac):
     """Random but consistent tables: distinct host slots per page, distinct
     resident blocks, hot blocks disjoint from resident blocks, unique tags."""
@@ -326,22 +309,6 @@ def test_quest_scores_with_special_values_bit_exact(gpu, dtype, B, Hq, Hkv, D, P
     assert nan.any() and torch.isinf(e_scores[:, :n_pages]).any()
     assert torch.equal(pages.cpu(), e_pages)
     assert torch.equal(pos.cpu(), e_pos)
-
-
-def test_quest_known_answers(gpu):
-    """tests/test_selection.py:18-33 of the reference."""
-    log_case(test="quest-kat")
-    low = torch.tensor([[[-10.0, 0.0]], [[1.0, 0.0]], [[0.0, 0.0]]])
-    high = torch.tensor([[[10.0, 0.0]], [[1.0, 0.0]], [[0.0, 0.0]]])
-    pages, pos, _ = rk.quest_batched(
-        torch.tensor([[[1.0, 0.0]]], device=gpu), low[None].to(gpu), high[None].to(gpu), 5, 2, 2, keep_sink=False
-    )
-    assert pages[0].tolist() == [0, 2]
-    assert pos[0].tolist() == [0, 1, 4, -1]
-    bounds = torch.tensor([[[9.0, 0.0]], [[0.0, 10.0]], [[-1.0, -1.0]]])[None].to(gpu)
-    pages, pos, _ = rk.quest_batched(torch.eye(2, device=gpu)[None], bounds, bounds, 5, 2, 2, keep_sink=False)
-    assert pages[0].tolist() == [1, 2]
-    assert pos[0].tolist() == [2, 3, 4, -1]
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,P,n_pages,top", [(4, 32, 8, 128, 64, 512, 32), (3, 4, 2, 8, 4, 20, 1),

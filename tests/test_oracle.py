@@ -1,8 +1,9 @@
 """The CPU oracle pinned against the reference's known answers, independent
 formulations and closed forms (no GPU needed), plus the C ABI export check.
 
-Known answers come from the reference's own tests (paths relative to the
-reference repository): tests/test_selection.py:18-50.
+The reference's own known answers (tests/test_selection.py:18-50, paths
+relative to the reference repository) are checked from the fixture
+tests/golden/reference_kats.json by test_golden.py.
 """
 
 import ctypes
@@ -28,26 +29,6 @@ def test_library_exports_every_header_symbol():
 
 
 # ---- resolver ----------------------------------------------------------------------
-
-KAT = dict(
-    source=[5, 2, 9, 4], resident=[-1, 7, -1, 3], hot=[6, 1], tags=[-1, -1, -1, -1, -1, 22, -1, -1],
-    lru=[0, 1, 2, 3, 4, 6, 7, 5], positions=[9, 2, 6, 9, 14, -1], length=16, page=4,
-)
-
-
-def test_resolver_known_answer_and_lru_post_state():
-    tags = np.array(KAT["tags"], np.int64)
-    lru = np.array(KAT["lru"], np.int64)
-    phys, mh, md, counts = oracle.resolve_rows(
-        KAT["positions"], KAT["source"], KAT["resident"], KAT["hot"], tags, lru, KAT["length"], KAT["page"]
-    )
-    assert phys.tolist() == [24, 5, 30, -1, 14, -1]
-    assert counts.tolist() == [2, 1, 1]
-    assert mh.tolist() == [37, -1, -1, -1, -1, -1]
-    assert md.tolist() == [24, -1, -1, -1, -1, -1]
-    assert tags[0] == 37 and tags[5] == 22
-    # slot 0 was inserted (category 1), slot 5 was a protected hit (category 2)
-    assert lru.tolist() == [1, 2, 3, 4, 6, 7, 0, 5]
 
 
 def _random_item(rng, n_pages, P, H):
@@ -85,16 +66,6 @@ def test_resolver_c_restatement_equals_bruteforce_simulation(seed):
 
 
 # ---- Quest ---------------------------------------------------------------------------
-
-
-def test_quest_known_answers():
-    low = torch.tensor([[[-10.0, 0.0]], [[1.0, 0.0]], [[0.0, 0.0]]])[None]
-    high = torch.tensor([[[10.0, 0.0]], [[1.0, 0.0]], [[0.0, 0.0]]])[None]
-    _, pages, pos = oracle.quest_select(torch.tensor([[[1.0, 0.0]]]), low, high, [5], 2, 2, keep_sink=False)
-    assert pages[0].tolist() == [0, 2] and pos[0].tolist() == [0, 1, 4, -1]
-    bounds = torch.tensor([[[9.0, 0.0]], [[0.0, 10.0]], [[-1.0, -1.0]]])[None]
-    _, pages, pos = oracle.quest_select(torch.eye(2)[None], bounds, bounds, [5], 2, 2, keep_sink=False)
-    assert pages[0].tolist() == [1, 2] and pos[0].tolist() == [2, 3, 4, -1]
 
 
 @pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.bfloat16, 128), (torch.float16, 24), (torch.float32, 3)])

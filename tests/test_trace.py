@@ -2,11 +2,14 @@
 
 The locality known-answer cases pin the resolver and gather end to end:
 hit/miss counts, Jaccard indices, page density, reuse gaps and the hot
-slots of the alternating pattern are the reference's own expected values.
+slots of the alternating pattern are the reference's own expected values
+(tests/golden/reference_kats.json).
 On CPU the kernels are the oracle; marked gpu they are libnhs_hip.so.
 """
 
 import copy
+import json
+import os
 
 import pytest
 import torch
@@ -23,20 +26,14 @@ from nano_hisparse.trace import (
     validate_trace,
 )
 
-GAPS = {"reuse": 1, "alternating": 2, "streaming": None, "packed": 1}
+with open(os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")) as _f:
+    LOCALITY = json.load(_f)["trace_locality"]
 
 
-@pytest.mark.parametrize(
-    "pattern,capacity,hits,misses,row_j,page_j,density",
-    [
-        ("reuse", 4, 28, 4, 1, 1, 0.25),
-        ("alternating", 4, 0, 32, 0, 1, 0.25),
-        ("alternating", 8, 24, 8, 0, 1, 0.25),
-        ("streaming", 8, 0, 32, 0, 6 / 7, 0.25),
-        ("packed", 4, 28, 4, 1, 1, 1),
-    ],
-)
-def test_row_locality_counts(device, pattern, capacity, hits, misses, row_j, page_j, density):
+@pytest.mark.parametrize("kat", LOCALITY, ids=[f"{k['pattern']}-{k['capacity']}" for k in LOCALITY])
+def test_row_locality_counts(device, kat):
+    pattern, capacity, hits, misses = kat["pattern"], kat["capacity"], kat["hits"], kat["misses"]
+    row_j, page_j, density = kat["row_jaccard"], kat["page_jaccard"], kat["density"]
     report = replay_trace(synthetic_trace(pattern), capacity, device)
     summary = report["summary"]
     assert summary["resident_hits"] == 0
@@ -45,7 +42,7 @@ def test_row_locality_counts(device, pattern, capacity, hits, misses, row_j, pag
     assert summary["mean_row_jaccard"] == pytest.approx(row_j)
     assert summary["mean_page_jaccard"] == pytest.approx(page_j)
     assert summary["mean_page_density"] == density
-    assert summary["mean_reuse_gap_steps"] == GAPS[pattern]
+    assert summary["mean_reuse_gap_steps"] == kat["reuse_gap"]
     for event in report["events"]:
         assert len(event["positions"]) == 4
         assert event["positions"] == tuple(event["union_rows"])
