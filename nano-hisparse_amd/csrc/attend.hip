@@ -567,6 +567,8 @@ static AttendKernel pick2(int G, int C) {
     case 2 * 4 + 2: return pick3<T, 2, 2, PK>();
     case 4 * 4 + 1: return pick3<T, 4, 1, PK>();
     case 4 * 4 + 2: return pick3<T, 4, 2, PK>();
+    case 7 * 4 + 1: return pick3<T, 7, 1, PK>();
+    case 7 * 4 + 2: return pick3<T, 7, 2, PK>();
     case 8 * 4 + 1: return pick3<T, 8, 1, PK>();
     case 8 * 4 + 2: return pick3<T, 8, 2, PK>();
   }
@@ -674,7 +676,9 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
     int chunks = 1;
     while (chunks * 2 <= share && chunks * 2 <= a.group && chunks * 2 <= kMaxHeadChunks) chunks *= 2;
     const int per_chunk = (a.group + chunks - 1) / chunks;
-    G = per_chunk <= 1 ? 1 : per_chunk <= 2 ? 2 : per_chunk <= 4 ? 4 : 8;
+    // 7 has its own instance (Qwen2 groups of 7 heads): rounded up to 8, one
+    // head of every group would be computed and masked
+    G = per_chunk <= 1 ? 1 : per_chunk <= 2 ? 2 : per_chunk <= 4 ? 4 : per_chunk == 7 ? 7 : 8;
     a.chunks_per_kv = (a.group + G - 1) / G;
   }
   AttendKernel kernel = pick_kernel(kv_dtype, packed, G, C);

@@ -78,6 +78,10 @@ def _attention_case(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, N, per_head, seed):
         (torch.bfloat16, torch.float32, 2, 16, 2, 128, 64, 257, False),  # fp32 query, bf16 KV, GQA 8
         (torch.bfloat16, torch.bfloat16, 1, 48, 4, 64, 16, 100, False),  # GQA 12 (two workgroups per KV head)
         (torch.float32, torch.float32, 1, 3, 3, 256, 8, 40, False),  # 1 KiB rows
+        # 256+ (request, KV head) items: one workgroup per item, all 7 heads of a group in it
+        (torch.bfloat16, torch.bfloat16, 64, 28, 4, 128, 32, 256, False),
+        (torch.bfloat16, torch.float32, 128, 14, 2, 64, 16, 100, False),  # fp32 query: unpacked scores
+        (torch.float32, torch.float32, 128, 14, 2, 64, 16, 60, False),
     ],
 )
 def test_attend_rows_matches_oracle(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, N, per_head):
