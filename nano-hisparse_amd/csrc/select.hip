@@ -11,11 +11,12 @@
 // scores and the chosen pages are bit-identical to it. FMA contraction is
 // disabled in this file so that products are rounded before they are added.
 //
-// Selection (one 1024-thread workgroup per request): keys are the scores
-// mapped to order-preserving uint32 (required pages get the maximum key); a
-// 4-pass 8-bit radix select finds the key of the k-th best page, ties at that
-// key go to the lowest page indices (block scan), and the chosen pages are
-// emitted in ascending order (block scan) and expanded to token positions.
+// Selection (one workgroup per request): keys are the scores mapped to
+// order-preserving uint32 (required pages get the maximum key). Up to 1024
+// pages, one wave finds the key of the k-th best page bit by bit with ballots;
+// beyond, a 4-pass 8-bit radix select does. Ties at that key go to the lowest
+// page indices, and the chosen pages are emitted in ascending order and
+// expanded to token positions.
 #include <math.h>
 
 #include "nhs_common.h"
@@ -30,6 +31,7 @@ constexpr int kPagesPerBlock = 8;
 constexpr int kQuestThreads = 512;
 constexpr int kSelectThreads = 1024;
 constexpr int kMaxSelectPerThread = NHS_MAX_SELECT_PAGES / kSelectThreads;  // 16
+constexpr int kSelectWaveThreads = 256;  // one-wave selection; 4 waves expand the positions
 
 enum { kModeQuest = 0, kModeMean = 1 };
 
@@ -544,6 +546,112 @@ __global__ __launch_bounds__(THREADS) void select_topk_kernel(SelectArgs a) {
   }
 }
 
+// Up to kWave * KPL pages: the selection runs in one wave, with no LDS and no
+// barrier until the output. Page q * kWave + lane sits in slot q of that lane.
+// The key of the k-th best page is found bit by bit, most significant first.
+// At each bit the wave counts the keys that match the prefix found so far
+// with that bit set (a ballot and a popcount per slot). If at least `need`
+// match, the bit is set; otherwise those keys are all taken and `need` drops
+// by their count. Ties at the final key go to the lowest pages and the chosen
+// pages come out in ascending order (ranks from mbcnt). The other waves
+// join for the page -> token expansion.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+template <int KPL>
+__global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectArgs a) {
+  __shared__ int32_t chosen[kWave * KPL];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
+  const int64_t len = a.lengths ? a.lengths[b] : a.length;
+  if (tid < kWave) {
+    const int lane = tid;
+    // the score loads are issued before the page count arrives (pages past
+    // max_pages read page 0; values past count are never used, and none are
+    // when every page is kept)
+    const float* sc = a.scores + (int64_t)b * a.max_pages;
+    float sv[KPL];
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) sv[q] = sc[q * kWave + lane < a.max_pages ? q * kWave + lane : 0];
+    bool sel[KPL];
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) sel[q] = q * kWave + lane < count;
+    if (a.top_pages < count) {
+      const bool second = a.mode == kModeQuest ? (a.keep_sink && a.top_pages > 1 && count > 1) : a.top_pages > 1;
+      // pages past count keep key 0, below every score's key (>= 0x007fffff),
+      // so no prefix tested below (it always has a bit set) matches them
+      uint32_t key[KPL];
+#pragma unroll
+      for (int q = 0; q < KPL; ++q) {
+        const int p = q * kWave + lane;
+        key[q] = p >= count ? 0u : (p == count - 1 || (second && p == 0)) ? 0xffffffffu : order_key(sv[q]);
+      }
+      // prefix = the largest key x with at least top_pages keys >= x, i.e.
+      // the key of the k-th best page
+      uint32_t prefix = 0u;
+#pragma unroll
+      for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = prefix | (1u << bit);
+        int c = 0;
+#pragma unroll
+        for (int q = 0; q < KPL; ++q) c += __popcll(__ballot(key[q] >= cand));
+        if (c >= a.top_pages) prefix = cand;
+      }
+      int above = 0;
+#pragma unroll
+      for (int q = 0; q < KPL; ++q) above += __popcll(__ballot(key[q] > prefix));
+      // every page above that key is taken, then the first `need` pages with
+      // that key in page order (slot, then lane)
+      const int need = a.top_pages - above;
+      int before = 0;
+#pragma unroll
+      for (int q = 0; q < KPL; ++q) {
+        const bool tie = key[q] == prefix;
+        const uint64_t m = __ballot(tie);
+        sel[q] = key[q] > prefix || (tie && before + lanes_below(m) < need);
+        before += __popcll(m);
+      }
+    }
+    int n_sel = 0;
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) {
+      const uint64_t m = __ballot(sel[q]);
+      if (sel[q]) chosen[n_sel + lanes_below(m)] = q * kWave + lane;
+      n_sel += __popcll(m);
+    }
+    for (int i = n_sel + lane; i < a.top_pages; i += kWave) chosen[i] = -1;
+  }
+  __syncthreads();
+  int32_t* pages = a.pages + (int64_t)b * a.top_pages;
+  for (int i = tid; i < a.top_pages; i += kSelectWaveThreads) pages[i] = chosen[i];
+  const int P = a.page_size;
+  const int64_t n_pos = (int64_t)a.top_pages * P;
+  int32_t* pos = a.positions + (int64_t)b * n_pos;
+  if (P % 4 == 0 && (uintptr_t)a.positions % 16 == 0) {
+    // four positions of one page per 16-byte store (n_pos is a multiple of 4)
+    for (int64_t i = 4 * (int64_t)tid; i < n_pos; i += 4 * kSelectWaveThreads) {
+      const uint32_t j = a.page_div.div((uint32_t)i);
+      const int32_t p = chosen[j];
+      const int64_t t = (int64_t)p * P + (int64_t)((uint32_t)i - j * (uint32_t)P);
+      int4 v;
+      v.x = (p >= 0 && t < len) ? (int32_t)t : -1;
+      v.y = (p >= 0 && t + 1 < len) ? (int32_t)(t + 1) : -1;
+      v.z = (p >= 0 && t + 2 < len) ? (int32_t)(t + 2) : -1;
+      v.w = (p >= 0 && t + 3 < len) ? (int32_t)(t + 3) : -1;
+      *reinterpret_cast<int4*>(pos + i) = v;
+    }
+  } else {
+    for (int64_t i = tid; i < n_pos; i += kSelectWaveThreads) {
+      const uint32_t j = a.page_div.div((uint32_t)i);
+      const int32_t p = chosen[j];
+      const int64_t t = (int64_t)p * P + (int64_t)((uint32_t)i - j * (uint32_t)P);
+      pos[i] = (p >= 0 && t < len) ? (int32_t)t : -1;
+    }
+  }
+}
+
 static int check_select_common(const char* who, int32_t batch, const void* query, int q_dtype, int32_t q_heads,
                                int32_t kv_heads, int32_t head_dim, const int64_t* lengths, int64_t length,
                                int32_t page_size, int32_t max_pages, int32_t top_pages, float* scores,
@@ -580,7 +688,12 @@ static int quest_chunk_elems(int head_dim, int esize) {
 
 static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, const char* who, hipEvent_t start,
                          hipEvent_t stop) {
-  if (s.max_pages <= 256 * kMaxSelectPerThread)
+  const int wave_pages = s.max_pages > s.top_pages ? s.max_pages : s.top_pages;
+  if (wave_pages <= kWave * 8)
+    launch(select_wave_kernel<8>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
+  else if (wave_pages <= kWave * 16)
+    launch(select_wave_kernel<16>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
+  else if (s.max_pages <= 256 * kMaxSelectPerThread)
     launch(select_topk_kernel<256>, dim3((unsigned)batch), dim3(256), 0, stream, start, stop, s);
   else
     launch(select_topk_kernel<kSelectThreads>, dim3((unsigned)batch), dim3(kSelectThreads), 0, stream, start, stop, s);

@@ -252,6 +252,8 @@ def _bounds(g, B, n_pages, Hkv, D, dtype, offsets=False):
         (torch.float16, torch.float32, 2, 6, 2, 24, 7, 30, 5, True),
         (torch.float32, torch.float32, 2, 2, 1, 2, 2, 3, 2, False),  # head_dim 2 (element lanes)
         (torch.bfloat16, torch.bfloat16, 2, 8, 2, 64, 16, 9000, 300, True),
+        (torch.bfloat16, torch.bfloat16, 3, 8, 2, 64, 16, 1000, 40, True),  # one-wave select, 16 keys per lane
+        (torch.float32, torch.float32, 2, 4, 2, 16, 5, 513, 64, False),
     ],
 )
 def test_quest_select_bit_exact(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, n_pages, top, keep_sink):
@@ -316,7 +318,8 @@ def test_quest_scores_with_special_values_bit_exact(gpu, dtype, B, Hq, Hkv, D, P
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,P,n_pages,top", [(4, 32, 8, 128, 64, 512, 32), (3, 4, 2, 8, 4, 20, 1),
-                                                      (2, 4, 2, 8, 4, 20, 2), (2, 6, 3, 24, 5, 33, 7)])
+                                                      (2, 4, 2, 8, 4, 20, 2), (2, 6, 3, 24, 5, 33, 7),
+                                                      (2, 4, 2, 16, 8, 700, 50)])
 def test_mean_select_bit_exact(gpu, B, Hq, Hkv, D, P, n_pages, top):
     log_case(test="mean", B=B, Hq=Hq, D=D, n_pages=n_pages, top=top)
     g = torch.Generator().manual_seed(5 + n_pages)
