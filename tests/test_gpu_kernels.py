@@ -254,6 +254,7 @@ def _bounds(g, B, n_pages, Hkv, D, dtype, offsets=False):
         (torch.bfloat16, torch.bfloat16, 2, 8, 2, 64, 16, 9000, 300, True),
         (torch.bfloat16, torch.bfloat16, 3, 8, 2, 64, 16, 1000, 40, True),  # one-wave select, 16 keys per lane
         (torch.float32, torch.float32, 2, 4, 2, 16, 5, 513, 64, False),
+        (torch.float32, torch.float32, 2, 4, 2, 64, 16, 40, 100, True),  # budget above the page count: -1 padding
     ],
 )
 def test_quest_select_bit_exact(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, n_pages, top, keep_sink):
