@@ -15,11 +15,15 @@
 //     that host row and marks its slot protected.
 //  5. victims = lru stably partitioned (unprotected first): the lru values
 //     are staged in LDS and ranked in 1024-slot chunks with wave ballots.
+//     The same pass writes the new lru: it is the lru stably partitioned by
+//     category (untouched, inserted, hit, inserted hit). Misses take the
+//     first n_miss victims, so with U / Pr the unprotected / protected slots
+//     in lru order, m = min(n_miss, |U|) and e = n_miss - m, the new lru is
+//     U[m:] ++ U[:m] ++ Pr[e:] ++ Pr[:e], a rotation of each part. n_miss is
+//     summed with the protected count before the pass.
 //  6. miss ranks by a block scan; assigned slot = victims[rank].
 //  7. physical rows (scattered back to input order), compact miss plan, tag
-//     writes for misses, counts.
-//  8. lru stably partitioned by category (untouched, inserted, hit), ranked
-//     the same way.
+//     writes for misses.
 #include "nhs_common.h"
 
 namespace nhs {
@@ -70,12 +74,11 @@ struct ResolveShared {
       int32_t hkey[kHashCap];  // phase 3-4: wanted host rows
       int32_t hslot[kHashCap]; // hot slot holding that host row, or -1
     } hash;
-    uint16_t lru16[kMaxH];     // phase 5-8: the item's lru, staged
+    uint16_t lru16[kMaxH];     // phase 5: the item's lru, staged
   } u;
   uint32_t prot[kMaxH / 32];  // protected slot bits
-  uint32_t ins[kMaxH / 32];   // inserted slot bits
   int32_t victims[kMaxK];     // victims[0 .. min(n, H)-1]
-  int32_t red[3][kWaves * 8];                    // one scratch row per block reduction
+  int32_t red[2][kWaves * 8];                    // one scratch row per block reduction
   int32_t wcount[2][kRankGroup][kWaves][4];      // per-wave category counts, double-buffered
   int32_t hot[kHotCache];                      // the item's hot block table, when it fits
 };
@@ -321,10 +324,7 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     sh.u.hash.hkey[i] = -1;
     sh.u.hash.hslot[i] = -1;
   }
-  for (int i = tid; i < kMaxH / 32; i += kResolveThreads) {
-    sh.prot[i] = 0u;
-    sh.ins[i] = 0u;
-  }
+  for (int i = tid; i < kMaxH / 32; i += kResolveThreads) sh.prot[i] = 0u;
   __syncthreads();
 #pragma unroll
   for (int q = 0; q < kKPerThread; ++q) {
@@ -357,11 +357,12 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
 
   bool hhit[kKPerThread], miss[kKPerThread];
   int32_t slot[kKPerThread];
-  int local_miss = 0;
+  int local_miss = 0, local_rhit = 0, local_hhit = 0;
 #pragma unroll
   for (int q = 0; q < kKPerThread; ++q) {
     hhit[q] = miss[q] = false;
     slot[q] = 0;
+    local_rhit += rhit[q];
     if (nhot[q]) {
       int h = hash_find(sh.u.hash.hkey, (int32_t)host[q]);
       int32_t es = sh.u.hash.hslot[h];
@@ -369,6 +370,7 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
       miss[q] = !hhit[q];
       slot[q] = es;
       local_miss += miss[q];
+      local_hhit += hhit[q];
     }
   }
 
@@ -384,13 +386,30 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     const int64_t v = lru_in[r];
     sh.u.lru16[r] = (uint16_t)(v < 0 ? 0 : v >= H ? H - 1 : v);
   }
-  int n_prot_v[1] = {0};
-  for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) n_prot_v[0] += __popc(sh.prot[i]);
-  block_sums<1>(n_prot_v, sh.red[0]);  // barrier: lru16 staged
-  const int n_unprot = H - n_prot_v[0];
+  // protected slots, misses, resident hits, hot hits
+  int tot4[4] = {0, local_miss, local_rhit, local_hhit};
+  for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) tot4[0] += __popc(sh.prot[i]);
+  block_sums<4>(tot4, sh.red[0]);  // barrier: lru16 staged
+  const int n_prot = tot4[0];
+  const int n_unprot = H - n_prot;
   const int vlimit = n < H ? n : H;
+  if (tid == 0) {
+    int64_t* c = a.counts + (int64_t)b * 3;
+    c[0] = tot4[2];
+    c[1] = tot4[3];
+    c[2] = tot4[1];
+    if (a.counts_total) {
+      atomicAdd((unsigned long long*)&a.counts_total[0], (unsigned long long)tot4[2]);
+      atomicAdd((unsigned long long*)&a.counts_total[1], (unsigned long long)tot4[3]);
+      atomicAdd((unsigned long long*)&a.counts_total[2], (unsigned long long)tot4[1]);
+    }
+  }
+  // the new lru: U[m:] ++ U[:m] ++ Pr[e:] ++ Pr[:e] (more misses than hot
+  // rows reuse the last victim, so at most H slots are inserted)
+  const int inserted = tot4[1] < H ? tot4[1] : H;
+  const int m_u = inserted < n_unprot ? inserted : n_unprot;
+  const int e_p = inserted - m_u;
   auto prot_bit = [&](int v) { return (int)((sh.prot[v >> 5] >> (v & 31)) & 1u); };
-  auto ins_bit = [&](int v) { return (int)((sh.ins[v >> 5] >> (v & 31)) & 1u); };
   const int n_chunks = (H + kResolveThreads - 1) / kResolveThreads;
   {
     int base_u = 0, base_p = 0, parity = 0;
@@ -407,8 +426,18 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
 #pragma unroll
       for (int c = 0; c < kRankGroup; ++c) {
         if (c < chunks && cat[c] >= 0) {
-          const int rank = cat[c] == 0 ? base_u + within[c] : n_unprot + base_p + within[c];
+          int rank, pos;
+          if (cat[c] == 0) {
+            const int u = base_u + within[c];
+            rank = u;
+            pos = u >= m_u ? u - m_u : n_unprot - m_u + u;
+          } else {
+            const int p = base_p + within[c];
+            rank = n_unprot + p;
+            pos = n_unprot + (p >= e_p ? p - e_p : n_prot - e_p + p);
+          }
           if (rank < vlimit) sh.victims[rank] = vv[c];
+          lru_out[pos] = vv[c];
         }
         base_u += tot[c][0];
         base_p += tot[c][1];
@@ -425,7 +454,6 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   int64_t* phys_out = a.physical + (int64_t)b * a.plan_stride;
   int64_t* mh = a.miss_host + (int64_t)b * a.plan_stride;
   int64_t* md = a.miss_device + (int64_t)b * a.plan_stride;
-  int local_rhit = 0, local_hhit = 0;
   {
     int64_t rank = miss_before;
 #pragma unroll
@@ -435,12 +463,10 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
       int64_t phys = -1;
       if (rhit[q]) {
         phys = (int64_t)res_blk[q] * P + off[q];
-        ++local_rhit;
       } else if (nhot[q]) {
         int32_t s;
         if (hhit[q]) {
           s = slot[q];
-          ++local_hhit;
         } else {
           int64_t vr = rank < H - 1 ? rank : H - 1;
           s = sh.victims[vr];
@@ -452,7 +478,6 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
           mh[rank] = host[q];
           md[rank] = hp;
           tags[s] = (int32_t)host[q];
-          atomicOr(&sh.ins[s >> 5], 1u << (s & 31));
           ++rank;
         }
       }
@@ -464,63 +489,6 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
       mh[i] = -1;
       md[i] = -1;
     }
-  __syncthreads();  // ins bits complete
-
-  // ---- 8. lru stably partitioned by category ----------------------------------
-  // category = inserted + 2 * protected: 0 untouched, 1 inserted, 2 hit.
-  // one reduction: slots inserted only, protected only, both; resident and hot hits
-  int sums[5] = {0, 0, 0, local_rhit, local_hhit};
-  for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) {
-    uint32_t in = sh.ins[i], pr = sh.prot[i];
-    uint32_t valid_bits = (i == (H - 1) / 32 && (H & 31)) ? ((1u << (H & 31)) - 1u) : 0xffffffffu;
-    sums[0] += __popc(in & ~pr & valid_bits);
-    sums[1] += __popc(pr & ~in & valid_bits);
-    sums[2] += __popc(in & pr & valid_bits);
-  }
-  block_sums<5>(sums, sh.red[2]);
-  if (tid == 0) {
-    int64_t* c = a.counts + (int64_t)b * 3;
-    c[0] = sums[3];
-    c[1] = sums[4];
-    c[2] = n_miss;
-    if (a.counts_total) {
-      atomicAdd((unsigned long long*)&a.counts_total[0], (unsigned long long)sums[3]);
-      atomicAdd((unsigned long long*)&a.counts_total[1], (unsigned long long)sums[4]);
-      atomicAdd((unsigned long long*)&a.counts_total[2], (unsigned long long)n_miss);
-    }
-  }
-  // start[c] = number of slots in lower categories
-  int start[4];
-  {
-    const int n1 = sums[0], n2 = sums[1], n0 = H - sums[0] - sums[1] - sums[2];
-    start[0] = 0;
-    start[1] = n0;
-    start[2] = n0 + n1;
-    start[3] = n0 + n1 + n2;
-  }
-  {
-    int parity = 0;
-    for (int g0 = 0; g0 < n_chunks; g0 += kRankGroup, parity ^= 1) {
-      const int chunks = min(kRankGroup, n_chunks - g0);
-      int cat[kRankGroup], vv[kRankGroup], within[kRankGroup], tot[kRankGroup][4];
-#pragma unroll
-      for (int c = 0; c < kRankGroup; ++c) {
-        const int r = (g0 + c) * kResolveThreads + tid;
-        vv[c] = r < H ? sh.u.lru16[r] : 0;
-        cat[c] = r < H ? ins_bit(vv[c]) + 2 * prot_bit(vv[c]) : -1;
-      }
-      rank_group(cat, chunks, sh.wcount[parity], within, tot);
-#pragma unroll
-      for (int c = 0; c < kRankGroup; ++c) {
-        if (c < chunks && cat[c] >= 0) {
-          const int pos = start[cat[c]] + within[c];
-          if (pos < H) lru_out[pos] = vv[c];
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) start[k] += tot[c][k];
-      }
-    }
-  }
 }
 
 }  // namespace nhs
