@@ -437,7 +437,9 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
             pos = n_unprot + (p >= e_p ? p - e_p : n_prot - e_p + p);
           }
           if (rank < vlimit) sh.victims[rank] = vv[c];
-          lru_out[pos] = vv[c];
+          // pos < H for a permutation; the check keeps a corrupt lru (clamped
+          // duplicates, so the protected count and the ranks disagree) in bounds
+          if (pos < H) lru_out[pos] = vv[c];
         }
         base_u += tot[c][0];
         base_p += tot[c][1];

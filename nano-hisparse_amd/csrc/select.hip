@@ -548,13 +548,13 @@ __global__ __launch_bounds__(THREADS) void select_topk_kernel(SelectArgs a) {
 
 // Up to kWave * KPL pages: the selection runs in one wave, with no LDS and no
 // barrier until the output. Page q * kWave + lane sits in slot q of that lane.
-// The key of the k-th best page is found bit by bit, most significant first.
-// At each bit the wave counts the keys that match the prefix found so far
-// with that bit set (a ballot and a popcount per slot). If at least `need`
-// match, the bit is set; otherwise those keys are all taken and `need` drops
-// by their count. Ties at the final key go to the lowest pages and the chosen
-// pages come out in ascending order (ranks from mbcnt). The other waves
-// join for the page -> token expansion.
+// The key of the k-th best page, the largest x with at least top_pages keys
+// >= x, is found bit by bit, most significant first: at each bit the wave
+// counts the keys >= the prefix found so far with that bit set (a compare, a
+// ballot and a popcount per slot) and keeps the bit when the count reaches
+// top_pages. Every key above it is taken, ties at it go to the lowest pages,
+// and the chosen pages come out in ascending order (ranks from mbcnt). The
+// other waves join for the page -> token expansion.
 __device__ __forceinline__ int lanes_below(uint64_t mask) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
