@@ -341,20 +341,35 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   }
   const int lpr = 1 << a.lpr_log2;
   const int page_lane0 = page_local * lanes_per_page;
+  // every slot is scored first (slots past count hold a live page's bounds
+  // and are not stored), then the KV-head sums of all slots are formed
+  // together: each group of 8 heads issues its lane reads for every slot
+  // before the adds, which stay sequential in head order
+  float t[kPageSlots], total[kPageSlots];
+#pragma unroll
+  for (int s = 0; s < kPageSlots; ++s) {
+    t[s] = group_sum(gq.template chunk_packed<T>(mn[s], mx[s]), lpr);
+    total[s] = 0.f;
+  }
+  for (int h0 = 0; h0 < a.kv_heads; h0 += 8) {
+    float v[kPageSlots][8];
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      const int src = page_lane0 + ((h0 + h < a.kv_heads ? h0 + h : h0) << a.lpr_log2);
+#pragma unroll
+      for (int s = 0; s < kPageSlots; ++s) v[s][h] = __shfl(t[s], src);
+    }
+#pragma unroll
+    for (int h = 0; h < 8; ++h)
+      if (h0 + h < a.kv_heads)
+#pragma unroll
+        for (int s = 0; s < kPageSlots; ++s) total[s] = h0 + h == 0 ? v[s][h] : total[s] + v[s][h];
+  }
 #pragma unroll
   for (int s = 0; s < kPageSlots; ++s) {
     const int p0 = wave_first + s * ppw;
-    if (p0 >= count) break;
-    const float t = group_sum(gq.template chunk_packed<T>(mn[s], mx[s]), lpr);
-    // sequential sum over the page's KV heads (every lane takes part in the
-    // lane reads; the page's first lane stores)
-    float total = 0.f;
-    for (int h = 0; h < a.kv_heads; ++h) {
-      const float v = __shfl(t, page_lane0 + (h << a.lpr_log2));
-      total = h == 0 ? v : total + v;
-    }
     if (within == 0 && page_local < ppw && p0 + page_local < count)
-      a.scores[(int64_t)b * a.max_pages + p0 + page_local] = total / (float)a.q_heads;
+      a.scores[(int64_t)b * a.max_pages + p0 + page_local] = total[s] / (float)a.q_heads;
   }
 }
 
