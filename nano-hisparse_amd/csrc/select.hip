@@ -262,13 +262,18 @@ __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a)
 // Page kernel, for pages that fit one wave (kv_heads * lanes per head <=
 // 64, 32-byte chunks): lane = (page of the wave, kv head, chunk). A wave
 // loads its query slices straight into registers, issues the bounds of all
-// its kPageSlots page slots, forms the grouped sums, then scores the slots
-// one by one: per-lane chunk sum, DPP tree over a KV head's lanes, and the
-// sequential KV-head sum read across lanes, with no barrier. It is
-// instantiated for each group size G (1..8), so no head is masked.
+// its page_slots(G) page slots, forms the grouped sums, then scores every
+// slot (per-lane chunk sum, DPP tree over a KV head's lanes) and forms the
+// slots' sequential KV-head sums together from lane reads, with no barrier.
+// It is instantiated for each group size G (1..8), so no head is masked.
 constexpr int kPageThreads = 256;
 constexpr int kPageWaves = kPageThreads / kWave;
-constexpr int kPageSlots = 4;
+// Page slots per wave: 2 up to 4 query heads per KV head, else 4. With the
+// smaller group the second slot pair is better spent on more waves (Quest +
+// select 17.0-17.6 against 18.0 us at Llama-3-8B heads); with 7 heads the
+// query registers dominate, waves per SIMD stay at 3 and 2 slots lost (58
+// against 49 us at Qwen2-7B heads).
+__host__ __device__ constexpr int page_slots(int group) { return group <= 4 ? 2 : 4; }
 
 template <typename T, int E, int G>
 __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
@@ -278,7 +283,8 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   const int b = blockIdx.y;
   const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
   const int ppw = a.pages_per_step;  // pages per wave slot
-  const int wave_first = (blockIdx.x * kPageWaves + wave) * kPageSlots * ppw;
+  constexpr int S = page_slots(G);
+  const int wave_first = (blockIdx.x * kPageWaves + wave) * S * ppw;
   if (wave_first >= count) return;
   const int lanes_per_page = a.kv_heads << a.lpr_log2;
   const int page_local = lane / lanes_per_page;
@@ -300,10 +306,10 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   bounds_of<T>(a, b, lo, hi);
   const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
   const int64_t lane_off = data ? (int64_t)kh * a.head_dim + sub * E : 0;
-  uint32_t mn[kPageSlots][W], mx[kPageSlots][W];
+  uint32_t mn[S][W], mx[S][W];
   auto load_bounds = [&]() {
 #pragma unroll
-    for (int s = 0; s < kPageSlots; ++s) {
+    for (int s = 0; s < S; ++s) {
       const int p = wave_first + s * ppw + page_local;
       const int pc = p < count ? p : wave_first;  // lanes past the end reread a live page
       const uint4* lp = reinterpret_cast<const uint4*>(lo + ((int64_t)pc * page_elems + lane_off) * T::bytes);
@@ -345,28 +351,28 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   // and are not stored), then the KV-head sums of all slots are formed
   // together: each group of 8 heads issues its lane reads for every slot
   // before the adds, which stay sequential in head order
-  float t[kPageSlots], total[kPageSlots];
+  float t[S], total[S];
 #pragma unroll
-  for (int s = 0; s < kPageSlots; ++s) {
+  for (int s = 0; s < S; ++s) {
     t[s] = group_sum(gq.template chunk_packed<T>(mn[s], mx[s]), lpr);
     total[s] = 0.f;
   }
   for (int h0 = 0; h0 < a.kv_heads; h0 += 8) {
-    float v[kPageSlots][8];
+    float v[S][8];
 #pragma unroll
     for (int h = 0; h < 8; ++h) {
       const int src = page_lane0 + ((h0 + h < a.kv_heads ? h0 + h : h0) << a.lpr_log2);
 #pragma unroll
-      for (int s = 0; s < kPageSlots; ++s) v[s][h] = __shfl(t[s], src);
+      for (int s = 0; s < S; ++s) v[s][h] = __shfl(t[s], src);
     }
 #pragma unroll
     for (int h = 0; h < 8; ++h)
       if (h0 + h < a.kv_heads)
 #pragma unroll
-        for (int s = 0; s < kPageSlots; ++s) total[s] = h0 + h == 0 ? v[s][h] : total[s] + v[s][h];
+        for (int s = 0; s < S; ++s) total[s] = h0 + h == 0 ? v[s][h] : total[s] + v[s][h];
   }
 #pragma unroll
-  for (int s = 0; s < kPageSlots; ++s) {
+  for (int s = 0; s < S; ++s) {
     const int p0 = wave_first + s * ppw;
     if (within == 0 && page_local < ppw && p0 + page_local < count)
       a.scores[(int64_t)b * a.max_pages + p0 + page_local] = total[s] / (float)a.q_heads;
@@ -779,7 +785,7 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
   if (E * esize == 32 && ppw > 0) {
     // a page fits one wave: the page kernel
     a.pages_per_step = ppw;
-    a.pages_per_block = kPageWaves * kPageSlots * ppw;
+    a.pages_per_block = kPageWaves * page_slots(a.group) * ppw;
     grid = dim3((unsigned)((max_pages + a.pages_per_block - 1) / a.pages_per_block), (unsigned)batch);
     block = dim3(kPageThreads);
     switch (bounds_dtype * 16 + a.group) {  // instantiated for every group size: no masked heads
