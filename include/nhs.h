@@ -40,9 +40,9 @@ enum {
 enum { NHS_F32 = 0, NHS_F16 = 1, NHS_BF16 = 2 };
 
 /* Library limits (checked; exceeding one returns NHS_ERR_UNSUPPORTED). */
-#define NHS_MAX_POSITIONS 4096   /* resolver: selected positions per item */
+#define NHS_MAX_POSITIONS 32768  /* resolver: selected positions per item (hybrid.py:36 caps U at 32768) */
 #define NHS_MAX_HOT_ROWS 32768   /* resolver: hot rows per item (hybrid.py:36) */
-#define NHS_MAX_SELECT_PAGES 16384 /* selectors: pages scored per request */
+#define NHS_MAX_SELECT_PAGES 16384 /* selectors: pages per request held in registers (more: a looping kernel) */
 
 /*
  * Device tables of one (request, layer), for the batched decode entry points
@@ -155,8 +155,11 @@ int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_batch_stride,
  * logical order, then -1) and counts[b, 0:3] = unique resident hits, hot
  * hits, misses; counts_total[0:3] (may be NULL) is incremented by them.
  * lengths[b] (int64, may be NULL to use `length` for every item) is the
- * causal length. Bit-exact with resolve_rows,
- * nano_hisparse/row_index.py:62-140.
+ * causal length. n <= NHS_MAX_POSITIONS, hot_rows <= NHS_MAX_HOT_ROWS;
+ * with batch > 1, plan_stride >= n. Above 4096 positions the item's
+ * physical / miss_host / miss_device rows also serve as scratch during the
+ * call (sorted keys, per-entry state) before they receive the results.
+ * Bit-exact with resolve_rows, nano_hisparse/row_index.py:62-140.
  */
 int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t positions_i64,
                      int64_t positions_stride, const int32_t* source, const int32_t* resident,
@@ -171,19 +174,27 @@ int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t po
  * Quest page selection for `batch` requests. Request b scores each of its
  * count = ceil(lengths[b]/page_size) pages (count is clamped to max_pages):
  *   score[p] = (sum_h sum_d max(q[h,d]*min[p,h/g,d], q[h,d]*max[p,h/g,d])) / q_heads
- * in fp32 with a fixed summation order: per KV head j and dimension d the
- * GQA group's terms are min*Qneg + max*Qpos (Qpos / Qneg: the sums, in head
+ * in fp32 with a fixed summation order: per KV head j and dimension d, with
+ * a / b the smaller / larger of the two bounds (swapped when max < min),
+ * the GQA group's terms are a*Qneg + b*Qpos (Qpos / Qneg: the sums, in head
  * order from 0.0, of the group's positive / non-positive q[h,d]); a bound
  * row is cut into chunks of 32 bytes when it is a multiple of 32 bytes of at
- * most 64 chunks, else of 16 bytes when a multiple of 16 bytes, else of one
- * element; each chunk is summed from 0.0 in element order with
- * t = fma(nneg ? min : 0, Qneg, t), t = fma(npos ? max : 0, Qpos, t) (npos,
- * nneg: whether any head contributed to Qpos, Qneg); chunk sums (padded with
- * +0.0 to a power of two) are added as a pairwise tree; KV-head sums are
- * added sequentially j = 0..kv_heads-1. q_heads/kv_heads <= 8.
- * Page count-1, and page 0 when keep_sink and
- * top_pages > 1 and count > 1, score +inf. The top_pages pages by (score
- * descending, page ascending) are written ascending to pages[b, :top_pages]
+ * most 64 chunks, else of 16 bytes when a multiple of 16 bytes of at most
+ * 64 chunks, else of one element up to 64 elements, else of
+ * ceil(head_dim/64) elements (the last chunk shorter); each chunk is summed
+ * from 0.0 in element order with t = fma(nneg ? a : 0, Qneg, t),
+ * t = fma(npos ? b : 0, Qpos, t) (npos, nneg: whether any head contributed
+ * to Qpos, Qneg); chunk sums (padded with +0.0 to a power of two) are added
+ * as a pairwise tree; KV-head sums are added sequentially j = 0..kv_heads-1.
+ * As torch.maximum does, a chunk sums to NaN when it holds a NaN bound, or
+ * a bound of +-inf (+-0) at a d where a head's query is +-0 (+-inf); NaN
+ * scores are stored as 0x7fc00000. Any group size and head_dim;
+ * kv_heads * head_dim <= 16384 when a page needs the general kernel.
+ * Page count-1, and page 0 when keep_sink and top_pages > 1 and
+ * count > 1, are forced (+inf in the reference). Ranking, as torch.topk's:
+ * NaN pages first, then forced pages, then scores descending; ties at the
+ * k-th rank go to the lowest pages. The top_pages chosen pages are written
+ * ascending to pages[b, :top_pages]
  * (-1 padded when count < top_pages) and expanded to causal token positions
  * positions[b, :top_pages*page_size] (ascending, -1 padded). scores[b, :]
  * (max_pages floats) is scratch that keeps the scores.
@@ -202,8 +213,9 @@ int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtype, int64_t 
  * averaged over each GQA group, dotted with the fp32 per-page mean keys
  * summaries[p, kv_heads, head_dim], pages {0, count-1} ({count-1} when
  * top_pages == 1) are always kept and the best top_pages - |kept| other
- * pages (score descending, page ascending) are added. Output layout as in
- * nhs_quest_select. Replaces select_pages, nano_hisparse/selection.py:119-145.
+ * pages (score descending, page ascending; NaN ranks first, below the kept
+ * pages) are added. Output layout as in nhs_quest_select. Replaces
+ * select_pages, nano_hisparse/selection.py:119-145.
  */
 int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
                     int64_t q_head_stride, const float* summaries, int64_t summaries_batch_stride,

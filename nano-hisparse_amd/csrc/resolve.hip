@@ -29,7 +29,7 @@
 namespace nhs {
 
 constexpr int kResolveThreads = 1024;
-constexpr int kMaxK = NHS_MAX_POSITIONS;          // sorted entries per item
+constexpr int kMaxK = 4096;                       // sorted entries per item held in LDS (resolve_rows_kernel)
 constexpr int kMaxH = NHS_MAX_HOT_ROWS;           // hot rows per item
 constexpr int kKPerThread = kMaxK / kResolveThreads;  // 4
 constexpr int kHashCap = 2 * kMaxK;                // load factor <= 1/2
@@ -173,6 +173,74 @@ __device__ __forceinline__ void rank_group(const int (&cat)[kRankGroup], int chu
 #pragma unroll
       for (int k = 0; k < 4; ++k) tot[c][k] = __shfl(incl, 60 + k);
     }
+  }
+}
+
+// Victims and the new lru (phase 5): the lru (staged in lru16) stably
+// partitioned into unprotected slots U and protected slots Pr, each in lru
+// order; victims[rank] = the rank-th slot of U ++ Pr for rank < vlimit. The
+// new lru is U[m:] ++ U[:m] ++ Pr[e:] ++ Pr[:e] with m = min(inserted, |U|)
+// and e = inserted - m, inserted = min(n_miss, H) (more misses than hot rows
+// reuse the last victim, so at most H slots are inserted). Ranks come from
+// rank_group over kRankGroup 1024-slot chunks per barrier. Ends without a
+// barrier: callers synchronise before reading victims.
+template <typename V>
+__device__ __forceinline__ void partition_lru(const uint16_t* lru16, const uint32_t* prot, int H, int n_prot,
+                                              int n_miss, int vlimit, V* victims, int64_t* lru_out,
+                                              int32_t (*wcount)[kRankGroup][kWaves][4]) {
+  const int tid = threadIdx.x;
+  const int n_unprot = H - n_prot;
+  const int inserted = n_miss < H ? n_miss : H;
+  const int m_u = inserted < n_unprot ? inserted : n_unprot;
+  const int e_p = inserted - m_u;
+  auto prot_bit = [&](int v) { return (int)((prot[v >> 5] >> (v & 31)) & 1u); };
+  const int n_chunks = (H + kResolveThreads - 1) / kResolveThreads;
+  int base_u = 0, base_p = 0, parity = 0;
+  for (int g0 = 0; g0 < n_chunks; g0 += kRankGroup, parity ^= 1) {
+    const int chunks = min(kRankGroup, n_chunks - g0);
+    int cat[kRankGroup], vv[kRankGroup], within[kRankGroup], tot[kRankGroup][4];
+#pragma unroll
+    for (int c = 0; c < kRankGroup; ++c) {
+      const int r = (g0 + c) * kResolveThreads + tid;
+      vv[c] = r < H ? lru16[r] : 0;
+      cat[c] = r < H ? prot_bit(vv[c]) : -1;  // 0 unprotected, 1 protected
+    }
+    rank_group(cat, chunks, wcount[parity], within, tot);
+#pragma unroll
+    for (int c = 0; c < kRankGroup; ++c) {
+      if (c < chunks && cat[c] >= 0) {
+        int rank, pos;
+        if (cat[c] == 0) {
+          const int u = base_u + within[c];
+          rank = u;
+          pos = u >= m_u ? u - m_u : n_unprot - m_u + u;
+        } else {
+          const int pr = base_p + within[c];
+          rank = n_unprot + pr;
+          pos = n_unprot + (pr >= e_p ? pr - e_p : n_prot - e_p + pr);
+        }
+        if (rank < vlimit) victims[rank] = (V)vv[c];
+        // pos < H for a permutation; the check keeps a corrupt lru (clamped
+        // duplicates, so the protected count and the ranks disagree) in bounds
+        if (pos < H) lru_out[pos] = vv[c];
+      }
+      base_u += tot[c][0];
+      base_p += tot[c][1];
+    }
+  }
+}
+
+// Writes an item's [resident hits, hot hits, misses] and adds them to the
+// running totals.
+__device__ __forceinline__ void write_counts(const ResolveArgs& a, int b, int rhit, int hhit, int miss) {
+  int64_t* c = a.counts + (int64_t)b * 3;
+  c[0] = rhit;
+  c[1] = hhit;
+  c[2] = miss;
+  if (a.counts_total) {
+    atomicAdd((unsigned long long*)&a.counts_total[0], (unsigned long long)rhit);
+    atomicAdd((unsigned long long*)&a.counts_total[1], (unsigned long long)hhit);
+    atomicAdd((unsigned long long*)&a.counts_total[2], (unsigned long long)miss);
   }
 }
 
@@ -391,61 +459,9 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) tot4[0] += __popc(sh.prot[i]);
   block_sums<4>(tot4, sh.red[0]);  // barrier: lru16 staged
   const int n_prot = tot4[0];
-  const int n_unprot = H - n_prot;
   const int vlimit = n < H ? n : H;
-  if (tid == 0) {
-    int64_t* c = a.counts + (int64_t)b * 3;
-    c[0] = tot4[2];
-    c[1] = tot4[3];
-    c[2] = tot4[1];
-    if (a.counts_total) {
-      atomicAdd((unsigned long long*)&a.counts_total[0], (unsigned long long)tot4[2]);
-      atomicAdd((unsigned long long*)&a.counts_total[1], (unsigned long long)tot4[3]);
-      atomicAdd((unsigned long long*)&a.counts_total[2], (unsigned long long)tot4[1]);
-    }
-  }
-  // the new lru: U[m:] ++ U[:m] ++ Pr[e:] ++ Pr[:e] (more misses than hot
-  // rows reuse the last victim, so at most H slots are inserted)
-  const int inserted = tot4[1] < H ? tot4[1] : H;
-  const int m_u = inserted < n_unprot ? inserted : n_unprot;
-  const int e_p = inserted - m_u;
-  auto prot_bit = [&](int v) { return (int)((sh.prot[v >> 5] >> (v & 31)) & 1u); };
-  const int n_chunks = (H + kResolveThreads - 1) / kResolveThreads;
-  {
-    int base_u = 0, base_p = 0, parity = 0;
-    for (int g0 = 0; g0 < n_chunks; g0 += kRankGroup, parity ^= 1) {
-      const int chunks = min(kRankGroup, n_chunks - g0);
-      int cat[kRankGroup], vv[kRankGroup], within[kRankGroup], tot[kRankGroup][4];
-#pragma unroll
-      for (int c = 0; c < kRankGroup; ++c) {
-        const int r = (g0 + c) * kResolveThreads + tid;
-        vv[c] = r < H ? sh.u.lru16[r] : 0;
-        cat[c] = r < H ? prot_bit(vv[c]) : -1;  // 0 unprotected, 1 protected
-      }
-      rank_group(cat, chunks, sh.wcount[parity], within, tot);
-#pragma unroll
-      for (int c = 0; c < kRankGroup; ++c) {
-        if (c < chunks && cat[c] >= 0) {
-          int rank, pos;
-          if (cat[c] == 0) {
-            const int u = base_u + within[c];
-            rank = u;
-            pos = u >= m_u ? u - m_u : n_unprot - m_u + u;
-          } else {
-            const int p = base_p + within[c];
-            rank = n_unprot + p;
-            pos = n_unprot + (p >= e_p ? p - e_p : n_prot - e_p + p);
-          }
-          if (rank < vlimit) sh.victims[rank] = vv[c];
-          // pos < H for a permutation; the check keeps a corrupt lru (clamped
-          // duplicates, so the protected count and the ranks disagree) in bounds
-          if (pos < H) lru_out[pos] = vv[c];
-        }
-        base_u += tot[c][0];
-        base_p += tot[c][1];
-      }
-    }
-  }
+  if (tid == 0) write_counts(a, b, tot4[2], tot4[3], tot4[1]);
+  partition_lru(sh.u.lru16, sh.prot, H, n_prot, tot4[1], vlimit, sh.victims, lru_out, sh.wcount);
   __syncthreads();  // victims complete
 
   // ---- 6. miss ranks ----------------------------------------------------------
@@ -493,21 +509,277 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     }
 }
 
+// ---- more than 4096 positions: resolve_large_kernel -------------------------
+//
+// One 1024-thread workgroup per item, for n up to NHS_MAX_POSITIONS. The
+// sorted entries fit neither registers nor LDS, so the item's own plan
+// outputs (3 x n int64, written last) hold the intermediate state:
+//  - unsorted input: keys (norm << 32 | input index) radix-sorted by norm
+//    (stable, 4 bits per pass over the bits of `length`) between physical
+//    and miss_host, ending in miss_host; sorted input (selector output)
+//    derives key j from positions[j] and materialises nothing;
+//  - one int32 of state per sorted entry in the upper half of miss_device.
+// Phases 2-4 run in rounds of kMaxK sorted entries (an LDS hash of the
+// round's wanted host rows, then one pass over the tags); phase 5 is the
+// small kernel's; phases 6-7 walk the sorted entries in chunks of 1024 with
+// one block scan each. A chunk's plan writes land at miss ranks <= the
+// sorted index being written, i.e. on keys and states already read.
+constexpr int kLargeMaxK = NHS_MAX_POSITIONS;
+constexpr int kRadixBits = 4;
+constexpr int kRadixBins = 1 << kRadixBits;
+
+struct LargeShared {
+  union {
+    uint16_t cnt[kRadixBins * kResolveThreads];  // radix counts, then offsets: [digit][thread]
+    struct {
+      int32_t hkey[kHashCap];   // a round's wanted host rows
+      int32_t hslot[kHashCap];  // hot slot holding that host row, or -1
+    } hash;
+    uint16_t lru16[kMaxH];      // phase 5: the item's lru, staged
+  } u;
+  uint16_t victims[kMaxH];
+  uint32_t prot[kMaxH / 32];
+  int32_t red[4][kWaves * 8];
+  int32_t wcount[2][kRankGroup][kWaves][4];
+  int32_t hot[kHotCache];
+};
+
+// state of a sorted entry: the hot slot of a hit in bits 0-15, then flags
+enum : uint32_t { kStRun = 1u << 16, kStRes = 1u << 17, kStHot = 1u << 18, kStHit = 1u << 19 };
+
+__global__ __launch_bounds__(kResolveThreads) void resolve_large_kernel(ResolveArgs a) {
+  __shared__ LargeShared sh;
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int n = a.n;
+  const int H = a.hot_rows;
+  const int P = a.page_size;
+  const int64_t length = a.lengths ? a.lengths[b] : a.length;
+
+  const nhs_layer_item* item = a.items ? a.items + b : nullptr;
+  const int32_t* source = item ? item->source : a.source + (int64_t)b * a.page_stride;
+  const int32_t* resident = item ? item->resident : a.resident + (int64_t)b * a.page_stride;
+  const int n_pages = item ? (int)item->n_pages : a.n_pages;
+  int32_t* const tags = item ? item->tags : a.tags + (int64_t)b * a.tags_stride;
+  int64_t* const lru_out = item ? item->lru : a.lru + (int64_t)b * a.lru_stride;
+  const int32_t* hot = item ? item->hot : a.hot + (int64_t)b * a.hot_stride;
+  const int hot_blocks = (H + P - 1) / P;
+  const bool hot_cached = hot_blocks <= kHotCache;
+  if (hot_cached)
+    for (int i = tid; i < hot_blocks; i += kResolveThreads) sh.hot[i] = hot[i];
+
+  int64_t* const phys_out = a.physical + (int64_t)b * a.plan_stride;
+  int64_t* const mh = a.miss_host + (int64_t)b * a.plan_stride;
+  int64_t* const md = a.miss_device + (int64_t)b * a.plan_stride;
+  uint64_t* const keys = reinterpret_cast<uint64_t*>(mh);         // sorted keys (unsorted input)
+  uint64_t* const keys2 = reinterpret_cast<uint64_t*>(phys_out);  // the radix sort's other buffer
+  uint32_t* const state = reinterpret_cast<uint32_t*>(md) + n;    // [n]: upper half of miss_device
+
+  auto norm_at = [&](int j) -> int64_t {
+    const int64_t raw = a.positions_i64
+                            ? static_cast<const int64_t*>(a.positions)[(int64_t)b * a.positions_stride + j]
+                            : (int64_t) static_cast<const int32_t*>(a.positions)[(int64_t)b * a.positions_stride + j];
+    return (raw >= 0 && raw < length) ? raw : length;
+  };
+
+  // ---- 1. sorted keys --------------------------------------------------------
+  int inverted = 0;
+  for (int i = tid; i + 1 < n; i += kResolveThreads) inverted |= norm_at(i) > norm_at(i + 1);
+  const bool sorted = !__syncthreads_or(inverted);
+  if (!sorted) {
+    // norm <= length < 2^31; an inversion needs length >= 1, so passes >= 1
+    int bits = 0;
+    while (bits < 31 && (length >> bits) != 0) ++bits;
+    const int passes = (bits + kRadixBits - 1) / kRadixBits;
+    const int per = (n + kResolveThreads - 1) / kResolveThreads;
+    const int j0 = tid * per, j1 = min(n, j0 + per);  // a thread's run, in order: the sort is stable
+    for (int pass = 0; pass < passes; ++pass) {
+      const int shift = 32 + pass * kRadixBits;
+      const bool to_keys = ((passes - 1 - pass) & 1) == 0;  // the last pass writes `keys`
+      uint64_t* dst = to_keys ? keys : keys2;
+      const uint64_t* prev = to_keys ? keys2 : keys;
+      auto src_key = [&](int j) -> uint64_t {
+        return pass == 0 ? (((uint64_t)norm_at(j) << 32) | (uint32_t)j) : prev[j];
+      };
+#pragma unroll
+      for (int d = 0; d < kRadixBins; ++d) sh.u.cnt[d * kResolveThreads + tid] = 0;
+      for (int j = j0; j < j1; ++j) ++sh.u.cnt[((src_key(j) >> shift) & (kRadixBins - 1)) * kResolveThreads + tid];
+      __syncthreads();
+      // exclusive scan of the counts in (digit, thread) order: thread t owns
+      // entries [16t, 16t + 16) of the flattened table
+      uint16_t* c = sh.u.cnt + tid * kRadixBins;
+      int v[kRadixBins], s = 0;
+#pragma unroll
+      for (int i = 0; i < kRadixBins; ++i) {
+        v[i] = c[i];
+        s += v[i];
+      }
+      int total;
+      int run = block_scan(s, sh.red[pass & 1], &total);
+#pragma unroll
+      for (int i = 0; i < kRadixBins; ++i) {
+        c[i] = (uint16_t)run;
+        run += v[i];
+      }
+      __syncthreads();
+      for (int j = j0; j < j1; ++j) {
+        const uint64_t k = src_key(j);
+        dst[sh.u.cnt[((k >> shift) & (kRadixBins - 1)) * kResolveThreads + tid]++] = k;
+      }
+      __syncthreads();
+    }
+  }
+  auto key_at = [&](int j) -> uint64_t { return sorted ? (((uint64_t)norm_at(j) << 32) | (uint32_t)j) : keys[j]; };
+
+  // ---- 2-4. per sorted entry, hash join with the tags in rounds -------------
+  for (int i = tid; i < kMaxH / 32; i += kResolveThreads) sh.prot[i] = 0u;
+  int local_rhit = 0, local_hhit = 0, local_miss = 0;
+  constexpr int kPer = kMaxK / kResolveThreads;
+  for (int r0 = 0; r0 < n; r0 += kMaxK) {
+    for (int i = tid; i < kHashCap; i += kResolveThreads) {
+      sh.u.hash.hkey[i] = -1;
+      sh.u.hash.hslot[i] = -1;
+    }
+    __syncthreads();
+    uint32_t st[kPer];
+    int32_t hrow[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int j = r0 + q * kResolveThreads + tid;
+      st[q] = 0u;
+      hrow[q] = -1;
+      if (j < n) {
+        const uint64_t key = key_at(j);
+        const int64_t lg = (int64_t)(key >> 32);
+        const bool run = j == 0 || (int64_t)(key_at(j - 1) >> 32) != lg;
+        const uint32_t pg = a.page_div.div((uint32_t)lg);
+        const int32_t off = (int32_t)((uint32_t)lg - pg * (uint32_t)P);
+        const int64_t page = pg < (uint32_t)(n_pages - 1) ? (int64_t)pg : (int64_t)(n_pages - 1);
+        const int64_t src = source[page], res = resident[page];
+        const bool valid = lg < length && run && src >= 0;
+        const bool rhit = valid && res >= 0;
+        const bool nhot = valid && !rhit;
+        st[q] = (run ? kStRun : 0u) | (rhit ? kStRes : 0u) | (nhot ? kStHot : 0u);
+        local_rhit += rhit;
+        if (nhot) {
+          hrow[q] = (int32_t)(src * P + off);
+          uint32_t h = hash_row(hrow[q]) & (kHashCap - 1);
+          while (true) {
+            const int32_t prev = atomicCAS(&sh.u.hash.hkey[h], -1, hrow[q]);
+            if (prev == -1 || prev == hrow[q]) break;
+            h = (h + 1) & (kHashCap - 1);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    for (int s = tid; s < H; s += kResolveThreads) {
+      const int32_t t = tags[s];
+      if (t >= 0) {
+        const int h = hash_find(sh.u.hash.hkey, t);
+        if (h >= 0) {
+          sh.u.hash.hslot[h] = s;
+          atomicOr(&sh.prot[s >> 5], 1u << (s & 31));
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+      const int j = r0 + q * kResolveThreads + tid;
+      if (j >= n) continue;
+      if (st[q] & kStHot) {
+        const int32_t es = sh.u.hash.hslot[hash_find(sh.u.hash.hkey, hrow[q])];
+        if (es >= 0) {
+          st[q] |= kStHit | (uint32_t)es;
+          ++local_hhit;
+        } else {
+          ++local_miss;
+        }
+      }
+      state[j] = st[q];
+    }
+    __syncthreads();  // the hash is cleared for the next round
+  }
+
+  // ---- 5. victims and the new lru ---------------------------------------------
+  for (int r = tid; r < H; r += kResolveThreads) {
+    const int64_t v = lru_out[r];
+    sh.u.lru16[r] = (uint16_t)(v < 0 ? 0 : v >= H ? H - 1 : v);
+  }
+  int tot4[4] = {0, local_miss, local_rhit, local_hhit};
+  for (int i = tid; i < (H + 31) / 32; i += kResolveThreads) tot4[0] += __popc(sh.prot[i]);
+  block_sums<4>(tot4, sh.red[2]);  // barrier: lru16 staged
+  const int vlimit = n < H ? n : H;
+  if (tid == 0) write_counts(a, b, tot4[2], tot4[3], tot4[1]);
+  partition_lru(sh.u.lru16, sh.prot, H, tot4[0], tot4[1], vlimit, sh.victims, lru_out, sh.wcount);
+  __syncthreads();  // victims complete
+
+  // ---- 6-7. miss ranks, physical rows, plan, tag writes ----------------------
+  int rank_base = 0;
+  for (int c0 = 0, parity = 0; c0 < n; c0 += kResolveThreads, parity ^= 1) {
+    const int j = c0 + tid;
+    uint64_t key = 0;
+    uint32_t st = 0u;
+    if (j < n) {
+      key = key_at(j);
+      st = state[j];
+    }
+    const bool miss = (st & kStHot) && !(st & kStHit);
+    int n_here;
+    const int rank = rank_base + block_scan(miss ? 1 : 0, sh.red[parity], &n_here);  // barrier: reads done
+    if (j < n) {
+      int64_t phys = -1;
+      if (st & (kStRes | kStHot)) {
+        const int64_t lg = (int64_t)(key >> 32);
+        const uint32_t pg = a.page_div.div((uint32_t)lg);
+        const int32_t off = (int32_t)((uint32_t)lg - pg * (uint32_t)P);
+        const int64_t page = pg < (uint32_t)(n_pages - 1) ? (int64_t)pg : (int64_t)(n_pages - 1);
+        if (st & kStRes) {
+          phys = (int64_t)resident[page] * P + off;
+        } else {
+          const int32_t s = (st & kStHit) ? (int32_t)(st & 0xffffu) : (int32_t)sh.victims[rank < H - 1 ? rank : H - 1];
+          const uint32_t sb = a.page_div.div((uint32_t)s);
+          const int64_t hp =
+              (int64_t)(hot_cached ? sh.hot[sb] : hot[sb]) * P + (int64_t)((uint32_t)s - sb * (uint32_t)P);
+          phys = hp;
+          if (miss) {
+            const int64_t host = (int64_t)source[page] * P + off;
+            mh[rank] = host;
+            md[rank] = hp;
+            tags[s] = (int32_t)host;
+          }
+        }
+      }
+      phys_out[(uint32_t)key] = (st & kStRun) ? phys : -1;
+    }
+    rank_base += n_here;
+  }
+  __syncthreads();
+  for (int i = rank_base + tid; i < n; i += kResolveThreads) {
+    mh[i] = -1;
+    md[i] = -1;
+  }
+}
+
 }  // namespace nhs
 
 namespace nhs {
 
 static int check_resolve(const char* who, int32_t batch, int32_t n, const void* positions, int32_t hot_rows,
                          const int64_t* lengths, int64_t length, int32_t page_size, const int64_t* physical,
-                         const int64_t* miss_host, const int64_t* miss_device, const int64_t* counts) {
+                         const int64_t* miss_host, const int64_t* miss_device, int64_t plan_stride,
+                         const int64_t* counts) {
   if (!positions || !physical || !miss_host || !miss_device || !counts)
     return fail(NHS_ERR_INVALID, "%s: null pointer", who);
   if (batch < 0 || n < 1 || hot_rows < 1 || page_size < 1)
     return fail(NHS_ERR_INVALID, "%s: need n, n_pages, hot_rows, page_size >= 1", who);
-  if (n > kMaxK || hot_rows > kMaxH)
-    return fail(NHS_ERR_UNSUPPORTED, "%s: n <= %d and hot_rows <= %d required", who, kMaxK, kMaxH);
+  if (n > kLargeMaxK || hot_rows > kMaxH)
+    return fail(NHS_ERR_UNSUPPORTED, "%s: n <= %d and hot_rows <= %d required", who, kLargeMaxK, kMaxH);
   if (!lengths && (length < 0 || length >= (1ll << 31)))
     return fail(NHS_ERR_INVALID, "%s: length must be in [0, 2^31)", who);
+  if (batch > 1 && plan_stride < n)
+    return fail(NHS_ERR_INVALID, "%s: plan_stride must be >= n (items' plans may not overlap)", who);
   return NHS_OK;
 }
 
@@ -546,7 +818,7 @@ extern "C" int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions,
   const LaunchEvents ev = take_launch_events();
   const char* who = "nhs_resolve_rows";
   int st = check_resolve(who, batch, n, positions, hot_rows, lengths, length, page_size, physical, miss_host,
-                         miss_device, counts);
+                         miss_device, plan_stride, counts);
   if (st != NHS_OK) return st;
   if (!source || !resident || !hot || !tags || !lru) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
   if (n_pages < 1) return fail(NHS_ERR_INVALID, "%s: need n, n_pages, hot_rows, page_size >= 1", who);
@@ -564,8 +836,8 @@ extern "C" int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions,
   a.tags_stride = tags_stride;
   a.lru = lru;
   a.lru_stride = lru_stride;
-  launch(resolve_rows_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0, (hipStream_t)stream, ev.start, ev.stop,
-         a);
+  launch(n <= kMaxK ? resolve_rows_kernel : resolve_large_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0,
+         (hipStream_t)stream, ev.start, ev.stop, a);
   return launch_status(who);
 }
 
@@ -578,7 +850,7 @@ extern "C" int nhs_resolve_items(int32_t batch, int32_t n, const void* positions
   const LaunchEvents ev = take_launch_events();
   const char* who = "nhs_resolve_items";
   int st = check_resolve(who, batch, n, positions, hot_rows, lengths, 0, page_size, physical, miss_host,
-                         miss_device, counts);
+                         miss_device, plan_stride, counts);
   if (st != NHS_OK) return st;
   if (!items || !lengths) return fail(NHS_ERR_INVALID, "%s: null items or lengths", who);
   if (batch == 0) return NHS_OK;
@@ -586,7 +858,7 @@ extern "C" int nhs_resolve_items(int32_t batch, int32_t n, const void* positions
   fill_common(a, n, positions, positions_i64, positions_stride, hot_rows, lengths, 0, page_size, physical, miss_host,
               miss_device, plan_stride, counts, counts_total);
   a.items = items;
-  launch(resolve_rows_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0, (hipStream_t)stream, ev.start, ev.stop,
-         a);
+  launch(n <= kMaxK ? resolve_rows_kernel : resolve_large_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0,
+         (hipStream_t)stream, ev.start, ev.stop, a);
   return launch_status(who);
 }

@@ -32,6 +32,10 @@ constexpr int kQuestThreads = 512;
 constexpr int kSelectThreads = 1024;
 constexpr int kMaxSelectPerThread = NHS_MAX_SELECT_PAGES / kSelectThreads;  // 16
 constexpr int kSelectWaveThreads = 256;  // one-wave selection; 4 waves expand the positions
+// The general Quest kernel's folded query (2 floats and a byte per (KV
+// head, d)) and KV-head sums fit the 160 KiB of LDS a workgroup may use.
+constexpr size_t kMaxQuestLds = 160 * 1024;
+constexpr int kMaxQuestFold = 16384;  // kv_heads * head_dim, for the message
 
 enum { kModeQuest = 0, kModeMean = 1 };
 
@@ -45,6 +49,8 @@ struct ScoreArgs {
   int64_t b_bs;     // elements between requests' bound tensors
   int q_heads, kv_heads, head_dim, group;
   int lanes_used, lpr_log2;
+  int elems;           // elements per lane chunk (the last chunk of a row may be shorter)
+  int heads_per_pass;  // general Quest kernel: KV heads scored together
   int pages_per_step, pages_per_block;
   const int64_t* lengths;
   int64_t length;
@@ -65,12 +71,6 @@ __device__ __forceinline__ void bounds_of(const ScoreArgs& a, int b, const char*
   }
 }
 
-__device__ __forceinline__ float torch_maximum(float a, float b) {
-  // torch.maximum propagates NaN from either operand.
-  if (a != a || b != b) return a + b;
-  return a > b ? a : b;
-}
-
 __device__ __forceinline__ int page_count(const int64_t* lengths, int64_t length, int b, int page_size, int max_pages) {
   int64_t len = lengths ? lengths[b] : length;
   if (len <= 0) return 0;
@@ -78,19 +78,55 @@ __device__ __forceinline__ int page_count(const int64_t* lengths, int64_t length
   return (int)(c < max_pages ? c : max_pages);
 }
 
-// Quest bounds score: (sum_h sum_d max(q*min, q*max)) / q_heads.
+// Quest bounds score: (sum_h sum_d torch.maximum(q*lo, q*hi)) / q_heads.
 //
-// The heads of one KV head's GQA group contribute q*kmax where q > 0 and
-// q*kmin elsewhere (kmax >= kmin), so per (KV head, d) the group's terms are
-//   kmin[d] * Qneg[d] + kmax[d] * Qpos[d]
+// With a = the smaller and b = the larger bound of an element (a = hi and
+// b = lo when hi < lo), the heads of one KV head's GQA group contribute q*b
+// where q > 0 and q*a elsewhere, so per (KV head, d) the group's terms are
+//   a[d] * Qneg[d] + b[d] * Qpos[d]
 // with Qpos / Qneg the group's positive / non-positive query sums (added in
 // head order from 0.0, once per request). A lane keeps them for its chunk
-// and scores a page with two fmas per element, t = fma(kmin', Qneg, t) then
-// t = fma(kmax', Qpos, t), where kmin' (kmax') is 0 when no head of the
-// group is non-positive (positive) at d, so a bound nobody selects is never
-// multiplied. Chunk sums are added as a pairwise tree over a KV head's
-// lanes, the KV-head sums sequentially; the CPU oracle sums in this order.
+// and scores a page with two fmas per element, t = fma(a', Qneg, t) then
+// t = fma(b', Qpos, t), where a' (b') is 0 when no head of the group is
+// non-positive (positive) at d. Chunk sums are added as a pairwise tree
+// over a KV head's lanes, the KV-head sums sequentially; the CPU oracle sums
+// in this order.
 //
+// Special values follow torch.maximum, which is NaN when either product is:
+// a chunk sums to NaN when it holds a NaN bound, a bound of +-inf at a d
+// where a head's query is +-0, or a bound of +-0 at a d where a head's query
+// is +-inf (0 * inf). NaN scores are stored as the quiet NaN 0x7fc00000.
+//
+// Side bits of a (KV head, d): a head of the group is > 0, is not > 0, is
+// +-0, is +-inf.
+enum : uint32_t { kSidePos = 1u, kSideNeg = 2u, kSideZero = 4u, kSideInf = 8u };
+
+__device__ __forceinline__ void fold_query(float q, float& p, float& n, uint32_t& side) {
+  // branch-free: a query value adds +0.0 to the other side's sum, which
+  // leaves it unchanged (the positive sum starts at +0.0 and only grows, the
+  // non-positive one starts at +0.0 and never becomes -0.0)
+  const bool up = q > 0.f;
+  p = p + (up ? q : 0.f);
+  n = n + (up ? 0.f : q);
+  side |= (up ? kSidePos : kSideNeg) | (q == 0.f ? kSideZero : 0u) | (__builtin_isinf(q) ? kSideInf : 0u);
+}
+
+__device__ __forceinline__ float quest_fma2(float x, float lo, float hi, float pos, float neg, bool use_pos,
+                                            bool use_neg) {
+  const bool sw = hi < lo;
+  const float a = sw ? hi : lo, b = sw ? lo : hi;
+  x = __builtin_fmaf(use_neg ? a : 0.f, neg, x);
+  return __builtin_fmaf(use_pos ? b : 0.f, pos, x);
+}
+
+// 0 * inf inside one of the products of an element whose group holds a zero
+// or an infinite query
+__device__ __forceinline__ bool zero_inf_product(float lo, float hi, bool zero_q, bool inf_q) {
+  return (zero_q && (__builtin_isinf(lo) || __builtin_isinf(hi))) || (inf_q && (lo == 0.f || hi == 0.f));
+}
+
+__device__ __forceinline__ float canonical_score(float s) { return s != s ? __uint_as_float(0x7fc00000u) : s; }
+
 // element e of E packed elements of T (raw 32-bit words), widened exactly to fp32
 template <typename T, int E>
 __device__ __forceinline__ float packed_elem(const uint32_t (&w)[E * T::bytes / 4], int e) {
@@ -105,157 +141,203 @@ __device__ __forceinline__ float packed_elem(const uint32_t (&w)[E * T::bytes / 
   }
 }
 
-// The per-lane grouped sums (and the masks of which side has contributors).
-// Branch-free: a query value adds +0.0 to the other side's sum, which leaves
-// it unchanged (the positive sum starts at +0.0 and only grows, the
-// non-positive one starts at +0.0 and never becomes -0.0); the side flags
-// are bit e of two per-lane masks.
+// Nonzero when a packed word of T holds a NaN. For 16-bit types both halves
+// at once: |x| + (0x8000 - the smallest NaN magnitude) reaches bit 15 exactly
+// for a NaN, and no half carries into the other.
+template <typename T>
+__device__ __forceinline__ uint32_t nan_bits(uint32_t w) {
+  if constexpr (T::bytes == 4) {
+    return (w & 0x7fffffffu) > 0x7f800000u ? 1u : 0u;
+  } else {
+    constexpr uint32_t add = T::dtype == NHS_BF16 ? 0x007f007fu : 0x03ff03ffu;
+    return ((w & 0x7fff7fffu) + add) & 0x80008000u;
+  }
+}
+
+// The rare test of one lane's chunk (n elements) of one page whose group has
+// a zero or infinite query: each element's query heads and bounds are
+// re-read from memory and tested for 0 * inf (zero_inf_product). q_off is
+// the element index of the group's first head at the chunk's first element.
+template <typename T>
+__device__ __forceinline__ bool zero_inf_chunk(const ScoreArgs& a, int64_t q_off, int group, const char* lo,
+                                                        const char* hi, int64_t b_off, int n) {
+#pragma unroll 1
+  for (int e = 0; e < n; ++e) {
+    bool zero_q = false, inf_q = false;
+#pragma unroll 1
+    for (int g = 0; g < group; ++g) {
+      const float q = load_elem(a.q, a.q_dtype, q_off + (int64_t)g * a.q_hs + e);
+      zero_q |= q == 0.f;
+      inf_q |= __builtin_isinf(q);
+    }
+    if ((zero_q || inf_q) &&
+        zero_inf_product(load_elem(lo, T::dtype, b_off + e), load_elem(hi, T::dtype, b_off + e), zero_q, inf_q))
+      return true;
+  }
+  return false;
+}
+
+// The per-lane grouped sums and the side bits of its E elements.
 template <int E, int G>
 struct GroupedQuery {
   static_assert(E <= 32, "side masks hold one bit per element");
   float pos[E], neg[E];
-  uint32_t has_pos = 0, has_neg = 0;  // bit e: a head of the group is > 0 (<= 0) at element e
-  // qv: the lane's slices of the group's query heads; live: this lane holds
-  // data (padding lanes add exactly +0)
+  uint32_t has_pos = 0, has_neg = 0;  // bit e: a head of the group is > 0 (not > 0) at element e
+  // a head's query is +-0 or +-inf somewhere in the chunk (one bit: per-element
+  // masks cost ~28 VGPRs; the rare lanes with it re-test from memory)
+  uint32_t special = 0;
+  __device__ __forceinline__ void set(int e, float p, float n, uint32_t side) {
+    pos[e] = p, neg[e] = n;
+    has_pos |= ((side & kSidePos) ? 1u : 0u) << e;
+    has_neg |= ((side & kSideNeg) ? 1u : 0u) << e;
+    special |= (side & (kSideZero | kSideInf)) ? 1u : 0u;
+  }
+  __device__ __forceinline__ void clear_if_idle(bool live) {
+    // padding lanes add exactly +0
+    if (!live) has_pos = has_neg = special = 0u;
+  }
+  // qv: the lane's slices of the group's query heads (heads >= group are ignored)
   __device__ __forceinline__ void init(const float (&qv)[G][E], int group, bool live) {
 #pragma clang fp contract(off)
-    uint32_t hp_bits = 0, hn_bits = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       float p = 0.f, n = 0.f;
-      uint32_t hp = 0, hn = 0;
+      uint32_t side = 0u;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float q = qv[g][e];
-        const bool in_group = g < group;
-        const bool up = q > 0.f;
-        p = p + (in_group && up ? q : 0.f);
-        n = n + (in_group && !up ? q : 0.f);
-        hp |= (uint32_t)(in_group && up);
-        hn |= (uint32_t)(in_group && !up);
-      }
-      pos[e] = p, neg[e] = n;
-      hp_bits |= hp << e;
-      hn_bits |= hn << e;
+      for (int g = 0; g < G; ++g)
+        if (g < group) fold_query(qv[g][e], p, n, side);
+      set(e, p, n, side);
     }
-    has_pos = live ? hp_bits : 0u;
-    has_neg = live ? hn_bits : 0u;
+    clear_if_idle(live);
   }
   // init() from the heads' slices kept packed in T (widened element by element)
   // (all G heads are in the group)
   template <typename T>
   __device__ __forceinline__ void init_packed(const uint32_t (&qw)[G][E * T::bytes / 4], bool live) {
 #pragma clang fp contract(off)
-    uint32_t hp_bits = 0, hn_bits = 0;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       float p = 0.f, n = 0.f;
-      uint32_t hp = 0, hn = 0;
+      uint32_t side = 0u;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float q = packed_elem<T, E>(qw[g], e);
-        const bool up = q > 0.f;
-        p = p + (up ? q : 0.f);
-        n = n + (up ? 0.f : q);
-        hp |= (uint32_t)up;
-        hn |= (uint32_t)!up;
-      }
-      pos[e] = p, neg[e] = n;
-      hp_bits |= hp << e;
-      hn_bits |= hn << e;
+      for (int g = 0; g < G; ++g) fold_query(packed_elem<T, E>(qw[g], e), p, n, side);
+      set(e, p, n, side);
     }
-    has_pos = live ? hp_bits : 0u;
-    has_neg = live ? hn_bits : 0u;
+    clear_if_idle(live);
   }
-  // chunk() of bounds kept packed in T
+  // this lane's chunk sum for one page's bounds kept packed in T
   template <typename T>
   __device__ __forceinline__ float chunk_packed(const uint32_t (&mn)[E * T::bytes / 4],
                                                 const uint32_t (&mx)[E * T::bytes / 4]) const {
     float x = 0.f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      x = __builtin_fmaf((has_neg >> e) & 1u ? packed_elem<T, E>(mn, e) : 0.f, neg[e], x);
-      x = __builtin_fmaf((has_pos >> e) & 1u ? packed_elem<T, E>(mx, e) : 0.f, pos[e], x);
-    }
+    for (int e = 0; e < E; ++e)
+      x = quest_fma2(x, packed_elem<T, E>(mn, e), packed_elem<T, E>(mx, e), pos[e], neg[e], (has_pos >> e) & 1u,
+                     (has_neg >> e) & 1u);
     return x;
   }
-  // this lane's chunk sum for one page's bounds
-  __device__ __forceinline__ float chunk(const float (&mn)[E], const float (&mx)[E]) const {
-    float x = 0.f;
+  // Nonzero when the chunk of one page's bounds makes the reference's
+  // torch.maximum NaN: a NaN bound, or 0 * inf against a zero or infinite
+  // query. Integer tests on the packed bits.
+  template <typename T>
+  __device__ __forceinline__ uint32_t nan_bound(const uint32_t (&mn)[E * T::bytes / 4],
+                                                const uint32_t (&mx)[E * T::bytes / 4]) const {
+    constexpr int W = E * T::bytes / 4;
+    uint32_t bad = 0u;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      x = __builtin_fmaf((has_neg >> e) & 1u ? mn[e] : 0.f, neg[e], x);
-      x = __builtin_fmaf((has_pos >> e) & 1u ? mx[e] : 0.f, pos[e], x);
-    }
-    return x;
+    for (int w = 0; w < W; ++w) bad |= nan_bits<T>(mn[w]) | nan_bits<T>(mx[w]);
+    return bad;
   }
 };
 //
-// General kernel, for pages wider than one wave: lanes are laid out as (page
-// of the step, kv head, chunk), so a lane keeps one kv head's query slices
-// in registers for the whole kernel; the next step's bounds are requested
-// before the current step is summed.
-template <typename T, int E, int G>
+// General kernel, for any group size, head_dim and KV head count: the
+// workgroup folds the query once into LDS (Qpos, Qneg and the side bits of
+// every (KV head, d), the heads of a group added in order), then lanes laid
+// out as (page of the step, KV head, chunk) score pages. A chunk is E
+// elements (E = 0: a.elems elements read one by one, the last chunk of a
+// row shorter). When a page needs more lanes than the workgroup has, its KV
+// heads are taken in passes. Each lane's chunk sum, the DPP tree over a KV
+// head's lanes and the sequential KV-head sum follow the page kernel's order.
+template <typename T, int E>
 __global__ __launch_bounds__(kQuestThreads) void quest_score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ float smem[];
-  const int pages_per_step = a.pages_per_step;
-  float* qs = smem;                              // [q_heads * head_dim]
-  float* hs = smem + a.q_heads * a.head_dim;     // [pages_per_step][kv_heads]
+  const int kvd = a.kv_heads * a.head_dim;
+  float* fpos = smem;                                           // [kv_heads * head_dim]
+  float* fneg = smem + kvd;                                     // [kv_heads * head_dim]
+  float* hs = smem + 2 * kvd;                                   // [pages_per_step][kv_heads]
+  uint8_t* fside = reinterpret_cast<uint8_t*>(hs + a.pages_per_step * a.kv_heads);  // [kv_heads * head_dim]
   const int b = blockIdx.y;
   const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
   const int p_begin = blockIdx.x * a.pages_per_block;
   if (p_begin >= count) return;
   const int p_end = min(count, p_begin + a.pages_per_block);
-  for (int i = threadIdx.x; i < a.q_heads * a.head_dim; i += blockDim.x) {
-    const int h = i / a.head_dim, d = i - h * a.head_dim;
-    qs[i] = load_elem(a.q, a.q_dtype, (int64_t)b * a.q_bs + (int64_t)h * a.q_hs + d);
+  for (int i = threadIdx.x; i < kvd; i += blockDim.x) {
+    const int kh = i / a.head_dim, d = i - kh * a.head_dim;
+    float p = 0.f, n = 0.f;
+    uint32_t side = 0u;
+    for (int g = 0; g < a.group; ++g)
+      fold_query(load_elem(a.q, a.q_dtype, (int64_t)b * a.q_bs + (int64_t)(kh * a.group + g) * a.q_hs + d), p, n,
+                 side);
+    fpos[i] = p, fneg[i] = n, fside[i] = (uint8_t)side;
   }
   __syncthreads();
+  const int ne = E > 0 ? E : a.elems;
   const int lpr = 1 << a.lpr_log2;
-  const int lanes_per_page = a.kv_heads << a.lpr_log2;
+  const int heads_per_pass = a.heads_per_pass;
+  const int lanes_per_page = heads_per_pass << a.lpr_log2;
   const int page_local = threadIdx.x / lanes_per_page;
   const int within = threadIdx.x - page_local * lanes_per_page;
-  const int kh = within >> a.lpr_log2;
+  const int kh_local = within >> a.lpr_log2;
   const int sub = within & (lpr - 1);
-  const bool active = page_local < pages_per_step;
-  const bool data = active && sub < a.lanes_used;
-  float qv[G][E];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < E; ++e) qv[g][e] = data && g < a.group ? qs[(kh * a.group + g) * a.head_dim + sub * E + e] : 0.f;
-  GroupedQuery<E, G> gq;
-  gq.init(qv, a.group, data);
+  const bool active = page_local < a.pages_per_step;
   const char *lo, *hi;
   bounds_of<T>(a, b, lo, hi);
-  const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
-  const int64_t lane_off = data ? (int64_t)kh * a.head_dim + sub * E : 0;
-  auto load = [&](int p, float (&mn)[E], float (&mx)[E]) {
-    const int pc = (active && p < p_end) ? p : p_begin;  // idle lanes reread a live page
-    load_vec<T, E>(lo, (int64_t)pc * page_elems + lane_off, mn);
-    load_vec<T, E>(hi, (int64_t)pc * page_elems + lane_off, mx);
-  };
-  float mn[E], mx[E], mn2[E], mx2[E];
-  load(p_begin + page_local, mn, mx);
-  for (int base = p_begin; base < p_end; base += pages_per_step) {
+  const int64_t page_elems = (int64_t)kvd;
+  for (int base = p_begin; base < p_end; base += a.pages_per_step) {
     const int p = base + page_local;
-    load(p + pages_per_step, mn2, mx2);
-    const float t = group_sum(gq.chunk(mn, mx), lpr);
-    if (active && sub == 0 && p < p_end) hs[page_local * a.kv_heads + kh] = t;
+    for (int kh0 = 0; kh0 < a.kv_heads; kh0 += heads_per_pass) {
+      const int kh = kh0 + kh_local;
+      const bool data = active && p < p_end && kh < a.kv_heads && sub < a.lanes_used;
+      float x = 0.f;
+      if (data) {
+        const int d0 = sub * ne;
+        const int d1 = min(d0 + ne, a.head_dim);
+        const int64_t off = (int64_t)p * page_elems + (int64_t)kh * a.head_dim;
+        bool bad = false;
+        if constexpr (E > 0) {
+          float mn[E], mx[E];
+          load_vec<T, E>(lo, off + d0, mn);
+          load_vec<T, E>(hi, off + d0, mx);
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const int i = kh * a.head_dim + d0 + e;
+            const uint32_t side = fside[i];
+            x = quest_fma2(x, mn[e], mx[e], fpos[i], fneg[i], side & kSidePos, side & kSideNeg);
+            bad |= mn[e] != mn[e] || mx[e] != mx[e] || zero_inf_product(mn[e], mx[e], side & kSideZero, side & kSideInf);
+          }
+        } else {
+          for (int d = d0; d < d1; ++d) {
+            const int i = kh * a.head_dim + d;
+            const uint32_t side = fside[i];
+            const float l = load_elem(lo, T::dtype, off + d), h = load_elem(hi, T::dtype, off + d);
+            x = quest_fma2(x, l, h, fpos[i], fneg[i], side & kSidePos, side & kSideNeg);
+            bad |= l != l || h != h || zero_inf_product(l, h, side & kSideZero, side & kSideInf);
+          }
+        }
+        if (bad) x = __uint_as_float(0x7fc00000u);
+      }
+      const float t = group_sum(x, lpr);
+      if (data && sub == 0) hs[page_local * a.kv_heads + kh] = t;
+    }
     __syncthreads();
-    if ((int)threadIdx.x < pages_per_step && base + (int)threadIdx.x < p_end) {
+    if ((int)threadIdx.x < a.pages_per_step && base + (int)threadIdx.x < p_end) {
       const float* row = hs + threadIdx.x * a.kv_heads;
       float total = row[0];
       for (int h = 1; h < a.kv_heads; ++h) total = total + row[h];
-      a.scores[(int64_t)b * a.max_pages + base + threadIdx.x] = total / (float)a.q_heads;
+      a.scores[(int64_t)b * a.max_pages + base + threadIdx.x] = canonical_score(total / (float)a.q_heads);
     }
     __syncthreads();
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      mn[e] = mn2[e];
-      mx[e] = mx2[e];
-    }
   }
 }
 
@@ -351,10 +433,21 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   // and are not stored), then the KV-head sums of all slots are formed
   // together: each group of 8 heads issues its lane reads for every slot
   // before the adds, which stay sequential in head order
+  // A slot's chunk sums to NaN when it holds a NaN bound, or a bound that
+  // meets a zero or infinite query in 0 * inf. The latter is rare: only the
+  // elements flagged in has_zero / has_inf are tested, re-read from memory.
   float t[S], total[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    t[s] = group_sum(gq.template chunk_packed<T>(mn[s], mx[s]), lpr);
+    float x = gq.template chunk_packed<T>(mn[s], mx[s]);
+    x = gq.template nan_bound<T>(mn[s], mx[s]) ? __uint_as_float(0x7fc00000u) : x;
+    if (gq.special) {
+      const int p = wave_first + s * ppw + page_local;
+      const int64_t boff = (int64_t)(p < count ? p : wave_first) * page_elems + lane_off;
+      if (zero_inf_chunk<T>(a, (int64_t)b * a.q_bs + (int64_t)kh * G * a.q_hs + sub * E, G, lo, hi, boff, E))
+        x = __uint_as_float(0x7fc00000u);
+    }
+    t[s] = group_sum(x, lpr);
     total[s] = 0.f;
   }
   for (int h0 = 0; h0 < a.kv_heads; h0 += 8) {
@@ -375,12 +468,13 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   for (int s = 0; s < S; ++s) {
     const int p0 = wave_first + s * ppw;
     if (within == 0 && page_local < ppw && p0 + page_local < count)
-      a.scores[(int64_t)b * a.max_pages + p0 + page_local] = total[s] / (float)a.q_heads;
+      a.scores[(int64_t)b * a.max_pages + p0 + page_local] = canonical_score(total[s] / (float)a.q_heads);
   }
 }
 
 // Page-mean score: sum_kh sum_d gq[kh,d] * summary[p,kh,d], with
-// gq = (sum_g q[kh*G+g]) / G.
+// gq = (sum_g q[kh*G+g]) / G. E = 0: a.elems elements per lane, read one by
+// one (the last chunk of a row shorter).
 template <int E>
 __global__ __launch_bounds__(kScoreThreads) void mean_score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
@@ -413,13 +507,21 @@ __global__ __launch_bounds__(kScoreThreads) void mean_score_kernel(ScoreArgs a) 
       const bool data = live && kh < a.kv_heads && sub < a.lanes_used;
       float t = 0.f;
       if (data) {
-        float sv[E];
-        int64_t idx = (int64_t)b * a.b_bs + (int64_t)p * page_elems + (int64_t)kh * a.head_dim + sub * E;
-        load_vec<F32, E>(a.lo, idx, sv);
-        const float* g = gq + kh * a.head_dim + sub * E;
-        t = g[0] * sv[0];
+        const int ne = E > 0 ? E : a.elems;
+        const int64_t idx = (int64_t)b * a.b_bs + (int64_t)p * page_elems + (int64_t)kh * a.head_dim + sub * ne;
+        const float* g = gq + kh * a.head_dim + sub * ne;
+        if constexpr (E > 0) {
+          float sv[E];
+          load_vec<F32, E>(a.lo, idx, sv);
+          t = g[0] * sv[0];
 #pragma unroll
-        for (int e = 1; e < E; ++e) t = t + g[e] * sv[e];
+          for (int e = 1; e < E; ++e) t = t + g[e] * sv[e];
+        } else {
+          const float* sv = static_cast<const float*>(a.lo) + idx;
+          const int n = min(ne, a.head_dim - sub * ne);
+          t = g[0] * sv[0];
+          for (int e = 1; e < n; ++e) t = t + g[e] * sv[e];
+        }
       }
       t = group_sum(t, lpr);
       if (live && kh < a.kv_heads && sub == 0) hs[wave * a.kv_heads + kh] = t;
@@ -428,14 +530,24 @@ __global__ __launch_bounds__(kScoreThreads) void mean_score_kernel(ScoreArgs a) 
     if (live && lane == 0) {
       float total = hs[wave * a.kv_heads];
       for (int kh = 1; kh < a.kv_heads; ++kh) total = total + hs[wave * a.kv_heads + kh];
-      a.scores[(int64_t)b * a.max_pages + p] = total;
+      a.scores[(int64_t)b * a.max_pages + p] = canonical_score(total);
     }
     __syncthreads();
   }
 }
 
+// Keys in descending rank order. Numbers map to 0x007fffff .. 0xff800000
+// (+inf); NaN ranks above every number, as in torch.topk. Quest's forced
+// pages are +inf in the reference (selection.py:86-89), so NaN pages outrank
+// them: they take kForcedQuest, just below NaN. The mean selector adds its
+// required pages outside the top-k (selection.py:138-145): kRequiredMean,
+// above NaN.
+constexpr uint32_t kKeyNaN = 0xfffffffeu;
+constexpr uint32_t kForcedQuest = 0xfffffffdu;
+constexpr uint32_t kRequiredMean = 0xffffffffu;
+
 __device__ __forceinline__ uint32_t order_key(float s) {
-  if (s != s) return 0xfffffffeu;  // NaN ranks just below required pages
+  if (s != s) return kKeyNaN;
   uint32_t u = __float_as_uint(s);
   if (u == 0x80000000u) u = 0u;  // -0.0 ties with +0.0
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
@@ -446,6 +558,7 @@ struct SelectArgs {
   const int64_t* lengths;
   int64_t length;
   int page_size, max_pages, top_pages, keep_sink, mode;
+  uint32_t forced_key;  // key of the forced (required) pages
   FastDiv page_div;
   int32_t* pages;
   int32_t* positions;
@@ -480,7 +593,7 @@ __global__ __launch_bounds__(THREADS) void select_topk_kernel(SelectArgs a) {
       int p = p0 + q;
       key[q] = 0u;
       if (q < per && p < count)
-        key[q] = (p == count - 1 || (second && p == 0)) ? 0xffffffffu : order_key(sc[p]);
+        key[q] = (p == count - 1 || (second && p == 0)) ? a.forced_key : order_key(sc[p]);
     }
     uint32_t prefix = 0u, pmask = 0u;
     int need = k;
@@ -607,7 +720,7 @@ __global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectA
 #pragma unroll
       for (int q = 0; q < KPL; ++q) {
         const int p = q * kWave + lane;
-        key[q] = p >= count ? 0u : (p == count - 1 || (second && p == 0)) ? 0xffffffffu : order_key(sv[q]);
+        key[q] = p >= count ? 0u : (p == count - 1 || (second && p == 0)) ? a.forced_key : order_key(sv[q]);
       }
       // prefix = the largest key x with at least top_pages keys >= x, i.e.
       // the key of the k-th best page
@@ -673,6 +786,106 @@ __global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectA
   }
 }
 
+// Any page count (beyond the register kernels' 16384): every pass recomputes
+// the keys from the scores (which stay in L2), a 4-pass 8-bit radix select
+// over an LDS histogram finds the k-th key, and the chosen pages are
+// compacted in page order, 1024 pages per block scan, straight into
+// `pages`. The page -> token expansion then reads them back (written by this
+// workgroup before the barrier).
+constexpr int kSelectLargeThreads = 1024;
+
+__global__ __launch_bounds__(kSelectLargeThreads) void select_large_kernel(SelectArgs a) {
+  __shared__ int32_t hist[256];
+  __shared__ int32_t scan[kSelectLargeThreads / 64 + 1];
+  __shared__ int32_t pick[2];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
+  const int64_t len = a.lengths ? a.lengths[b] : a.length;
+  int32_t* pages = a.pages + (int64_t)b * a.top_pages;
+  int n_sel = 0;
+  if (a.top_pages < count) {
+    const float* sc = a.scores + (int64_t)b * a.max_pages;
+    const bool second = a.mode == kModeQuest ? (a.keep_sink && a.top_pages > 1 && count > 1) : a.top_pages > 1;
+    auto key_of = [&](int p) -> uint32_t {
+      return (p == count - 1 || (second && p == 0)) ? a.forced_key : order_key(sc[p]);
+    };
+    uint32_t prefix = 0u, pmask = 0u;
+    int need = a.top_pages;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      if (tid < 256) hist[tid] = 0;
+      __syncthreads();
+      for (int p = tid; p < count; p += kSelectLargeThreads) {
+        const uint32_t k = key_of(p);
+        if ((k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1);
+      }
+      __syncthreads();
+      if (tid < 64) {
+        // lane l holds bins 255-4l .. 252-4l (descending digit order)
+        int c[4], csum = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          c[i] = hist[255 - 4 * tid - i];
+          csum += c[i];
+        }
+        int incl = csum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const int o = __shfl_up(incl, d);
+          if (tid >= d) incl += o;
+        }
+        const int before = incl - csum;
+        if (before < need && incl >= need) {
+          int cum = before;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (cum + c[i] >= need) {
+              pick[0] = 255 - 4 * tid - i;
+              pick[1] = need - cum;
+              break;
+            }
+            cum += c[i];
+          }
+        }
+      }
+      __syncthreads();
+      prefix |= (uint32_t)pick[0] << shift;
+      pmask |= 255u << shift;
+      need = pick[1];
+      __syncthreads();
+    }
+    // every key above `prefix` is taken, then the first `need` pages with it
+    int tie_base = 0;
+    for (int c0 = 0; c0 < count; c0 += kSelectLargeThreads) {
+      const int p = c0 + tid;
+      const uint32_t k = p < count ? key_of(p) : 0u;
+      const bool tie = p < count && k == prefix;
+      int n_tie;
+      const int tie_rank = tie_base + block_exclusive_scan<int32_t>(tie ? 1 : 0, scan, &n_tie);
+      const bool sel = p < count && (k > prefix || (tie && tie_rank < need));
+      int n_here;
+      const int out = n_sel + block_exclusive_scan<int32_t>(sel ? 1 : 0, scan, &n_here);
+      if (sel) pages[out] = p;
+      tie_base += n_tie;
+      n_sel += n_here;
+    }
+  } else {
+    n_sel = count;
+    for (int i = tid; i < count; i += kSelectLargeThreads) pages[i] = i;
+  }
+  for (int i = n_sel + tid; i < a.top_pages; i += kSelectLargeThreads) pages[i] = -1;
+  __syncthreads();
+  const int P = a.page_size;
+  const int64_t n_pos = (int64_t)a.top_pages * P;
+  int32_t* pos = a.positions + (int64_t)b * n_pos;
+  for (int64_t i = tid; i < n_pos; i += kSelectLargeThreads) {
+    const uint32_t j = a.page_div.div((uint32_t)i);
+    const int32_t p = pages[j];
+    const int64_t t = (int64_t)p * P + (int64_t)((uint32_t)i - j * (uint32_t)P);
+    pos[i] = (p >= 0 && t < len) ? (int32_t)t : -1;
+  }
+}
+
 static int check_select_common(const char* who, int32_t batch, const void* query, int q_dtype, int32_t q_heads,
                                int32_t kv_heads, int32_t head_dim, const int64_t* lengths, int64_t length,
                                int32_t page_size, int32_t max_pages, int32_t top_pages, float* scores,
@@ -682,9 +895,7 @@ static int check_select_common(const char* who, int32_t batch, const void* query
   if (batch < 0 || q_heads < 1 || kv_heads < 1 || head_dim < 1 || page_size < 1 || max_pages < 1 ||
       top_pages < 1 || q_heads % kv_heads)
     return fail(NHS_ERR_INVALID, "%s: invalid shape or page budget", who);
-  if (max_pages > NHS_MAX_SELECT_PAGES || top_pages > NHS_MAX_SELECT_PAGES)
-    return fail(NHS_ERR_UNSUPPORTED, "%s: at most %d pages", who, NHS_MAX_SELECT_PAGES);
-  if ((int64_t)top_pages * page_size >= (1ll << 31))
+  if ((int64_t)top_pages * page_size >= (1ll << 31) || (int64_t)max_pages * page_size >= (1ll << 32))
     return fail(NHS_ERR_UNSUPPORTED, "%s: top_pages * page_size must be < 2^31", who);
   if (!lengths && (length < 0 || length >= (1ll << 31)))
     return fail(NHS_ERR_INVALID, "%s: length must be in [0, 2^31)", who);
@@ -692,12 +903,20 @@ static int check_select_common(const char* who, int32_t batch, const void* query
 }
 
 // Chunking of a bound row (head_dim elements of `esize` bytes) into lanes:
-// 16-byte chunks when the row is a multiple of 16 bytes, else one element
-// per lane (head_dim <= 64). Returns elements per lane, or 0 if unsupported.
+// 16-byte chunks when the row is a multiple of 16 bytes of at most 64
+// chunks, else one element per lane up to 64 elements, else
+// ceil(head_dim / 64) elements (the last lane's chunk shorter). Returns the
+// elements per lane.
 static int chunk_elems(int head_dim, int esize) {
   if ((head_dim * esize) % 16 == 0 && head_dim * esize / 16 <= 64) return 16 / esize;
   if (head_dim <= 64) return 1;
-  return 0;
+  return (head_dim + 63) / 64;
+}
+
+// A chunk of E elements is loaded as one vector when it is 16 or 32 bytes
+// and divides the row; otherwise element by element (kernel instance E = 0).
+static bool vector_chunk(int head_dim, int E, int esize) {
+  return head_dim % E == 0 && (E * esize == 16 || E * esize == 32);
 }
 
 // Quest cuts a bound row into 32-byte chunks when it is a multiple of 32
@@ -710,7 +929,9 @@ static int quest_chunk_elems(int head_dim, int esize) {
 static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, const char* who, hipEvent_t start,
                          hipEvent_t stop) {
   const int wave_pages = s.max_pages > s.top_pages ? s.max_pages : s.top_pages;
-  if (wave_pages <= kWave * 8)
+  if (wave_pages > NHS_MAX_SELECT_PAGES)
+    launch(select_large_kernel, dim3((unsigned)batch), dim3(kSelectLargeThreads), 0, stream, start, stop, s);
+  else if (wave_pages <= kWave * 8)
     launch(select_wave_kernel<8>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
   else if (wave_pages <= kWave * 16)
     launch(select_wave_kernel<16>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
@@ -739,12 +960,10 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
   if (st != NHS_OK) return st;
   if (items ? !lengths : (!minimum || !maximum)) return fail(NHS_ERR_INVALID, "%s: null bounds", who);
   if (!valid_dtype(bounds_dtype)) return fail(NHS_ERR_INVALID, "%s: bad bounds dtype", who);
-  if ((int64_t)q_heads * head_dim + 8 * q_heads > 16384)
-    return fail(NHS_ERR_UNSUPPORTED, "%s: q_heads * head_dim too large", who);
   const int esize = elem_size(bounds_dtype);
   const int E = quest_chunk_elems(head_dim, esize);
-  if (E == 0) return fail(NHS_ERR_UNSUPPORTED, "%s: head_dim %d unsupported", who, head_dim);
-  if (!items && E > 1 && (((uintptr_t)minimum | (uintptr_t)maximum) % 16 || (bounds_batch_stride * esize) % 16))
+  const bool vec = vector_chunk(head_dim, E, esize);
+  if (!items && vec && (((uintptr_t)minimum | (uintptr_t)maximum) % 16 || (bounds_batch_stride * esize) % 16))
     return fail(NHS_ERR_INVALID, "%s: bounds must be 16-byte aligned", who);
   if (batch == 0) return NHS_OK;
   hipStream_t s = (hipStream_t)stream;
@@ -765,7 +984,8 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
   a.q_heads = q_heads;
   a.kv_heads = kv_heads;
   a.head_dim = head_dim;
-  a.lanes_used = head_dim / E;
+  a.elems = E;
+  a.lanes_used = (head_dim + E - 1) / E;
   a.lpr_log2 = ilog2(a.lanes_used);
   a.lengths = lengths;
   a.length = length;
@@ -773,16 +993,13 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
   a.max_pages = max_pages;
   a.scores = scores;
   a.group = q_heads / kv_heads;
-  const int lanes_per_page = kv_heads << a.lpr_log2;
-  if (a.group > 8 || lanes_per_page > kQuestThreads)
-    return fail(NHS_ERR_UNSUPPORTED, "%s: needs q_heads/kv_heads <= 8 and kv_heads * lanes per head <= %d", who,
-                kQuestThreads);
-  const int G = a.group == 1 ? 1 : a.group == 2 ? 2 : a.group <= 4 ? 4 : 8;
+  const int lpr = 1 << a.lpr_log2;
+  const int lanes_per_page = kv_heads * lpr;
   void (*kernel)(ScoreArgs) = nullptr;
   dim3 grid, block;
   size_t lds = 0;
   const int ppw = lanes_per_page <= kWave ? kWave / lanes_per_page : 0;
-  if (E * esize == 32 && ppw > 0) {
+  if (vec && E * esize == 32 && ppw > 0 && a.group <= 8) {
     // a page fits one wave: the page kernel
     a.pages_per_step = ppw;
     a.pages_per_block = kPageWaves * page_slots(a.group) * ppw;
@@ -801,27 +1018,31 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
 #undef NHS_PAGE_CASE
     }
   } else {
-    const int threads = lanes_per_page >= 256 ? ((lanes_per_page + 63) / 64) * 64 : 256;
-    a.pages_per_step = threads / lanes_per_page;
+    // the general kernel: the folded query in LDS; a page's KV heads in
+    // passes when they need more lanes than the workgroup has
+    const int threads = kQuestThreads;
+    a.heads_per_pass = lanes_per_page <= threads ? kv_heads : threads / lpr;
+    a.pages_per_step = threads / (a.heads_per_pass * lpr);
     a.pages_per_block = a.pages_per_step * ((kPagesPerBlock + a.pages_per_step - 1) / a.pages_per_step);
     grid = dim3((unsigned)((max_pages + a.pages_per_block - 1) / a.pages_per_block), (unsigned)batch);
     block = dim3(threads);
-    lds = ((size_t)q_heads * head_dim + (size_t)a.pages_per_step * kv_heads) * sizeof(float);
-    switch (bounds_dtype * 1024 + E * 16 + G) {
-#define NHS_QUEST_CASE(DT, TY, EE, GG) \
-  case DT * 1024 + EE * 16 + GG: kernel = quest_score_kernel<TY, EE, GG>; break;
-#define NHS_QUEST_GS(DT, TY, EE) \
-  NHS_QUEST_CASE(DT, TY, EE, 1) NHS_QUEST_CASE(DT, TY, EE, 2) NHS_QUEST_CASE(DT, TY, EE, 4) NHS_QUEST_CASE(DT, TY, EE, 8)
-      NHS_QUEST_GS(NHS_F32, F32, 8)
-      NHS_QUEST_GS(NHS_F32, F32, 4)
-      NHS_QUEST_GS(NHS_F32, F32, 1)
-      NHS_QUEST_GS(NHS_F16, F16, 16)
-      NHS_QUEST_GS(NHS_F16, F16, 8)
-      NHS_QUEST_GS(NHS_F16, F16, 1)
-      NHS_QUEST_GS(NHS_BF16, BF16, 16)
-      NHS_QUEST_GS(NHS_BF16, BF16, 8)
-      NHS_QUEST_GS(NHS_BF16, BF16, 1)
-#undef NHS_QUEST_GS
+    const size_t kvd = (size_t)kv_heads * head_dim;
+    lds = kvd * (2 * sizeof(float) + 1) + (size_t)a.pages_per_step * kv_heads * sizeof(float);
+    if (lds > kMaxQuestLds)
+      return fail(NHS_ERR_UNSUPPORTED, "%s: kv_heads * head_dim = %zu exceeds %d", who, kvd, kMaxQuestFold);
+    const int EV = vec ? E : 0;
+    switch (bounds_dtype * 64 + EV) {
+#define NHS_QUEST_CASE(DT, TY, EE) \
+  case DT * 64 + EE: kernel = quest_score_kernel<TY, EE>; break;
+      NHS_QUEST_CASE(NHS_F32, F32, 8)
+      NHS_QUEST_CASE(NHS_F32, F32, 4)
+      NHS_QUEST_CASE(NHS_F32, F32, 0)
+      NHS_QUEST_CASE(NHS_F16, F16, 16)
+      NHS_QUEST_CASE(NHS_F16, F16, 8)
+      NHS_QUEST_CASE(NHS_F16, F16, 0)
+      NHS_QUEST_CASE(NHS_BF16, BF16, 16)
+      NHS_QUEST_CASE(NHS_BF16, BF16, 8)
+      NHS_QUEST_CASE(NHS_BF16, BF16, 0)
 #undef NHS_QUEST_CASE
     }
   }
@@ -841,6 +1062,7 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
   sa.top_pages = top_pages;
   sa.keep_sink = keep_sink;
   sa.mode = kModeQuest;
+  sa.forced_key = kForcedQuest;
   sa.page_div = FastDiv((uint32_t)page_size);
   sa.pages = pages;
   sa.positions = positions;
@@ -883,11 +1105,12 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
                                max_pages, top_pages, scores, pages, positions);
   if (st != NHS_OK) return st;
   if (!summaries) return fail(NHS_ERR_INVALID, "%s: null summaries", who);
-  if ((int64_t)kv_heads * head_dim + 4 * kv_heads > 16384)
+  if (((size_t)kv_heads * head_dim + (size_t)kScoreWaves * kv_heads) * sizeof(float) > kMaxQuestLds)
     return fail(NHS_ERR_UNSUPPORTED, "%s: kv_heads * head_dim too large", who);
   const int E = chunk_elems(head_dim, 4);
-  if (E == 0) return fail(NHS_ERR_UNSUPPORTED, "%s: head_dim %d unsupported", who, head_dim);
-  if (E > 1 && (uintptr_t)summaries % 16) return fail(NHS_ERR_INVALID, "%s: summaries must be 16-byte aligned", who);
+  const bool vec = vector_chunk(head_dim, E, 4);
+  if (vec && ((uintptr_t)summaries % 16 || (summaries_batch_stride * 4) % 16))
+    return fail(NHS_ERR_INVALID, "%s: summaries must be 16-byte aligned", who);
   if (batch == 0) return NHS_OK;
   hipStream_t s = (hipStream_t)stream;
   ScoreArgs a{};
@@ -901,7 +1124,8 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
   a.q_heads = q_heads;
   a.kv_heads = kv_heads;
   a.head_dim = head_dim;
-  a.lanes_used = head_dim / E;
+  a.elems = E;
+  a.lanes_used = (head_dim + E - 1) / E;
   a.lpr_log2 = ilog2(a.lanes_used);
   a.lengths = lengths;
   a.length = length;
@@ -911,10 +1135,12 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
   dim3 grid((unsigned)((max_pages + kPagesPerBlock - 1) / kPagesPerBlock), (unsigned)batch);
   size_t lds = ((size_t)kv_heads * head_dim + (size_t)kScoreWaves * kv_heads) * sizeof(float);
   if (top_pages < max_pages) {
-    if (E == 4)
+    if (vec)
       launch(mean_score_kernel<4>, grid, dim3(kScoreThreads), lds, s, ev.start, nullptr, a);
-    else
+    else if (E == 1)
       launch(mean_score_kernel<1>, grid, dim3(kScoreThreads), lds, s, ev.start, nullptr, a);
+    else
+      launch(mean_score_kernel<0>, grid, dim3(kScoreThreads), lds, s, ev.start, nullptr, a);
     ev.start = nullptr;
     st = launch_status(who);
     if (st != NHS_OK) return st;
@@ -928,6 +1154,7 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
   sa.top_pages = top_pages;
   sa.keep_sink = 1;
   sa.mode = kModeMean;
+  sa.forced_key = kRequiredMean;
   sa.page_div = FastDiv((uint32_t)page_size);
   sa.pages = pages;
   sa.positions = positions;

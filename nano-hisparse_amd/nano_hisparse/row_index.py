@@ -16,20 +16,34 @@ import torch
 
 from .selection import Selection
 
-MAX_POSITIONS = 4096  # NHS_MAX_POSITIONS of include/nhs.h
+MAX_POSITIONS = 32768  # NHS_MAX_POSITIONS of include/nhs.h
 
 
-@dataclass(frozen=True)
 class LogicalTopK:
-    positions: torch.Tensor  # shared [K] token positions (-1 entries are padding)
-    head_columns: torch.Tensor | None = None  # legacy per-head columns into positions
+    """Shared [K] token positions, with optional legacy per-head columns
+    (reference row_index.py:15-51).
+
+    For a selector's device output (ascending positions, -1 padding at the
+    end) `positions` is the exact token list, as the reference builds it
+    (row_index.py:22-23): the padding is cut off on first access, which
+    reads its length back from the device once. The resolver reads the
+    padded tensor (`resolver_positions`; padding resolves to -1) and never
+    waits for that read.
+    """
+
+    __slots__ = ("_positions", "_padded", "head_columns")
+
+    def __init__(self, positions, head_columns=None, *, padded=None):
+        self._positions = positions
+        self._padded = padded
+        self.head_columns = head_columns
 
     @classmethod
     def from_selection(cls, selection: Selection, device):
         device = torch.device(device)
         shared = selection.shared_positions
         if shared is not None and shared.device == device:
-            return cls(shared)
+            return cls(None, padded=shared)
         rows = selection.positions
         if all(row == rows[0] for row in rows):
             return cls(torch.tensor(rows[0], dtype=torch.int32, device=device))
@@ -43,15 +57,32 @@ class LogicalTopK:
             torch.tensor(columns, dtype=torch.int64, device=device),
         )
 
+    @property
+    def positions(self):
+        if self._positions is None:  # the valid entries of the padded output are a prefix
+            self._positions = self._padded[: int((self._padded >= 0).sum())]
+        return self._positions
+
+    @property
+    def resolver_positions(self):
+        """The tensor the resolver reads: the padded selector output, or the
+        exact positions."""
+        return self._padded if self._padded is not None else self._positions
+
     def validate(self, device, maximum):
-        p = self.positions
+        p = self.resolver_positions
         if p.ndim != 1 or p.numel() < 1 or p.dtype not in (torch.int32, torch.int64) or p.device != device:
             raise ValueError("logical top-k must be a nonempty device integer vector")
-        if p.numel() > maximum:
+        # padding never counts: the exact length is read back only when the
+        # padded width exceeds the budget
+        if p.numel() > maximum and self.positions.numel() > maximum:
             raise ValueError("top-k width/union exceeds the admitted max_union_rows")
         c = self.head_columns
         if c is not None and (c.ndim != 2 or c.device != device or c.dtype != torch.int64):
             raise ValueError("head columns must be a device int64 matrix")
+
+    def __repr__(self):
+        return f"LogicalTopK(positions={self.positions!r}, head_columns={self.head_columns!r})"
 
 
 @dataclass
@@ -75,7 +106,7 @@ def resolve_rows(topk, source_table, resident_table, hot_table, tags, lru, lengt
     of the hot slots, least recent first) are updated in place. Duplicate,
     padding and out-of-range positions resolve to -1.
     """
-    positions = topk.positions
+    positions = topk.resolver_positions
     if positions.device.type != "cuda":
         from .row_kernels import cpu_provider
 

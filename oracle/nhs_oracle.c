@@ -17,25 +17,43 @@
  * follow exactly (the reference sums in torch's CPU reduction order, which
  * no other implementation reproduces): a bound row of head_dim elements is
  * cut into E-element chunks (Quest: E = 32 bytes / element size when the
- * row is a multiple of 32 bytes; otherwise, and for the mean selector, 16
- * bytes / element size when the row is a multiple of 16 bytes, else 1);
+ * row is a multiple of 32 bytes of at most 64 chunks; otherwise, and for
+ * the mean selector, 16 bytes / element size when the row is a multiple of
+ * 16 bytes of at most 64 chunks, else 1 up to 64 elements, else
+ * ceil(head_dim / 64) with a shorter last chunk);
  * each chunk is summed sequentially from 0.0; the chunk sums, padded with
  * +0.0 to a power of two, are added as a pairwise tree in chunk order; the
  * per-KV-head sums are added sequentially.
  *
- * Quest (selection.py:84-85) sums max(q*kmin, q*kmax) over the query heads
- * and dimensions. For one KV head and dimension d the heads of its GQA group
- * contribute q*kmax if q > 0 and q*kmin otherwise (kmin <= kmax), that is
- *   kmin[d] * Qneg[d] + kmax[d] * Qpos[d],
+ * Quest (selection.py:84-85) sums torch.maximum(q*lo, q*hi) over the query
+ * heads and dimensions. For one KV head and dimension d, with a = the
+ * smaller and b = the larger of the two bounds (a = hi, b = lo when
+ * hi < lo, else a = lo, b = hi), a head of its GQA group contributes q*b if
+ * q > 0 and q*a otherwise, so the group's terms are
+ *   a[d] * Qneg[d] + b[d] * Qpos[d],
  * with Qpos / Qneg the sums of the group's positive / non-positive query
  * values at d (added sequentially in head order from 0.0). Each chunk step
- * is t = fma(nneg ? kmin : 0, Qneg, t) then t = fma(npos ? kmax : 0, Qpos, t),
- * where npos / nneg say whether any head contributed to Qpos / Qneg: a
- * bound that no head multiplies is never multiplied (so an infinite bound
- * gives no 0 * inf), and NaN queries or bounds propagate as in the
- * reference. The score is the sum over KV heads divided by q_heads. The mean
- * selector rounds each product before adding it. Build with
- * -ffp-contract=off so no other product is fused.
+ * is t = fma(nneg ? a : 0, Qneg, t) then t = fma(npos ? b : 0, Qpos, t),
+ * where npos / nneg say whether any head contributed to Qpos / Qneg.
+ *
+ * Special values follow torch.maximum, which returns NaN when either
+ * product is NaN: a page's score is NaN when one of its bounds is NaN, when
+ * a head's query is +-0 at a d where a bound is +-inf, or when a head's
+ * query is +-inf at a d where a bound is +-0 (each is 0 * inf in one of the
+ * two products). The chunk holding such an element sums to NaN. +-inf
+ * terms of both signs add to NaN, as in the reference's sum. Every NaN score
+ * is stored as the quiet NaN 0x7fc00000.
+ *
+ * The score is the sum over KV heads divided by q_heads. The mean selector
+ * rounds each product before adding it. Build with -ffp-contract=off so no
+ * other product is fused.
+ *
+ * Ranking (torch.topk, selection.py:90): NaN ranks above every number,
+ * including the +inf given to Quest's forced pages (selection.py:86-89), so
+ * NaN pages take slots first; then forced pages; then scores in descending
+ * order. Ties at the k-th key go to the lowest page. The mean selector
+ * (selection.py:138-145) always keeps its required pages, so they rank
+ * above NaN there.
  */
 #include <math.h>
 #include <stdint.h>
@@ -147,10 +165,13 @@ void oracle_attend_rows(const void* q, int q_dtype, int64_t q_bs, int64_t q_hs, 
 
 /* ---- selectors ---------------------------------------------------------------- */
 
+/* Elements per lane chunk: 16 bytes when the row is a multiple of 16 bytes
+   of at most 64 chunks; else one element per lane up to 64 elements; else
+   ceil(head_dim / 64) elements (the last lane's chunk is shorter). */
 static int chunk_elems(int head_dim, int esize) {
   if ((head_dim * esize) % 16 == 0 && head_dim * esize / 16 <= 64) return 16 / esize;
   if (head_dim <= 64) return 1;
-  return 0;
+  return (head_dim + 63) / 64;
 }
 
 /* Quest cuts a bound row into 32-byte chunks when it is a multiple of 32
@@ -158,6 +179,14 @@ static int chunk_elems(int head_dim, int esize) {
 static int quest_chunk_elems(int head_dim, int esize) {
   if ((head_dim * esize) % 32 == 0 && head_dim * esize / 32 <= 64) return 32 / esize;
   return chunk_elems(head_dim, esize);
+}
+
+/* The quiet NaN every NaN score is stored as. */
+static float canonical_nan(void) {
+  const uint32_t bits = 0x7fc00000u;
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
 }
 
 static int pow2_at_least(int v) {
@@ -184,55 +213,63 @@ static void quest_scores_one(const void* q, int q_dtype, int64_t q_hs, const voi
                              int q_heads, int kv_heads, int head_dim, int count, float* scores) {
   const int group = q_heads / kv_heads;
   const int E = quest_chunk_elems(head_dim, elem_size(bdt));
-  const int used = head_dim / E, L = pow2_at_least(used);
+  const int used = (head_dim + E - 1) / E, L = pow2_at_least(used);
   const size_t n = (size_t)kv_heads * head_dim;
   float* qpos = (float*)malloc(sizeof(float) * n);
   float* qneg = (float*)malloc(sizeof(float) * n);
-  char* npos = (char*)malloc(n);
-  char* nneg = (char*)malloc(n);
+  /* bit 0: a head is > 0; bit 1: a head is not > 0; bit 2: a head is +-0;
+     bit 3: a head is +-inf */
+  unsigned char* side = (unsigned char*)malloc(n);
   float* t = (float*)malloc(sizeof(float) * (size_t)L);
   float* hs = (float*)malloc(sizeof(float) * (size_t)kv_heads);
   for (int kh = 0; kh < kv_heads; ++kh)
     for (int d = 0; d < head_dim; ++d) {
       float pos = 0.0f, neg = 0.0f;
-      char np = 0, nn = 0;
+      unsigned char f = 0;
       for (int g = 0; g < group; ++g) {
         float qd = load_elem(q, q_dtype, (int64_t)(kh * group + g) * q_hs + d);
         if (qd > 0.0f) {
           pos = pos + qd;
-          np = 1;
+          f |= 1;
         } else {
           neg = neg + qd;
-          nn = 1;
+          f |= 2;
         }
+        if (qd == 0.0f) f |= 4;
+        if (isinf(qd)) f |= 8;
       }
       qpos[kh * head_dim + d] = pos, qneg[kh * head_dim + d] = neg;
-      npos[kh * head_dim + d] = np, nneg[kh * head_dim + d] = nn;
+      side[kh * head_dim + d] = f;
     }
   for (int p = 0; p < count; ++p) {
     for (int kh = 0; kh < kv_heads; ++kh) {
       const int64_t base = ((int64_t)p * kv_heads + kh) * head_dim;
       for (int l = 0; l < L; ++l) {
         t[l] = 0.0f;
-        if (l >= used) continue;
-        for (int e = 0; e < E; ++e) {
-          int d = l * E + e, i = kh * head_dim + d;
-          float kmin = nneg[i] ? load_elem(lo, bdt, base + d) : 0.0f;
-          float kmax = npos[i] ? load_elem(hi, bdt, base + d) : 0.0f;
-          t[l] = fmaf(kmin, qneg[i], t[l]);
-          t[l] = fmaf(kmax, qpos[i], t[l]);
+        int bad = 0;
+        for (int d = l * E; l < used && d < head_dim && d < (l + 1) * E; ++d) {
+          const int i = kh * head_dim + d;
+          const float x = load_elem(lo, bdt, base + d), y = load_elem(hi, bdt, base + d);
+          const float a = y < x ? y : x, b = y < x ? x : y;
+          const unsigned char f = side[i];
+          t[l] = fmaf((f & 2) ? a : 0.0f, qneg[i], t[l]);
+          t[l] = fmaf((f & 1) ? b : 0.0f, qpos[i], t[l]);
+          bad |= isnan(x) || isnan(y);
+          bad |= (f & 4) && (isinf(x) || isinf(y));
+          bad |= (f & 8) && (x == 0.0f || y == 0.0f);
         }
+        if (bad) t[l] = NAN;
       }
       hs[kh] = tree_sum(t, L);
     }
     float total = hs[0];
     for (int kh = 1; kh < kv_heads; ++kh) total = total + hs[kh];
-    scores[p] = total / (float)q_heads;
+    total = total / (float)q_heads;
+    scores[p] = total != total ? canonical_nan() : total;
   }
   free(qpos);
   free(qneg);
-  free(npos);
-  free(nneg);
+  free(side);
   free(t);
   free(hs);
 }
@@ -241,7 +278,7 @@ static void mean_scores_one(const void* q, int q_dtype, int64_t q_hs, const floa
                             int head_dim, int count, float* scores) {
   const int group = q_heads / kv_heads;
   const int E = chunk_elems(head_dim, 4);
-  const int used = head_dim / E, L = pow2_at_least(used);
+  const int used = (head_dim + E - 1) / E, L = pow2_at_least(used);
   float* gq = (float*)malloc(sizeof(float) * (size_t)kv_heads * head_dim);
   float* t = (float*)malloc(sizeof(float) * (size_t)L);
   for (int kh = 0; kh < kv_heads; ++kh)
@@ -257,24 +294,27 @@ static void mean_scores_one(const void* q, int q_dtype, int64_t q_hs, const floa
       const float* g = gq + kh * head_dim;
       for (int l = 0; l < L; ++l) {
         t[l] = 0.0f;
-        if (l >= used) continue;
-        for (int e = 0; e < E; ++e) {
-          int d = l * E + e;
+        for (int d = l * E; l < used && d < head_dim && d < (l + 1) * E; ++d) {
           float x = g[d] * sv[d];
-          t[l] = e == 0 ? x : t[l] + x;
+          t[l] = d == l * E ? x : t[l] + x;
         }
       }
       float hsum = tree_sum(t, L);
       total = kh == 0 ? hsum : total + hsum;
     }
-    scores[p] = total;
+    scores[p] = total != total ? canonical_nan() : total;
   }
   free(gq);
   free(t);
 }
 
+/* Keys in descending rank order: NaN 0xfffffffe above every number (+inf is
+   0xff800000); Quest's forced pages 0xfffffffd, just below NaN; the mean
+   selector's required pages 0xffffffff, above NaN. */
+enum { KEY_NAN = 0xfffffffeu, KEY_QUEST_FORCED = 0xfffffffdu, KEY_MEAN_REQUIRED = 0xffffffffu };
+
 static uint32_t order_key(float s) {
-  if (s != s) return 0xfffffffeu;
+  if (s != s) return KEY_NAN;
   uint32_t u;
   memcpy(&u, &s, 4);
   if (u == 0x80000000u) u = 0u;
@@ -300,7 +340,7 @@ static int cmp_int(const void* a, const void* b) {
 
 /* Top-k of one request by (score desc, page asc); required pages first. */
 static void select_one(const float* scores, int count, int64_t len, int page_size, int top_pages, int second,
-                       int32_t* pages, int32_t* positions) {
+                       uint32_t forced_key, int32_t* pages, int32_t* positions) {
   int* chosen = (int*)malloc(sizeof(int) * (size_t)(top_pages > 0 ? top_pages : 1));
   int n_sel = 0;
   if (top_pages >= count) {
@@ -309,7 +349,7 @@ static void select_one(const float* scores, int count, int64_t len, int page_siz
     KeyPage* kp = (KeyPage*)malloc(sizeof(KeyPage) * (size_t)count);
     for (int p = 0; p < count; ++p) {
       kp[p].page = p;
-      kp[p].key = (p == count - 1 || (second && p == 0)) ? 0xffffffffu : order_key(scores[p]);
+      kp[p].key = (p == count - 1 || (second && p == 0)) ? forced_key : order_key(scores[p]);
     }
     qsort(kp, (size_t)count, sizeof(KeyPage), cmp_keypage_desc);
     for (int i = 0; i < top_pages; ++i) chosen[n_sel++] = kp[i].page;
@@ -338,7 +378,7 @@ void oracle_quest_select(int batch, const void* q, int q_dtype, int64_t q_bs, in
                        (const char*)minimum + (int64_t)b * b_bs * esize, (const char*)maximum + (int64_t)b * b_bs * esize,
                        bounds_dtype, q_heads, kv_heads, head_dim, count, sc);
     const int second = keep_sink && top_pages > 1 && count > 1;
-    select_one(sc, count, lengths[b], page_size, top_pages, second, pages + (int64_t)b * top_pages,
+    select_one(sc, count, lengths[b], page_size, top_pages, second, KEY_QUEST_FORCED, pages + (int64_t)b * top_pages,
                positions + (int64_t)b * top_pages * page_size);
   }
 }
@@ -352,7 +392,8 @@ void oracle_mean_select(int batch, const void* q, int q_dtype, int64_t q_bs, int
     if (top_pages < count)
       mean_scores_one((const char*)q + ((int64_t)b * q_bs) * elem_size(q_dtype), q_dtype, q_hs, summaries + b * s_bs,
                       q_heads, kv_heads, head_dim, count, sc);
-    select_one(sc, count, lengths[b], page_size, top_pages, top_pages > 1, pages + (int64_t)b * top_pages,
+    select_one(sc, count, lengths[b], page_size, top_pages, top_pages > 1, KEY_MEAN_REQUIRED,
+               pages + (int64_t)b * top_pages,
                positions + (int64_t)b * top_pages * page_size);
   }
 }

@@ -21,7 +21,7 @@ class OracleProvider:
         tags_np = tags.numpy().astype(np.int64)
         lru_np = lru.numpy().astype(np.int64)
         physical, mh, md, counts = oracle.resolve_rows(
-            topk.positions.numpy(), source.numpy(), resident.numpy(), hot.numpy(), tags_np, lru_np, length, page_size
+            topk.resolver_positions.numpy(), source.numpy(), resident.numpy(), hot.numpy(), tags_np, lru_np, length, page_size
         )
         tags.copy_(torch.from_numpy(tags_np))
         lru.copy_(torch.from_numpy(lru_np))

@@ -255,6 +255,14 @@ def _bounds(g, B, n_pages, Hkv, D, dtype, offsets=False):
         (torch.bfloat16, torch.bfloat16, 3, 8, 2, 64, 16, 1000, 40, True),  # one-wave select, 16 keys per lane
         (torch.float32, torch.float32, 2, 4, 2, 16, 5, 513, 64, False),
         (torch.float32, torch.float32, 2, 4, 2, 64, 16, 40, 100, True),  # budget above the page count: -1 padding
+        (torch.bfloat16, torch.bfloat16, 2, 96, 8, 128, 64, 300, 16, True),  # 12 query heads per KV head
+        (torch.bfloat16, torch.bfloat16, 2, 12, 1, 72, 16, 100, 10, True),  # GQA 12, rows of 144 bytes
+        (torch.float32, torch.float32, 2, 8, 2, 100, 16, 60, 8, True),  # rows of 400 bytes: 25 lanes of 16 bytes
+        (torch.bfloat16, torch.bfloat16, 2, 4, 2, 100, 16, 60, 8, True),  # rows of 200 bytes: 2 elements per lane
+        (torch.bfloat16, torch.float32, 1, 16, 8, 520, 16, 50, 6, True),  # 9 elements per lane, last lane short
+        (torch.bfloat16, torch.bfloat16, 2, 64, 16, 128, 64, 200, 12, True),  # 128 lanes per page: general kernel
+        (torch.float32, torch.float32, 1, 64, 64, 256, 4, 20, 4, True),  # 2048 lanes per page: KV heads in passes
+        (torch.bfloat16, torch.bfloat16, 1, 8, 2, 64, 2, 20000, 100, True),  # beyond 16384 pages
     ],
 )
 def test_quest_select_bit_exact(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, n_pages, top, keep_sink):
@@ -278,49 +286,53 @@ def test_quest_select_bit_exact(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, n_pages, 
 
 
 @pytest.mark.parametrize(
-    "dtype,B,Hq,Hkv,D,P,n_pages,top",
+    "dtype,Hq,Hkv,D,nan_pages,top,inf_query",
     [
-        (torch.bfloat16, 3, 32, 8, 128, 64, 96, 8),  # 4 query heads per KV head
-        (torch.bfloat16, 3, 28, 4, 128, 32, 96, 8),  # 7 per KV head
-        (torch.float32, 2, 8, 2, 64, 16, 50, 6),
-        (torch.float16, 2, 6, 2, 128, 16, 50, 6),  # 3 per KV head
+        (torch.bfloat16, 32, 8, 128, 0, 8, False),  # page kernel, group 4
+        (torch.bfloat16, 32, 8, 128, 3, 8, False),  # NaN pages below the budget
+        (torch.bfloat16, 28, 4, 128, 8, 8, False),  # group 7: NaN pages fill the budget
+        (torch.bfloat16, 8, 2, 64, 11, 8, False),  # more NaN pages than slots
+        (torch.float32, 8, 2, 64, 3, 6, False),  # fp32 page kernel
+        (torch.float16, 6, 2, 128, 3, 6, False),  # fp16, group 3
+        (torch.bfloat16, 12, 1, 72, 4, 10, False),  # group 12, general kernel
+        (torch.bfloat16, 64, 16, 128, 4, 10, False),  # general kernel, 16-byte loads
+        (torch.bfloat16, 32, 8, 128, 4, 4, True),  # an infinite query
+        (torch.bfloat16, 32, 8, 128, 4, 8, True),
     ],
 )
-def test_quest_scores_with_special_values_bit_exact(gpu, dtype, B, Hq, Hkv, D, P, n_pages, top):
-    """Queries and bounds holding +-inf, NaN, +-0 and exact ties: every score
-    (NaN where the oracle's is NaN) and every selection equal the oracle's."""
-    log_case(test="quest-special", dtype=dtype, B=B, Hq=Hq, Hkv=Hkv, D=D, n_pages=n_pages)
-    g = torch.Generator().manual_seed(D + Hq)
-    q = torch.randn(B, Hq, D, generator=g)
-    pick = torch.randint(0, 8, q.shape, generator=g)
-    q[pick == 0] = 0.0
-    q[pick == 1] = -0.0
-    q[0, 1, 3], q[0, 2, 5], q[1, 0, 7] = float("inf"), float("-inf"), float("nan")
-    q = q.to(dtype)
-    mn, mx = _bounds(g, B, n_pages, Hkv, D, dtype, offsets=False)
-    mn, mx = mn.float(), mx.float()
-    mn[:, 5], mx[:, 5] = mn[:, 4], mx[:, 4]  # an exact tie between pages 4 and 5
-    mx[0, 7, 0, 1] = float("inf")
-    mn[0, 8, 1, 2] = float("-inf")
-    mx[1, 9, 0, :] = float("nan")
-    mn[2 % B, 10, Hkv - 1, D - 1] = float("-inf")
-    mn[:, 11], mx[:, 11] = 0.0, -0.0
-    mn, mx = mn.to(dtype), mx.to(dtype)
-    lengths = torch.full((B,), n_pages * P)
+def test_quest_special_values_match_oracle_and_reference(gpu, dtype, Hq, Hkv, D, nan_pages, top, inf_query):
+    """Zero and infinite queries; +-inf, NaN, zero and inverted bounds; NaN
+    pages below, at and above the budget. Every score (NaN as 0x7fc00000)
+    and every page equals the oracle's, and the pages are a top-k of the
+    reference formula's ranking (torch.maximum scores, forced pages at +inf,
+    NaN above them: selection.py:82-90), the same set wherever that ranking
+    has no tie at the k-th key."""
+    from quest_reference import check_page_set, reference_ranked, special_case
+
+    log_case(test="quest-special", dtype=dtype, Hq=Hq, Hkv=Hkv, D=D, nan_pages=nan_pages, top=top, inf=inf_query)
+    n_pages, P, B = 40, 16, 6
+    cases = [special_case(100 * s + Hq + D, Hq, Hkv, D, n_pages, nan_pages, inf_query, dtype) for s in range(B)]
+    q = torch.stack([c[0] for c in cases])
+    mn = torch.stack([c[1] for c in cases])
+    mx = torch.stack([c[2] for c in cases])
+    lengths = torch.full((B,), n_pages * P - 5)
     e_scores, e_pages, e_pos = oracle.quest_select(q, mn, mx, lengths, P, top)
     pages, pos, scores = rk.quest_batched(q.to(gpu), mn.to(gpu), mx.to(gpu), lengths.to(gpu), P, top)
-    scores = scores.cpu()[:, :n_pages]
-    nan = torch.isnan(e_scores[:, :n_pages])
-    assert torch.equal(torch.isnan(scores), nan)
-    assert torch.equal(scores[~nan].view(torch.int32), e_scores[:, :n_pages][~nan].view(torch.int32))
-    assert nan.any() and torch.isinf(e_scores[:, :n_pages]).any()
+    scores = scores.cpu()
+    assert torch.equal(scores.view(torch.int32), e_scores.view(torch.int32))
     assert torch.equal(pages.cpu(), e_pages)
     assert torch.equal(pos.cpu(), e_pos)
+    for b, (qb, lob, hib, nan_set) in enumerate(cases):
+        assert {p for p in range(n_pages) if torch.isnan(scores[b, p])} == nan_set
+        check_page_set(pages[b].cpu(), reference_ranked(qb, lob, hib, int(lengths[b]), P, top), top)
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,D,P,n_pages,top", [(4, 32, 8, 128, 64, 512, 32), (3, 4, 2, 8, 4, 20, 1),
                                                       (2, 4, 2, 8, 4, 20, 2), (2, 6, 3, 24, 5, 33, 7),
-                                                      (2, 4, 2, 16, 8, 700, 50)])
+                                                      (2, 4, 2, 16, 8, 700, 50),
+                                                      (2, 24, 2, 100, 16, 60, 8),  # GQA 12, 25 lanes of 16 bytes
+                                                      (2, 8, 2, 300, 16, 40, 6),  # 5 elements per lane
+                                                      (1, 8, 2, 16, 2, 20000, 64)])  # beyond 16384 pages
 def test_mean_select_bit_exact(gpu, B, Hq, Hkv, D, P, n_pages, top):
     log_case(test="mean", B=B, Hq=Hq, D=D, n_pages=n_pages, top=top)
     g = torch.Generator().manual_seed(5 + n_pages)

@@ -110,34 +110,59 @@ def test_quest_pages_agree_with_float64_scores_outside_ties():
             assert abs(ex[p].item() - kth) < 1e-4
 
 
-def test_quest_infinite_and_nan_bounds_behave_as_the_reference_maximum():
-    """Bounds of +-inf (keys of inf) and NaN: the score is finite exactly where
-    the reference's sum of max(q*kmin, q*kmax) is, and NaN/inf where it is.
-    The grouped form never multiplies a bound that no head selects, so an
-    infinite bound on the unused side gives no 0 * inf."""
-    Hq, Hkv, D, P = 4, 2, 8, 4
-    q = torch.tensor([[1.0, -2.0, 0.5, 3.0, -1.0, 2.0, -0.5, 1.5]]).repeat(Hq, 1)
-    q[1] = -q[1].abs()  # KV head 0 serves heads 0 (mixed signs) and 1 (all negative)
-    q[2] = q[2].abs()  # KV head 1 serves heads 2 (all positive) and 3 (mixed signs)
-    mn = torch.full((1, 6, Hkv, D), -1.0)
-    mx = torch.full((1, 6, Hkv, D), 1.0)
-    mx[0, 1, 0, 1] = float("inf")  # d 1: both heads of KV head 0 are negative, kmax unused: finite
-    mn[0, 2, 1, 0] = float("-inf")  # d 0: both heads of KV head 1 are positive, kmin unused: finite
-    mx[0, 3, 0, :] = float("nan")  # NaN bounds: NaN score
-    mn[0, 4, 0, 2] = float("-inf")  # d 2: head 1 is negative and reads kmin: +inf
-    qe = q.double()
-    kmin = mn.double().repeat_interleave(2, 2)
-    kmax = mx.double().repeat_interleave(2, 2)
-    ref = torch.maximum(qe[None, None] * kmin, qe[None, None] * kmax).sum(-1).mean(-1)[0]
-    scores, _, _ = oracle.quest_select(q[None], mn, mx, [6 * P], P, 2)
-    for p in range(6):
-        r, s_ = ref[p].item(), scores[0, p].item()
-        if math.isnan(r):
-            assert math.isnan(s_), p
-        elif math.isinf(r):
-            assert s_ == r, p
-        else:
-            assert abs(s_ - r) < 1e-5, (p, s_, r)
+@pytest.mark.parametrize("Hq,Hkv,D,nan_pages,top,inf_query,unique_set", [
+    (32, 8, 128, 0, 8, False, True),    # no NaN page
+    (32, 8, 128, 3, 8, False, True),    # NaN pages below the budget: forced pages kept
+    (28, 4, 128, 8, 8, False, True),    # NaN pages fill the budget: forced pages dropped
+    (8, 2, 64, 11, 8, False, False),    # more NaN pages than slots (ties among NaN)
+    (6, 2, 24, 5, 9, False, True),      # group 3, rows of 48 bytes (16-byte chunks)
+    (12, 1, 72, 4, 10, False, True),    # group 12 (one KV head), head_dim 72
+    (32, 8, 128, 4, 4, True, True),     # an infinite query: +-inf and NaN pages only
+    (32, 8, 128, 4, 8, True, False),    # ... with slots left inside the +inf tie
+])
+def test_quest_special_values_match_the_reference_formula(Hq, Hkv, D, nan_pages, top, inf_query, unique_set):
+    """Zero and infinite queries, +-inf / NaN / zero / inverted bounds: the
+    oracle's scores are NaN, +-inf or finite exactly where the reference's
+    torch.maximum formula (evaluated with torch ops, selection.py:82-85) is,
+    and its pages are a top-k of the reference's ranking (NaN above the
+    forced +inf pages, selection.py:86-90); unique wherever that ranking has
+    no tie at the k-th key."""
+    from quest_reference import check_page_set, check_score_classes, reference_ranked, reference_scores, special_case
+
+    n_pages, P = 40, 16
+    unique = 0
+    for seed in range(6):
+        q, lo, hi, nan_set = special_case(100 * seed + Hq + D, Hq, Hkv, D, n_pages, nan_pages, inf_query)
+        length = n_pages * P - 5
+        scores, pages, _ = oracle.quest_select(q[None], lo[None], hi[None], [length], P, top)
+        ref = reference_scores(q, lo, hi, n_pages)
+        assert {p for p in range(n_pages) if math.isnan(ref[p])} == nan_set
+        check_score_classes(scores[0, :n_pages], ref)
+        assert all(scores[0, p].view(torch.int32).item() == 0x7FC00000 for p in nan_set)
+        ranked = reference_ranked(q, lo, hi, length, P, top)
+        unique += check_page_set(pages[0], ranked, top)
+        if nan_pages >= top:  # NaN outranks the forced pages: they are dropped
+            assert set(pages[0].tolist()) <= nan_set
+        if nan_pages > top and not inf_query:  # inside the NaN tie: the lowest pages
+            assert pages[0].tolist() == sorted(nan_set)[:top]
+    if unique_set:  # the reference's page set is unique for these inputs, and equal
+        assert unique == 6
+
+
+def test_quest_forced_pages_rank_below_nan_and_above_inf():
+    """Ranking alone: NaN > forced (+inf) > natural +inf > finite, lowest page
+    first inside a class: the sink before the last page (all three +inf in
+    the reference, where torch.topk's pick among them is unspecified)."""
+    Hq, Hkv, D, P, n_pages = 2, 1, 8, 4, 10
+    q = torch.ones(Hq, D)
+    lo = torch.zeros(n_pages, Hkv, D)
+    hi = torch.arange(n_pages, dtype=torch.float32)[:, None, None].expand(n_pages, Hkv, D).clone()
+    hi[3, 0, 2] = math.nan
+    hi[6, 0, 4] = math.nan
+    hi[5, 0, 0] = math.inf  # natural +inf
+    for top, want in ((2, [3, 6]), (3, [0, 3, 6]), (4, [0, 3, 6, 9]), (5, [0, 3, 5, 6, 9]), (6, [0, 3, 5, 6, 8, 9])):
+        _, pages, _ = oracle.quest_select(q[None], lo[None], hi[None], [n_pages * P], P, top)
+        assert pages[0].tolist() == want, (top, pages[0].tolist())
 
 
 def test_mean_select_forces_first_and_last_page():
