@@ -188,7 +188,13 @@ def random_positions(rng, B, K, length, P, mode):
         (3, 1024, 1024, 32, 256, "pages", 4),  # H = U: every miss replaces a row
         (2, 777, 1500, 7, 300, "random", 4),  # unsorted, duplicates, invalid entries, odd sizes
         (2, 4096, 8192, 64, 2048, "pages", 2),  # 128K context, 4096-row budget
-        (1, 4096, 32768, 16, 4096, "random", 2),  # maximum sizes
+        (1, 4096, 32768, 16, 4096, "random", 2),  # largest in-LDS sort
+        (3, 4097, 8192, 32, 1000, "pages", 2),  # first size of the large-K kernel
+        (2, 8192, 16384, 64, 1024, "pages", 3),  # top-128 pages of 64 rows
+        (2, 8192, 8192, 64, 512, "random", 3),  # unsorted large K: radix sort, duplicates, H = K
+        (2, 5000, 6000, 7, 2000, "random", 3),  # odd sizes
+        (1, 32768, 32768, 64, 2048, "pages", 2),  # maximum, sorted (selector output)
+        (1, 32768, 32768, 16, 4096, "random", 2),  # maximum, unsorted
     ],
 )
 def test_resolver_matches_oracle_over_steps(gpu, B, K, H, P, n_pages, mode, steps):

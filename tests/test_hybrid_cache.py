@@ -270,3 +270,30 @@ def test_deferred_reuse_keeps_host_rows_and_hot_readers_alive(gpu):
     torch.testing.assert_close(seen, k[0])
     cache.release_request("same")
     cache.assert_invariants()
+
+
+def test_a_selection_of_8192_rows_resolves_and_attends(device):
+    """Quest top-128 pages of 64 rows (8192 positions, max_union_rows 8192,
+    hot_rows 16384, both within the reference's HotConfig limits,
+    hybrid.py:31-41) decodes through HybridKVCache.attention: rows beyond the
+    in-LDS resolver's 4096 go through the large-selection resolver."""
+    from nano_hisparse.selection import quest_selection
+
+    P, pages = 64, 300
+    cfg = CacheConfig(gpu_pages=270, host_pages=pages + 8, page_size=P, kv_heads=2, head_dim=64, device=device)
+    cache = HybridKVCache(cfg, HotConfig(128 * P))
+    cache.reserve("a", pages * P, 1)
+    k, v = append(cache, count=pages * P - 17)
+    request = cache.storage.requests["a"]
+    length = request.lengths[0]
+    for step in range(2):  # the second step hits the rows the first one gathered
+        q = torch.randn(4, 64, device=device)
+        sel = quest_selection(q, request.minimum[0], request.maximum[0], length, P, 128)
+        assert len(sel.pages) == 128 and pages - 1 in sel.pages
+        chosen = list(sel.positions[0])
+        assert len(chosen) == 128 * P - 17
+        out = cache.attention(q, "a", 0, sel)
+        torch.testing.assert_close(out, dense_attention(q, k[chosen], v[chosen]), atol=1e-4, rtol=1e-4)
+    stats = cache.snapshot()["row_stats"]
+    assert stats["resident_hits"] + stats["hot_hits"] + stats["misses"] == 2 * len(chosen)
+    cache.assert_invariants()
