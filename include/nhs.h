@@ -144,6 +144,26 @@ int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_batch_stride,
                     int64_t workspace_bytes, void* stream);
 
 /*
+ * nhs_attend_rows without a workspace argument, for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. Its
+ * workspace is a file-scope device array of NHS_ATTEND_NOALLOC_BYTES that
+ * each GPU holds until the process ends; a shape whose
+ * nhs_attend_workspace_bytes exceeds it returns NHS_ERR_WORKSPACE. The
+ * call allocates nothing; a device's first call sets the array up on the
+ * caller's stream. Every call on one GPU shares the array, so calls that
+ * overlap on one GPU race. Results equal nhs_attend_rows's bit for bit.
+ */
+#define NHS_ATTEND_NOALLOC_BYTES (32ll << 20)
+int nhs_attend_rows_noalloc(const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                            int64_t q_head_stride, const void* pool, int32_t kv_dtype,
+                            const int64_t* rows, int64_t rows_batch_stride,
+                            int64_t rows_head_stride, int64_t rows_col_stride, int32_t batch,
+                            int32_t n_rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                            int32_t page_size, void* out, int64_t out_batch_stride,
+                            int64_t out_head_stride, void* stream);
+
+/*
  * Row resolver for `batch` independent (request, layer) items, one
  * workgroup each, with no host round trip. Item b reads positions[b, :n]
  * (int32 or int64 per positions_i64), its page tables source/resident

@@ -703,3 +703,73 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
          a);
   return launch_status("nhs_attend_rows");
 }
+
+// ---- allocation-free entry point -------------------------------------------
+//
+// nhs_attend_rows_noalloc runs nhs_attend_rows on a workspace held in this
+// file-scope device array, for callers that cannot allocate. Each GPU the
+// library runs on holds its own copy until the process ends. On a device's
+// first call (with that device current) the array's device address is
+// looked up with hipGetSymbolAddress and kept per device, and its header
+// (arrival counters and zero block) is cleared by a fill kernel on the
+// caller's stream; every call leaves the header zero again. Host code uses
+// only the looked-up address, never the array's name. All calls on one GPU
+// share the array, so calls that overlap on one GPU race.
+namespace nhs {
+
+constexpr int64_t kNoAllocScratchBytes = NHS_ATTEND_NOALLOC_BYTES;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+__global__ void clear_words_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// The current device's address of `scratch`, set up on its first call.
+static int scratch_on_device(hipStream_t stream, void** out) {
+  static std::mutex mu;
+  static std::vector<std::pair<int, void*>> addresses;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, "nhs_attend_rows_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& a : addresses)
+    if (a.first == dev) {
+      *out = a.second;
+      return NHS_OK;
+    }
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return fail(e != hipSuccess ? (int)e : NHS_ERR_INVALID, "nhs_attend_rows_noalloc: hipGetSymbolAddress: %s",
+                hipGetErrorString(e));
+  hipLaunchKernelGGL(clear_words_kernel, dim3(64), dim3(256), 0, stream, static_cast<uint32_t*>(p),
+                     kHeaderBytes / (int64_t)sizeof(uint32_t));
+  const int st = launch_status("nhs_attend_rows_noalloc");
+  if (st != NHS_OK) return st;
+  addresses.emplace_back(dev, p);
+  *out = p;
+  return NHS_OK;
+}
+
+}  // namespace nhs
+
+extern "C" int nhs_attend_rows_noalloc(const void* query, int32_t q_dtype, int64_t q_batch_stride,
+                                       int64_t q_head_stride, const void* pool, int32_t kv_dtype, const int64_t* rows,
+                                       int64_t rows_batch_stride, int64_t rows_head_stride, int64_t rows_col_stride,
+                                       int32_t batch, int32_t n_rows, int32_t q_heads, int32_t kv_heads,
+                                       int32_t head_dim, int32_t page_size, void* out, int64_t out_batch_stride,
+                                       int64_t out_head_stride, void* stream) {
+  using namespace nhs;
+  const int64_t need = nhs_attend_workspace_bytes(batch, q_heads, head_dim, n_rows);
+  if (need > kNoAllocScratchBytes)
+    return fail(NHS_ERR_WORKSPACE,
+                "nhs_attend_rows_noalloc: this shape needs %lld bytes of scratch, above the %lld-byte maximum",
+                (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int st = scratch_on_device((hipStream_t)stream, &ws);
+  if (st != NHS_OK) return st;
+  return nhs_attend_rows(query, q_dtype, q_batch_stride, q_head_stride, pool, kv_dtype, rows, rows_batch_stride,
+                         rows_head_stride, rows_col_stride, batch, n_rows, q_heads, kv_heads, head_dim, page_size, out,
+                         out_batch_stride, out_head_stride, ws, kNoAllocScratchBytes, stream);
+}

@@ -37,6 +37,11 @@ SIGNATURES = {
          _i64, _p, _i64, _p],
         ctypes.c_int,
     ),
+    "nhs_attend_rows_noalloc": (
+        [_p, _i32, _i64, _i64, _p, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64,
+         _i64, _p],
+        ctypes.c_int,
+    ),
     "nhs_resolve_rows": (
         [_i32, _i32, _p, _i32, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p,
          _p, _p, _i64, _p, _p, _p],
