@@ -343,18 +343,13 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
 #pragma unroll
           for (int e = 0; e < E; ++e) acc[g][c][e] *= alpha[g];
       if constexpr (PK) {
-        // P.V with v_dot2 over pairs of rows: the weights are rounded to the
-        // KV dtype and the denominator sums the same rounded weights, so the
-        // output stays an exact convex combination of the V rows.
-        uint32_t pp[G][U / 2];
+        // P.V in fp32, as the reference's numerator (row_kernels.py:109-110):
+        // each V element is widened once and serves the G heads' weights.
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           float psum = 0.f;
 #pragma unroll
-          for (int j = 0; j < U / 2; ++j) {
-            pp[g][j] = pack_pair<T>(p[g][2 * j], p[g][2 * j + 1]);
-            psum += pair_lo<T>(pp[g][j]) + pair_hi<T>(pp[g][j]);
-          }
+          for (int u = 0; u < U; ++u) psum += p[g][u];
           l[g] = l[g] * alpha[g] + psum;
         }
 #pragma unroll
@@ -362,14 +357,13 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
 #pragma unroll
           for (int w = 0; w < 4; ++w)
 #pragma unroll
-            for (int j = 0; j < U / 2; ++j) {
-              const uint32_t x = word_of(vr[2 * j][c], w), y = word_of(vr[2 * j + 1][c], w);
-              const uint32_t lo = __builtin_amdgcn_perm(y, x, 0x05040100u);  // (x.lo, y.lo)
-              const uint32_t hi = __builtin_amdgcn_perm(y, x, 0x07060302u);  // (x.hi, y.hi)
+            for (int u = 0; u < U; ++u) {
+              const uint32_t x = word_of(vr[u][c], w);
+              const float lo = pair_lo<T>(x), hi = pair_hi<T>(x);
 #pragma unroll
               for (int g = 0; g < G; ++g) {
-                acc[g][c][2 * w] = packed_dot<T>(lo, pp[g][j], acc[g][c][2 * w]);
-                acc[g][c][2 * w + 1] = packed_dot<T>(hi, pp[g][j], acc[g][c][2 * w + 1]);
+                acc[g][c][2 * w] = __builtin_fmaf(p[g][u], lo, acc[g][c][2 * w]);
+                acc[g][c][2 * w + 1] = __builtin_fmaf(p[g][u], hi, acc[g][c][2 * w + 1]);
               }
             }
       } else {

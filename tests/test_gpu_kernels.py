@@ -95,6 +95,35 @@ def test_attend_rows_matches_oracle(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, N, pe
     assert err <= ATOL[dtype if dtype != torch.float32 else q_dtype], err
 
 
+@pytest.mark.parametrize("N", [16, 64, 256, 2048])
+@pytest.mark.parametrize("score_std,v_std", [(4.0, 4.0), (4.0, 8.0), (3.0, 8.0)])
+def test_attend_rows_precision_with_peaky_scores_and_large_values(gpu, N, score_std, v_std):
+    """Scores of std 3-4 (few rows carry the weight) and V of std 4-8, bf16
+    query and KV (the packed path): within 2e-2 of the float64 oracle beyond
+    the rounding of the output to bf16 (half an ulp of the expected value;
+    the reference rounds its output to the query's dtype too,
+    attention.py:35). The weights stay fp32 in P.V as in the reference
+    (row_kernels.py:109-110)."""
+    log_case(test="attend-precision", N=N, score_std=score_std, v_std=v_std)
+    B, Hq, Hkv, D, P = 4, 32, 8, 128, 64
+    g = torch.Generator().manual_seed(N + int(10 * score_std + v_std))
+    blocks = max(4, -(-N // P) + 4)
+    s = score_std ** 0.5  # q and k of std s: q.k / sqrt(D) has std s^2
+    pool = torch.randn(blocks, 2, P, Hkv, D, generator=g)
+    pool[:, 0] *= s
+    pool[:, 1] *= v_std
+    pool = pool.bfloat16()
+    q = (s * torch.randn(B, Hq, D, generator=g)).bfloat16()
+    rows = torch.stack([torch.randperm(blocks * P, generator=g)[:N] for _ in range(B)])
+    expected = oracle.attend_rows(q, pool, rows, P)
+    out = rk.attend_batched(q.to(gpu), pool.to(gpu), rows.to(gpu), P).cpu().float()
+    mag = torch.maximum(expected.abs(), out.abs()).clamp_min(2.0 ** -126)
+    half_ulp = (mag.log2().floor() - 8).exp2()  # bf16 keeps 8 significant bits
+    beyond = ((out - expected).abs() - half_ulp).clamp_min(0).max().item()
+    print(f"max error beyond output rounding {beyond:.3e}; max-abs {(out - expected).abs().max().item():.3e}")
+    assert beyond <= 2e-2
+
+
 def test_attend_rows_repeated_calls_share_one_workspace(gpu):
     """The splits of a head group are merged by the last workgroup to arrive
     (arrival counters in the workspace, left at zero by every call). Many
