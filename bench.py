@@ -83,6 +83,9 @@ def parse_args():
     ap.add_argument("--workload", choices=("kernel", "miss-heavy", "model", "resolver-stress"), default="kernel",
                     help="kernel: one-layer sparse decode step (default); miss-heavy: the same step at batch 4, "
                     "128K context, 4096-row budget, ~90%% of rows gathered; model: whole-model batched decode")
+    ap.add_argument("--warm-steps", type=int, default=None,
+                    help="kernel workloads: steps of the warm single-layer pass (default --steps; 0: none, as for "
+                    "a kernel-trace profile whose attention dispatches should all be cold)")
     ap.add_argument("--cold-layers", type=int, default=4,
                     help="kernel workloads: layers with their own device state cycled by the timed steps")
     ap.add_argument("--model-steps", type=int, default=16,
@@ -674,12 +677,16 @@ def main():
     kernel_us = {n: len(stamped[0][n]) * launch_us(stamped, n) for n in names}
     kernel_us["gather"] = gather_us  # from the timed pass, like the attention's launch time
     # warm: every step on layer 0, whose data the previous step left in the caches
-    warm_events = []
-    for _ in range(args.steps):
-        full = w.step.timing_events()
-        warm_events.append({"gather": full["gather"], "attention": full["attention"]})
-    warm_ms, _, _ = timed_pass(lambda i: w, warm_events)
-    warm_attn_us = launch_us(warm_events, "attention")
+    warm_steps = args.steps if args.warm_steps is None else args.warm_steps
+    if warm_steps > 0:
+        warm_events = []
+        for _ in range(warm_steps):
+            full = w.step.timing_events()
+            warm_events.append({"gather": full["gather"], "attention": full["attention"]})
+        steps, args.steps = args.steps, warm_steps
+        warm_ms, _, _ = timed_pass(lambda i: w, warm_events)
+        args.steps = steps
+        warm_attn_us = launch_us(warm_events, "attention")
 
     # measured pinned H2D copy ceiling (copy engine), for reference
     probe = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
@@ -770,7 +777,7 @@ def main():
             "launch_us": round(warm_attn_us, 2),
             "step_us": round(warm_ms * 1e3, 2),
             "cache": "warm: layer 0 repeated, ~202 MB per step (below the 256 MB Infinity Cache)",
-        },
+        } if warm_steps > 0 else None,
         "gather_roofline": {
             "kernel": "nhs_gather_rows (gather_rows_kernel)",
             "bound": "pcie",

@@ -227,3 +227,130 @@ def test_miss_heavy_long_context(gpu):
     assert torch.equal(pool.cpu().view(torch.uint8), cpool.view(torch.uint8))
     e_out = oracle.attend_rows(q.cpu(), cpool, torch.from_numpy(e_phys), P)
     assert (out.float().cpu() - e_out).abs().max().item() <= 2e-2
+
+
+def _llama8b_width_engine(device, layers, prompt, new_tokens, B=8):
+    """A random-init decoder of Llama-3-8B width (hidden 4096, 32/8 heads x
+    128, MLP 14336, vocab 128256, bf16, seed 42) with `layers` layers, B
+    requests of `prompt` seeded random tokens, pages of 64, 2048 hot rows,
+    Quest top-32 pages and a pool of the admission credits plus 30% of the
+    history, through the batched engine."""
+    from math import ceil
+
+    from nano_hisparse.config import CacheConfig
+    from nano_hisparse.engine import Engine
+    from nano_hisparse.hybrid import HotConfig, HybridKVCache
+    from nano_hisparse.model import Model, ModelConfig
+
+    cfg = ModelConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=layers,
+                      num_attention_heads=32, num_key_value_heads=8, rope_theta=10000.0)
+    torch.manual_seed(42)
+    default_dtype = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            model = Model(cfg).eval()
+    finally:
+        torch.set_default_dtype(default_dtype)
+    P, H, top = 64, 2048, 32
+    pages = ceil((prompt + new_tokens) / P)
+    hot = HotConfig(H, H)
+    kv = CacheConfig(gpu_pages=B * hot.admission_blocks(P, layers) + int(0.3 * B * layers * pages),
+                     host_pages=B * layers * pages, page_size=P, kv_heads=8, head_dim=128, dtype=torch.bfloat16,
+                     device=str(device))
+    cache = HybridKVCache(kv, hot)
+    engine = Engine(model, cache, top_k=top, batch_decode=True)
+    g = torch.Generator().manual_seed(42)
+    for b in range(B):
+        engine.add_request(f"r{b}", torch.randint(0, cfg.vocab_size, (prompt,), generator=g).tolist(), new_tokens)
+    while engine.waiting:
+        engine.step()
+    return engine, cache
+
+
+@pytest.mark.gpu
+def test_llama8b_width_batched_decode_matches_the_oracle_per_layer(gpu, monkeypatch):
+    """Config 4's width at 2 layers: 8 requests x 8229-token prompts (129
+    pages, so Quest scores them and picks 32; a history four times the
+    32-block hot region, so with a pool of the admission credits plus 30% of
+    the history most pages live on the host and selected rows are gathered),
+    2048 hot rows, top-32 pages. For every layer of
+    every batched decode step (Model.decode_batch -> BatchDecode), the
+    selected pages and positions, resolved rows, miss plans, counts, tags
+    and LRU order, and the whole pool after the gather equal the oracle's on
+    the same inputs, and attention is within 2e-2 of the oracle's."""
+    from nano_hisparse import batched
+
+    log_case(test="llama8b-width", layers=2, requests=8, prompt=8229)
+    steps = 4
+    # admission decodes the admitted requests meanwhile: nobody may finish before the checked steps end
+    engine, cache = _llama8b_width_engine(gpu, layers=2, prompt=8229, new_tokens=8 + steps + 2)
+    store = cache.storage
+    P = cache.config.page_size
+    expected_out = {}
+    checked = []
+    orig_select, orig_finish = batched.BatchDecode.select, batched.BatchDecode.finish
+
+    def select(self, layer, query, top_pages, keep_sink=True):
+        torch.cuda.synchronize()
+        reqs = [store.requests[r] for r in self.ids]
+        lengths = torch.tensor([r.lengths[layer] for r in reqs])
+        mn = torch.stack([r.minimum[layer][: self.max_pages] for r in reqs]).cpu()
+        mx = torch.stack([r.maximum[layer][: self.max_pages] for r in reqs]).cpu()
+        tables = [cache.tables[r, layer] for r in self.ids]
+        src = [t.source.cpu().numpy() for t in tables]
+        res = [t.resident.cpu().numpy() for t in tables]
+        hot = [t.hot.cpu().numpy() for t in tables]
+        tags = [t.tags.cpu().numpy().astype(np.int64) for t in tables]
+        lru = [t.lru.cpu().numpy().copy() for t in tables]
+        q, pool = query.cpu(), cache.pool.cpu()
+        seen = {}
+
+        def quest_items(*a, **k):
+            seen["quest"] = rk_quest(*a, **k)
+            return seen["quest"]
+
+        def resolve_items(*a, **k):
+            seen["resolve"] = rk_resolve(*a, **k)
+            return seen["resolve"]
+
+        monkeypatch.setattr(rk, "quest_items", quest_items)
+        monkeypatch.setattr(rk, "resolve_items", resolve_items)
+        try:
+            handle = orig_select(self, layer, query, top_pages, keep_sink)
+        finally:
+            monkeypatch.setattr(rk, "quest_items", rk_quest)
+            monkeypatch.setattr(rk, "resolve_items", rk_resolve)
+        torch.cuda.synchronize()
+        _, e_pages, e_pos = oracle.quest_select(q, mn, mx, lengths, P, top_pages, keep_sink)
+        pages, positions, _ = seen["quest"]
+        assert torch.equal(pages.cpu(), e_pages) and torch.equal(positions.cpu(), e_pos), layer
+        physical, mh, md, counts = (t.cpu().numpy() for t in seen["resolve"])
+        for b, t in enumerate(tables):
+            want = oracle.resolve_rows(e_pos[b].numpy(), src[b], res[b], hot[b], tags[b], lru[b],
+                                       int(lengths[b]), P)
+            for got, exp in zip((physical[b], mh[b], md[b], counts[b]), want):
+                np.testing.assert_array_equal(got, exp)
+            np.testing.assert_array_equal(t.tags.cpu().numpy(), tags[b])
+            np.testing.assert_array_equal(t.lru.cpu().numpy(), lru[b])
+        oracle.gather_rows(store.host, pool, mh.reshape(-1), md.reshape(-1), P)
+        assert torch.equal(cache.pool.cpu().view(torch.uint8), pool.view(torch.uint8)), layer
+        expected_out[id(self), layer] = oracle.attend_rows(q, pool, torch.from_numpy(physical), P)
+        checked.append((layer, int(counts[:, 2].sum())))
+        return handle
+
+    def finish(self, handle):
+        out = orig_finish(self, handle)
+        torch.cuda.synchronize()
+        want = expected_out.pop((id(self), handle[0]))
+        assert (out.cpu().float() - want).abs().max().item() <= 2e-2
+        return out
+
+    rk_quest, rk_resolve = rk.quest_items, rk.resolve_items
+    monkeypatch.setattr(batched.BatchDecode, "select", select)
+    monkeypatch.setattr(batched.BatchDecode, "finish", finish)
+    for _ in range(steps):
+        assert len(engine.step()) == 8
+    assert len(checked) == 2 * steps and not expected_out
+    assert sum(m for _, m in checked) > 0  # rows were gathered from the host store
+    cache.assert_invariants()
