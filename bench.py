@@ -93,6 +93,8 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=32, help="model workload: decoder layers")
     ap.add_argument("--prompt", type=int, default=16384, help="model workload: prompt tokens per request")
     ap.add_argument("--requests", type=int, default=8, help="model workload: concurrent requests")
+    ap.add_argument("--graph", type=int, default=1, choices=(0, 1),
+                    help="model workloads: 1 replays each decode step from a captured HIP graph")
     ap.add_argument("--micro-batches", type=int, default=1, choices=(1, 2),
                     help="model workload: 2 pipelines two halves of the batch (gathers beside compute)")
     return ap.parse_args()
@@ -510,7 +512,8 @@ def model_decode(args, B, L, T, K, W):
     print(f"[bench] cache: {kv.gpu_pages} pool blocks ({kv.gpu_pages * kv.row_bytes * P / 2**30:.1f} GiB), "
           f"{kv.host_pages} host pages ({kv.host_pages * kv.row_bytes * P / 2**30:.1f} GiB pinned), "
           f"{time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
-    engine = Engine(model, cache, top_k=top, batch_decode=True, micro_batches=args.micro_batches)
+    graph = bool(args.graph) and args.micro_batches == 1
+    engine = Engine(model, cache, top_k=top, batch_decode=True, micro_batches=args.micro_batches, graph=graph)
     gen = torch.Generator().manual_seed(args.seed)
     for b in range(B):
         engine.add_request(f"r{b}", torch.randint(0, cfg.vocab_size, (T,), generator=gen).tolist(), new_tokens)
@@ -564,6 +567,7 @@ def model_decode(args, B, L, T, K, W):
             "prompt": T,
             "layers": L,
             "micro_batches": args.micro_batches,
+            "decode_graph": graph,
             "parallelism": "single GPU",
         },
         "rows_per_step": {"resident_hits": resident_hits / K, "hot_hits": hot_hits / K, "misses": misses / K},
@@ -833,6 +837,7 @@ def main():
                 "value": m["value"], "unit": "tokens/s", "ms_per_step": m["ms_per_step"], "steps": m["steps"],
                 "workload": m["config"]["workload"], "step_roofline": m["step_roofline"],
                 "rows_per_step": m["rows_per_step"], "pcie_gbs": m["pcie_gbs"], "admit_s": m["admit_s"],
+                "decode_graph": m["config"]["decode_graph"],
             }
         except Exception as exc:  # the kernel line stands on its own
             result["model_decode"] = {"error": f"{type(exc).__name__}: {exc}"}

@@ -38,12 +38,14 @@ class BatchDecode:
     be appended before it is attended; lengths advance per layer.
     """
 
-    def __init__(self, cache, request_ids, overlap=False):
+    def __init__(self, cache, request_ids, overlap=False, lengths_buffer=None):
         """overlap=True puts each layer's gather on the cache's transfer
         stream, ordered by events, for callers that run other work beside
         it; by default it runs in order on the compute stream (a gather
         that nothing runs beside gains nothing from a second queue and would
-        pay two cross-queue event hops per layer)."""
+        pay two cross-queue event hops per layer). lengths_buffer: a device
+        int64 [2, B] tensor that receives the step's lengths (the kernels
+        read it), for a caller that replays captured launches reading it."""
         store = cache.storage
         if not store.cuda:
             raise RuntimeError("batched decode runs on a GPU cache (libnhs_hip.so)")
@@ -71,8 +73,13 @@ class BatchDecode:
         self.layers = store.requests[ids[0]].layers
         self.items = cache._layer_items(ids)
         self.max_pages = max(store.requests[r].page_count for r in ids)
-        both = torch.tensor([lengths, [n + 1 for n in lengths]], dtype=torch.int64)
-        self.dev_lengths = both.pin_memory().to(cache.device, non_blocking=True)
+        both = torch.tensor([lengths, [n + 1 for n in lengths]], dtype=torch.int64).pin_memory()
+        if lengths_buffer is None:
+            self.dev_lengths = both.to(cache.device, non_blocking=True)
+        else:
+            if lengths_buffer.shape != both.shape or lengths_buffer.dtype != torch.int64:
+                raise ValueError("lengths_buffer must be int64 [2, B]")
+            self.dev_lengths = lengths_buffer.copy_(both, non_blocking=True)
         self._appended = set()
         self._attended = set()
         self._pages = self._place_all()
@@ -133,9 +140,15 @@ class BatchDecode:
             raise ValueError("K/V dtype/device must match the cache")
         if not (k[0].is_contiguous() and v[0].is_contiguous() and k.stride() == v.stride()):
             k, v = k.contiguous(), v.contiguous()  # rows may be views of a fused projection
-        pages = self._pages[layer]
         rk.append_items(k, v, cache.pool, store.host_alias, self.items[layer], self.dev_lengths[0])
-        P = cfg.page_size
+        self._account_append(layer)
+
+    def _account_append(self, layer):
+        """The host state of layer's append: page contents and versions,
+        request lengths, the mirror byte count."""
+        cache, store = self.cache, self.cache.storage
+        P = cache.config.page_size
+        pages = self._pages[layer]
         row_bytes = store.page_bytes // P
         for rid, length, page in zip(self.ids, self.lengths, pages):
             page.valid_tokens = length % P + 1
@@ -144,8 +157,28 @@ class BatchDecode:
             page.host_enqueued_version = page.content_version
             store.requests[rid].lengths[layer] = length + 1
         self._written.extend(pages)
-        store.stats["d2h_bytes"] += row_bytes * B
+        store.stats["d2h_bytes"] += row_bytes * len(self.ids)
         self._appended.add(layer)
+
+    def sync_tables(self):
+        """Make the compute stream wait for every pending event of the batch's
+        tables (all layers) now, so the layer launches that follow wait for
+        none (as launches replayed from a captured graph cannot)."""
+        store = self.cache.storage
+        tables = [self.cache.tables[rid, layer] for layer in range(self.layers) for rid in self.ids]
+        _wait_all(store, store.compute, (t.ready for t in tables))
+        for t in tables:
+            t.ready = None
+
+    def account_replayed(self):
+        """Host state of a step whose launches were replayed from a captured
+        graph of a step over the same batch: every layer appended and
+        attended, gathers in order on the compute stream."""
+        if self.overlap:
+            raise RuntimeError("replayed steps gather on the compute stream")
+        for layer in range(self.layers):
+            self._account_append(layer)
+            self._attended.add(layer)
 
     def end(self):
         """Close the step: one compute-stream event, recorded after every

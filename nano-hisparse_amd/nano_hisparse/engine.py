@@ -28,11 +28,12 @@ class Request:
 
 class Engine:
     def __init__(self, model: Model, cache, top_k=None, backend="auto", eos_token_id=None, selector="quest",
-                 batch_decode=False, micro_batches=1):
+                 batch_decode=False, micro_batches=1, graph=False):
         """batch_decode=True gives all running requests their decode turn in
         one Model.decode_batch call (GPU cache, Quest top_k; micro_batches=2
-        pipelines two halves of the batch); emission order and admission are
-        unchanged."""
+        pipelines two halves of the batch; graph=True replays each batch
+        composition's step from a captured HIP graph); emission order and
+        admission are unchanged."""
         cfg, kv = model.config, cache.config
         if (cfg.num_key_value_heads, cfg.head_dim) != (kv.kv_heads, kv.head_dim):
             raise ValueError("model/cache head dimensions differ")
@@ -47,6 +48,9 @@ class Engine:
             raise ValueError("batched decode needs a GPU cache and the Quest selector with a top_k")
         self.batch_decode = batch_decode
         self.micro_batches = micro_batches
+        self.graph = graph
+        if graph and (not batch_decode or micro_batches != 1):
+            raise ValueError("graph replay needs batch_decode with one micro-batch")
         self.requests: dict = {}
         self.waiting: deque = deque()
         self.running: deque = deque()
@@ -113,7 +117,7 @@ class Engine:
             self.running.clear()
             logits = self.model.decode_batch(
                 [r.generated[-1] for r in batch], [r.request_id for r in batch], self.cache, self.top_k,
-                micro_batches=self.micro_batches,
+                micro_batches=self.micro_batches, graph=self.graph,
             )
             for request, token in zip(batch, logits.argmax(-1).tolist()):
                 request.decode_count += 1

@@ -612,11 +612,11 @@ class HybridKVCache:
 
     # ---- batched decode ---------------------------------------------------------------------
 
-    def decode_batch(self, request_ids, overlap=False):
+    def decode_batch(self, request_ids, overlap=False, lengths_buffer=None):
         """A BatchDecode step over `request_ids` (one new token each)."""
         from .batched import BatchDecode
 
-        return BatchDecode(self, request_ids, overlap)
+        return BatchDecode(self, request_ids, overlap, lengths_buffer)
 
     def _layer_items(self, request_ids):
         """Device table [layers, B, nhs_layer_item] of the requests' tables,

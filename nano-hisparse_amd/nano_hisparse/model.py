@@ -248,7 +248,8 @@ class Model(nn.Module):
         return out
 
     @torch.inference_mode()
-    def decode_batch(self, tokens: list[int], request_ids: list, cache, top_k: int, micro_batches: int = 1):
+    def decode_batch(self, tokens: list[int], request_ids: list, cache, top_k: int, micro_batches: int = 1,
+                     graph: bool = False):
         """One decode step for several requests at once (Quest top_k pages).
 
         Dense layers run on the batch with fused projections (one q/k/v
@@ -260,7 +261,12 @@ class Model(nn.Module):
         (transfer stream) runs beside the other group's layer compute; the
         gather's grid is capped meanwhile to leave compute units to that
         work. Returns fp32 logits [B, vocab]; row b equals decode(tokens[b],
-        request_ids[b]) up to the order of the dense layers' reductions."""
+        request_ids[b]) up to the order of the dense layers' reductions.
+
+        graph=True (one group) replays the step's launches from a HIP graph
+        captured at the first step of this batch composition (see
+        _decode_batch_graph): the same kernels on the same buffers, with no
+        per-launch host work."""
         from . import row_kernels as rk
 
         if len(tokens) != len(request_ids):
@@ -269,6 +275,10 @@ class Model(nn.Module):
             raise ValueError("batched decode needs a positive Quest top_k")
         if micro_batches not in (1, 2):
             raise ValueError("micro_batches must be 1 or 2")
+        if graph:
+            if micro_batches != 1:
+                raise ValueError("graph replay runs one group")
+            return self._decode_batch_graph(tokens, request_ids, cache, top_k)
         n = len(tokens)
         if n < 2:
             micro_batches = 1
@@ -304,21 +314,82 @@ class Model(nn.Module):
         return _linear(self.model.norm(x), self.lm_head.weight, self.lm_head.bias).float()
 
 
+    def _decode_batch_graph(self, tokens, request_ids, cache, top_k):
+        """decode_batch with the step's launches (every layer, the final norm
+        and the lm_head) captured once per batch composition into a HIP graph
+        and replayed from then on.
+
+        Per step, outside the graph: the page placement and residency policy
+        (BatchDecode's constructor; its table writes precede the replay on
+        the compute stream), the upload of the lengths and token ids into the
+        buffers the graph reads, the wait for the tables' pending events, and
+        after the replay the pages' host state and the policy tick (end()).
+        Every launch's shape depends only on the batch, the budget and the
+        requests' reserved pages, so the replayed step is the eager one. A
+        graph is reused only while the cache's device item table of the
+        composition is the same object (it holds the pointers the graph
+        read); otherwise it is captured again."""
+        store = cache.storage
+        store.check_stream()
+        graphs = self.__dict__.setdefault("_decode_graphs", {})
+        key = (tuple(request_ids), top_k)
+        items = cache._layer_items(request_ids)
+        entry = graphs.get(key)
+        if entry is not None and (entry["cache"] is not cache or entry["items"] is not items):
+            del graphs[key]
+            entry = None
+        n = len(tokens)
+        token_ids = torch.tensor(tokens, dtype=torch.int64).pin_memory()
+        if entry is None:
+            lengths = torch.empty(2, n, dtype=torch.int64, device=cache.device)
+            ids = torch.empty(n, dtype=torch.int64, device=cache.device)
+            step = cache.decode_batch(request_ids, lengths_buffer=lengths)
+            step.sync_tables()
+            ids.copy_(token_ids, non_blocking=True)
+            fused = self._fused_projections()
+            graph = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream(device=cache.device)
+            side.wait_stream(store.compute)
+            with store.capturing(side), torch.cuda.graph(graph, stream=side):
+                group = _Group(self, None, request_ids, cache, False, step=step, ids=ids)
+                for index, layer in enumerate(self.model.layers):
+                    group.pre(index, layer, fused[index], top_k)
+                    group.post(layer)
+                x = group.x + group.delta
+                logits = _linear(self.model.norm(x), self.lm_head.weight, self.lm_head.bias).float()
+            # the capture stream lives as long as the graph: buffers cached per stream during the capture
+            # (the attention workspace) belong to the graph's memory
+            entry = {"cache": cache, "items": items, "lengths": lengths, "ids": ids, "graph": graph,
+                     "logits": logits, "stream": side}
+            graphs[key] = entry
+            while len(graphs) > 8:  # the most recent compositions keep their graphs
+                del graphs[next(iter(graphs))]
+        else:
+            step = cache.decode_batch(request_ids, lengths_buffer=entry["lengths"])
+            step.sync_tables()
+            entry["ids"].copy_(token_ids, non_blocking=True)
+            step.account_replayed()
+        entry["graph"].replay()
+        step.end()
+        return entry["logits"].clone()
+
+
 class _Group:
     """One batch group of decode_batch: its residual stream, RoPE tables,
     cache step and the gather handle in flight."""
 
-    def __init__(self, model, tokens, request_ids, cache, overlap):
+    def __init__(self, model, tokens, request_ids, cache, overlap, step=None, ids=None):
         cfg = model.config
         self.model, self.cfg = model, cfg
-        self.step = cache.decode_batch(request_ids, overlap)
+        self.step = cache.decode_batch(request_ids, overlap) if step is None else step
         D = cfg.head_dim
         positions = self.step.dev_lengths[0]  # already on the device
         inv_freq = cfg.rope_theta ** (-torch.arange(0, D, 2, device=model.device).float() / D)
         angle = positions.float()[:, None] * inv_freq[None, :]
         self.cos = angle.cos().to(model.dtype).contiguous()
         self.sin = angle.sin().to(model.dtype).contiguous()
-        ids = torch.tensor(tokens, dtype=torch.int64).pin_memory().to(model.device, non_blocking=True)
+        if ids is None:
+            ids = torch.tensor(tokens, dtype=torch.int64).pin_memory().to(model.device, non_blocking=True)
         self.x = model.model.embed_tokens(ids).contiguous()
         self.delta = None
         self.handle = None

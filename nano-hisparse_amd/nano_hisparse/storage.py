@@ -12,6 +12,8 @@ reused. The store knows no residency policy: callers place pages.
 
 from __future__ import annotations
 
+import contextlib
+
 from collections import Counter
 from contextlib import nullcontext
 from dataclasses import dataclass, field
@@ -146,6 +148,7 @@ class HostStore:
 
             self.host_alias = MappedHost(self.host)
         self.compute = torch.cuda.current_stream(self.device) if self.cuda else None
+        self._capture_stream = None
         self.transfer = torch.cuda.Stream(device=self.device) if self.cuda else None
         self.pages: dict = {}
         self.group_pages: dict = {}  # (request_id, layer) -> pages in index order
@@ -217,8 +220,19 @@ class HostStore:
             stream.wait_event(event)
 
     def check_stream(self):
-        if self.cuda and torch.cuda.current_stream(self.device) != self.compute:
+        if self.cuda and torch.cuda.current_stream(self.device) not in (self.compute, self._capture_stream):
             raise RuntimeError("cache operations must use the construction compute stream")
+
+    @contextlib.contextmanager
+    def capturing(self, stream):
+        """Within: cache operations may also run on `stream`, whose launches
+        are being captured into a graph that is replayed on the compute
+        stream (so the stream order of cache work is unchanged)."""
+        previous, self._capture_stream = self._capture_stream, stream
+        try:
+            yield
+        finally:
+            self._capture_stream = previous
 
     def synchronize(self):
         if self.cuda:

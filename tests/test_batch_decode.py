@@ -194,3 +194,65 @@ def test_engine_batch_decode_generates_the_sequential_tokens(gpu, micro_batches)
         assert not cache.storage.requests and not any(cache.owners)
         cache.assert_invariants()
     assert results[0] == results[1]
+
+
+@pytest.mark.gpu
+def test_graph_replayed_decode_equals_the_eager_decode(gpu):
+    """Engine(graph=True) replays each batch composition's step from a HIP
+    graph captured at its first step. Run in lockstep with an eager batched
+    engine on the same model and prompts (separate caches of one config),
+    over admissions (each new composition is captured) and a finished
+    request, with the engines' own host work and synchronisations between
+    the replays: every step's logits are equal bit for bit, and so are the
+    tokens. Projections of this model all take nhs_linear_small_m."""
+    log_case(test="decode-graph")
+    cfg = ModelConfig(vocab_size=32000, hidden_size=2048, intermediate_size=4096, num_hidden_layers=2,
+                      num_attention_heads=16, num_key_value_heads=4)
+    torch.manual_seed(7)
+    default = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(gpu):
+            model = Model(cfg).eval()
+    finally:
+        torch.set_default_dtype(default)
+    P, top = 16, 4
+    hot = HotConfig(top * P, top * P)
+    g = torch.Generator().manual_seed(3)
+    prompts = [torch.randint(0, cfg.vocab_size, (n,), generator=g).tolist() for n in (200, 150, 260)]
+    budgets = (12, 5, 12)  # the second request finishes mid-run: a new composition
+
+    def engine(graph):
+        kv = CacheConfig(gpu_pages=3 * hot.admission_blocks(P, 2) + 16, host_pages=3 * 2 * 24, page_size=P,
+                         kv_heads=4, head_dim=128, dtype=torch.bfloat16, device=str(gpu))
+        e = Engine(model, HybridKVCache(kv, hot), top_k=top, batch_decode=True, graph=graph)
+        for i, (prompt, n) in enumerate(zip(prompts, budgets)):
+            e.add_request(f"r{i}", prompt, n)
+        return e
+
+    seen = []
+    decode_batch = model.decode_batch
+
+    def recording(*a, **k):
+        out = decode_batch(*a, **k)
+        seen.append((k.get("graph", False), out.clone()))
+        return out
+
+    model.decode_batch = recording
+    try:
+        eager, replayed = engine(False), engine(True)
+        steps = 0
+        while eager.waiting or eager.running:
+            a, b = eager.step(), replayed.step()
+            torch.cuda.synchronize()
+            assert a == b, steps
+            steps += 1
+    finally:
+        del model.decode_batch
+    assert steps >= 10
+    pairs = list(zip(seen[0::2], seen[1::2]))
+    assert pairs and all(not ge and gr for (ge, _), (gr, _) in pairs)
+    for i, ((_, le), (_, lr)) in enumerate(pairs):
+        assert torch.equal(le.view(torch.int32), lr.view(torch.int32)), i
+    graphs = model.__dict__["_decode_graphs"]
+    assert 1 <= len(graphs) < len(pairs)  # most steps replayed an existing graph
