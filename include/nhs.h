@@ -217,7 +217,9 @@ int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t po
  * ascending to pages[b, :top_pages]
  * (-1 padded when count < top_pages) and expanded to causal token positions
  * positions[b, :top_pages*page_size] (ascending, -1 padded). scores[b, :]
- * (max_pages floats) is scratch that keeps the scores.
+ * (max_pages floats) keeps the scores. With pages and positions both NULL
+ * only the scores are computed (nothing runs when top_pages >= max_pages:
+ * every page is then kept), for nhs_select_resolve_rows / _items.
  * minimum/maximum are [max_pages, kv_heads, head_dim] per request.
  * Replaces quest_selection, nano_hisparse/selection.py:69-91.
  */
@@ -234,8 +236,9 @@ int nhs_quest_select(int32_t batch, const void* query, int32_t q_dtype, int64_t 
  * summaries[p, kv_heads, head_dim], pages {0, count-1} ({count-1} when
  * top_pages == 1) are always kept and the best top_pages - |kept| other
  * pages (score descending, page ascending; NaN ranks first, below the kept
- * pages) are added. Output layout as in nhs_quest_select. Replaces
- * select_pages, nano_hisparse/selection.py:119-145.
+ * pages) are added. Output layout, and the scores-only form (pages and
+ * positions NULL), as in nhs_quest_select. Replaces select_pages,
+ * nano_hisparse/selection.py:119-145.
  */
 int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q_batch_stride,
                     int64_t q_head_stride, const float* summaries, int64_t summaries_batch_stride,
@@ -300,6 +303,41 @@ int nhs_resolve_items(int32_t batch, int32_t n, const void* positions, int32_t p
                       const int64_t* lengths, int32_t page_size, int64_t* physical, int64_t* miss_host,
                       int64_t* miss_device, int64_t plan_stride, int64_t* counts, int64_t* counts_total,
                       void* stream);
+
+/*
+ * Page selection and row resolution in one launch, one workgroup per item:
+ * the selection step of nhs_quest_select (mode 0, keep_sink as there) or
+ * nhs_mean_select (mode 1) on scores[b, :max_pages] as their scores-only
+ * form leaves them, writing pages[b, :top_pages] and
+ * positions[b, :n] (n = top_pages * page_size) exactly as the selector
+ * does, then nhs_resolve_rows on those n positions (int32, in order). Every
+ * output is bit-identical to the selector launch followed by the resolver
+ * launch. Requires max(max_pages, top_pages) <= 1024 and n <= 4096, else
+ * returns NHS_ERR_UNSUPPORTED (the two launches handle any size). Tables,
+ * outputs and plan_stride as nhs_resolve_rows; the selection stays in LDS,
+ * so no launch boundary and no global round trip separate the two steps.
+ * Replaces the sequence quest_selection / select_pages then resolve_rows
+ * (nano_hisparse/selection.py:69-91, 119-145; row_index.py:62-140).
+ */
+int nhs_select_resolve_rows(int32_t batch, const float* scores, int32_t max_pages, int32_t mode,
+                            int32_t top_pages, int32_t keep_sink, const int32_t* source,
+                            const int32_t* resident, int64_t page_table_stride, int32_t n_pages,
+                            const int32_t* hot, int64_t hot_stride, int32_t* tags, int64_t tags_stride,
+                            int64_t* lru, int64_t lru_stride, int32_t hot_rows, const int64_t* lengths,
+                            int64_t length, int32_t page_size, int32_t* pages, int32_t* positions,
+                            int64_t* physical, int64_t* miss_host, int64_t* miss_device,
+                            int64_t plan_stride, int64_t* counts, int64_t* counts_total, void* stream);
+
+/*
+ * nhs_select_resolve_rows over per-item tables, as nhs_resolve_items reads
+ * them (lengths required).
+ */
+int nhs_select_resolve_items(int32_t batch, const float* scores, int32_t max_pages, int32_t mode,
+                             int32_t top_pages, int32_t keep_sink, const nhs_layer_item* items,
+                             int32_t hot_rows, const int64_t* lengths, int32_t page_size, int32_t* pages,
+                             int32_t* positions, int64_t* physical, int64_t* miss_host,
+                             int64_t* miss_device, int64_t plan_stride, int64_t* counts,
+                             int64_t* counts_total, void* stream);
 
 /*
  * Elementwise stages of the batched decode layer (model.py:43-71, 140-158 of

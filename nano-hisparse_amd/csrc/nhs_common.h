@@ -64,6 +64,18 @@ struct FastDiv {
 
 // ---- element conversion -------------------------------------------------
 
+// Pointers known to address global memory: loads and stores through them
+// compile to global_* instructions. Through a generic pointer (one read from
+// a table in memory, or chosen between two) they are flat instructions, which
+// also count against the LDS wait counter, so every wait for an LDS result
+// would also wait for them.
+#define NHS_GLOBAL __attribute__((address_space(1)))
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));  // copyable from any address space
+template <typename T>
+__device__ __forceinline__ NHS_GLOBAL T* to_global(T* p) {
+  return (NHS_GLOBAL T*)p;
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {

@@ -4,17 +4,23 @@
 //
 // The semantics are those of resolve_rows (nano_hisparse/row_index.py:62-140),
 // restated as LDS passes instead of sorts over the hot rows:
+//  0. (resolve_rows_kernel<KPL > 0>, nhs_select_resolve_*) wave 0 selects the
+//     top_pages best pages of the item's scores as the selectors do
+//     (wave_select, select_common.h) while the other waves stage the tables;
+//     the chosen pages expanded to tokens are the positions.
 //  1. keys (norm << 32 | input index), norm = raw if 0 <= raw < length else
 //     length, bitonic-sorted in LDS unless already in order: sorted order =
 //     ascending logical, and the first entry of each run of equal positions
 //     is its first occurrence in the input.
-//  2. per sorted entry: page/offset, source and resident tables, host row,
-//     valid / resident_hit / needs_hot.
+//  2. per sorted entry: page/offset, source and resident tables (staged in
+//     LDS at entry when they fit), host row, valid / resident_hit /
+//     needs_hot.
 //  3. an LDS hash of the host rows that need the hot buffer.
 //  4. one coalesced pass over tags: a tag found in the hash is a hot hit for
 //     that host row and marks its slot protected.
 //  5. victims = lru stably partitioned (unprotected first): the lru values
-//     are staged in LDS and ranked in 1024-slot chunks with wave ballots.
+//     are staged in LDS and ranked in 1024-slot chunks with wave ballots
+//     and a DPP scan of the per-wave counts.
 //     The same pass writes the new lru: it is the lru stably partitioned by
 //     category (untouched, inserted, hit, inserted hit). Misses take the
 //     first n_miss victims, so with U / Pr the unprotected / protected slots
@@ -24,7 +30,7 @@
 //  6. miss ranks by a block scan; assigned slot = victims[rank].
 //  7. physical rows (scattered back to input order), compact miss plan, tag
 //     writes for misses.
-#include "nhs_common.h"
+#include "select_common.h"
 
 namespace nhs {
 
@@ -37,6 +43,8 @@ constexpr int kRegH = 8;        // hot rows per thread whose tag and lru are loa
 constexpr int kHotCache = 1024; // hot blocks staged in LDS at entry
 constexpr int kWaves = kResolveThreads / 64;
 constexpr int kRankGroup = 4;   // 1024-slot chunks ranked per barrier
+constexpr int kTableCache = 2048;  // page table entries staged in LDS at entry
+constexpr int kFusedMaxPages = kWave * 16;  // pages the fused select ranks in one wave
 
 struct ResolveArgs {
   int n;  // positions per item
@@ -65,11 +73,23 @@ struct ResolveArgs {
   int64_t* counts;
   int64_t* counts_total;
   const nhs_layer_item* items;  // per-item tables (then the strided table fields are unused)
+  // fused selection (resolve_rows_kernel<KPL > 0>): the positions are the
+  // top_pages best pages of `scores` expanded to tokens, n = top_pages * P
+  const float* scores;  // [batch, max_pages]
+  int max_pages, top_pages, keep_sink, mode;
+  uint32_t forced_key;
+  int32_t* pages_out;      // [batch, top_pages]
+  int32_t* positions_out;  // [batch, n]
 };
 
 struct ResolveShared {
   union {
-    uint64_t keys[kMaxK];  // phase 1-2
+    struct {
+      uint64_t keys[kMaxK];           // phase 1-2
+      int32_t src[kTableCache];       // the item's page tables, when they fit
+      int32_t res[kTableCache];
+      int32_t chosen[kFusedMaxPages]; // fused selection: chosen pages, ascending, -1 padded
+    } e;
     struct {
       int32_t hkey[kHashCap];  // phase 3-4: wanted host rows
       int32_t hslot[kHashCap]; // hot slot holding that host row, or -1
@@ -79,32 +99,38 @@ struct ResolveShared {
   uint32_t prot[kMaxH / 32];  // protected slot bits
   int32_t victims[kMaxK];     // victims[0 .. min(n, H)-1]
   int32_t red[2][kWaves * 8];                    // one scratch row per block reduction
-  int32_t wcount[2][kRankGroup][kWaves][4];      // per-wave category counts, double-buffered
+  int32_t wcount[2][kRankGroup][kWaves];         // per-wave unprotected counts, double-buffered
   int32_t hot[kHotCache];                      // the item's hot block table, when it fits
 };
 
 // Block reductions with one barrier each. Every call site passes its own
 // scratch row, so no barrier is needed before the scratch is reused.
 
-// Sums of N ints over the block; every thread receives the sums.
+// Sum of x over each 16-lane row of the wave, in every lane of the row.
+__device__ __forceinline__ int row_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  x += __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  x += __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  x += __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);  // row_mirror
+  return x;
+}
+
+// Sums of N ints over the block; every thread receives the sums. Wave sums
+// are row sums read from lanes 0, 16, 32, 48; after the barrier lane w
+// (< kWaves) of every wave reads wave w's sums and a row sum adds them.
 template <int N>
 __device__ __forceinline__ void block_sums(int (&v)[N], int32_t* scratch) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1)
-#pragma unroll
-    for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], d);
-  if (lane == 0)
-#pragma unroll
-    for (int i = 0; i < N; ++i) scratch[wave * N + i] = v[i];
+  for (int i = 0; i < N; ++i) {
+    const int r = row_sum(v[i]);
+    const int t = __builtin_amdgcn_readlane(r, 0) + __builtin_amdgcn_readlane(r, 16) +
+                  __builtin_amdgcn_readlane(r, 32) + __builtin_amdgcn_readlane(r, 48);
+    if (lane == 0) scratch[wave * N + i] = t;
+  }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < N; ++i) {
-    int t = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) t += scratch[w * N + i];
-    v[i] = t;
-  }
+  for (int i = 0; i < N; ++i) v[i] = __builtin_amdgcn_readlane(row_sum(lane < kWaves ? scratch[lane * N + i] : 0), 0);
 }
 
 // Exclusive prefix sum over the block in thread order; *total gets the sum.
@@ -129,66 +155,28 @@ __device__ __forceinline__ int block_scan(int v, int32_t* scratch, int* total) {
   return before + incl - v;
 }
 
-// Ranks within up to kRankGroup 1024-slot chunks at once: for the category
-// cat[c] (0..3, or -1 for an empty slot) of this thread's slot in chunk c,
-// within[c] = number of lower threads of the block with the same category in
-// that chunk, and tot[c][k] = chunk c's count of category k. One barrier;
-// the count table alternates between two buffers, so a buffer is rewritten
-// only after every thread has passed the next group's barrier. After the
-// barrier lane w * 4 + k of every wave holds wave w's count of category k,
-// and a shuffle scan with stride 4 gives the prefix over waves.
-static_assert(kWaves * 4 == 64, "one lane per (wave, category)");
-__device__ __forceinline__ void rank_group(const int (&cat)[kRankGroup], int chunks,
-                                           int32_t (*wcount)[kWaves][4], int (&within)[kRankGroup],
-                                           int (&tot)[kRankGroup][4]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t lt = (1ull << lane) - 1ull;
-  int mine[kRankGroup];
-#pragma unroll
-  for (int c = 0; c < kRankGroup; ++c) {
-    mine[c] = 0;
-    if (c < chunks)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint64_t m = __ballot(cat[c] == k);
-        if (cat[c] == k) mine[c] = __popcll(m & lt);
-        if (lane == 0) wcount[c][wave][k] = __popcll(m);
-      }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int c = 0; c < kRankGroup; ++c) {
-    within[c] = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) tot[c][k] = 0;
-    if (c < chunks) {
-      const int v = (&wcount[c][0][0])[lane];
-      int incl = v;
-#pragma unroll
-      for (int d = 4; d < 64; d <<= 1) {
-        const int o = __shfl_up(incl, d);
-        if (lane >= d) incl += o;
-      }
-      within[c] = __shfl(incl - v, wave * 4 + (cat[c] < 0 ? 0 : cat[c])) + mine[c];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) tot[c][k] = __shfl(incl, 60 + k);
-    }
-  }
-}
-
 // Victims and the new lru (phase 5): the lru (staged in lru16) stably
 // partitioned into unprotected slots U and protected slots Pr, each in lru
 // order; victims[rank] = the rank-th slot of U ++ Pr for rank < vlimit. The
 // new lru is U[m:] ++ U[:m] ++ Pr[e:] ++ Pr[:e] with m = min(inserted, |U|)
 // and e = inserted - m, inserted = min(n_miss, H) (more misses than hot rows
-// reuse the last victim, so at most H slots are inserted). Ranks come from
-// rank_group over kRankGroup 1024-slot chunks per barrier. Ends without a
+// reuse the last victim, so at most H slots are inserted).
+// The lru is walked in 1024-slot chunks, kRankGroup chunks per barrier. A
+// slot's rank among the unprotected slots of its chunk is its lane's rank in
+// the wave's ballot plus the unprotected counts of the lower waves: lane w
+// (< kWaves) of every wave reads wave w's count (ucount, double-buffered, so
+// a buffer is rewritten only after every thread has passed the next group's
+// barrier) and a DPP scan over those 16 lanes gives the prefixes. Valid
+// slots are a prefix of the threads, so a protected slot's rank is its
+// thread index minus the unprotected slots below it. Ends without a
 // barrier: callers synchronise before reading victims.
+static_assert(kWaves == 16, "one row of 16 lanes holds the wave counts");
 template <typename V>
 __device__ __forceinline__ void partition_lru(const uint16_t* lru16, const uint32_t* prot, int H, int n_prot,
-                                              int n_miss, int vlimit, V* victims, int64_t* lru_out,
-                                              int32_t (*wcount)[kRankGroup][kWaves][4]) {
+                                              int n_miss, int vlimit, V* victims, NHS_GLOBAL int64_t* lru_out,
+                                              int32_t (*ucount)[kRankGroup][kWaves]) {
   const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int n_unprot = H - n_prot;
   const int inserted = n_miss < H ? n_miss : H;
   const int m_u = inserted < n_unprot ? inserted : n_unprot;
@@ -198,34 +186,55 @@ __device__ __forceinline__ void partition_lru(const uint16_t* lru16, const uint3
   int base_u = 0, base_p = 0, parity = 0;
   for (int g0 = 0; g0 < n_chunks; g0 += kRankGroup, parity ^= 1) {
     const int chunks = min(kRankGroup, n_chunks - g0);
-    int cat[kRankGroup], vv[kRankGroup], within[kRankGroup], tot[kRankGroup][4];
+    int vv[kRankGroup], below[kRankGroup];
+    bool valid[kRankGroup], unprot[kRankGroup];
 #pragma unroll
     for (int c = 0; c < kRankGroup; ++c) {
-      const int r = (g0 + c) * kResolveThreads + tid;
-      vv[c] = r < H ? lru16[r] : 0;
-      cat[c] = r < H ? prot_bit(vv[c]) : -1;  // 0 unprotected, 1 protected
-    }
-    rank_group(cat, chunks, wcount[parity], within, tot);
-#pragma unroll
-    for (int c = 0; c < kRankGroup; ++c) {
-      if (c < chunks && cat[c] >= 0) {
-        int rank, pos;
-        if (cat[c] == 0) {
-          const int u = base_u + within[c];
-          rank = u;
-          pos = u >= m_u ? u - m_u : n_unprot - m_u + u;
-        } else {
-          const int pr = base_p + within[c];
-          rank = n_unprot + pr;
-          pos = n_unprot + (pr >= e_p ? pr - e_p : n_prot - e_p + pr);
-        }
-        if (rank < vlimit) victims[rank] = (V)vv[c];
-        // pos < H for a permutation; the check keeps a corrupt lru (clamped
-        // duplicates, so the protected count and the ranks disagree) in bounds
-        if (pos < H) lru_out[pos] = vv[c];
+      valid[c] = unprot[c] = false;
+      vv[c] = below[c] = 0;
+      if (c < chunks) {
+        const int r = (g0 + c) * kResolveThreads + tid;
+        valid[c] = r < H;
+        vv[c] = valid[c] ? lru16[r] : 0;
+        unprot[c] = valid[c] && !prot_bit(vv[c]);
+        const uint64_t m = __ballot(unprot[c]);
+        below[c] = lanes_below(m);
+        if (lane == 0) ucount[parity][c][wave] = __popcll(m);
       }
-      base_u += tot[c][0];
-      base_p += tot[c][1];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < kRankGroup; ++c) {
+      if (c < chunks) {
+        // inclusive scan of the wave counts over lanes 0..15 (row_shr 1, 2, 4, 8)
+        int x = lane < kWaves ? ucount[parity][c][lane] : 0;
+        x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);
+        x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);
+        x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);
+        x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);
+        const int total_u = __builtin_amdgcn_readlane(x, kWaves - 1);
+        const int waves_below = wave > 0 ? __builtin_amdgcn_readlane(x, wave - 1) : 0;
+        const int n_valid = min(kResolveThreads, H - (g0 + c) * kResolveThreads);
+        if (valid[c]) {
+          const int within_u = waves_below + below[c];
+          int rank, pos;
+          if (unprot[c]) {
+            const int u = base_u + within_u;
+            rank = u;
+            pos = u >= m_u ? u - m_u : n_unprot - m_u + u;
+          } else {
+            const int pr = base_p + tid - within_u;
+            rank = n_unprot + pr;
+            pos = n_unprot + (pr >= e_p ? pr - e_p : n_prot - e_p + pr);
+          }
+          if (rank < vlimit) victims[rank] = (V)vv[c];
+          // pos < H for a permutation; the check keeps a corrupt lru (clamped
+          // duplicates, so the protected count and the ranks disagree) in bounds
+          if (pos >= 0 && pos < H) lru_out[pos] = vv[c];
+        }
+        base_u += total_u;
+        base_p += n_valid - total_u;
+      }
     }
   }
 }
@@ -256,6 +265,12 @@ __device__ __forceinline__ int hash_find(const int32_t* hkey, int32_t key) {
   }
 }
 
+// KPL = 0: the positions are read from a.positions. KPL = 8 or 16: wave 0
+// first selects the top_pages best of the request's page scores
+// (wave_select over up to kWave * KPL pages, as the selectors do) and the
+// positions are the chosen pages expanded to tokens, written to pages_out
+// and positions_out as the selectors write them; they come out sorted.
+template <int KPL>
 __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveArgs a) {
   __shared__ ResolveShared sh;
   const int tid = threadIdx.x;
@@ -266,20 +281,24 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   const int64_t length = a.lengths ? a.lengths[b] : a.length;
   int kp = 1;
   while (kp < n) kp <<= 1;
+  // fused selection: wave 0's score loads go first
+  float sv[KPL > 0 ? KPL : 1];
+  if constexpr (KPL > 0)
+    if (tid < kWave) wave_scores<KPL>(a.scores + (int64_t)b * a.max_pages, a.max_pages, sv);
 
   // This item's tables: from its entry in the item table, or strided.
   const nhs_layer_item* item = a.items ? a.items + b : nullptr;
-  const int32_t* source = item ? item->source : a.source + (int64_t)b * a.page_stride;
-  const int32_t* resident = item ? item->resident : a.resident + (int64_t)b * a.page_stride;
+  NHS_GLOBAL const int32_t* source = to_global(item ? item->source : a.source + (int64_t)b * a.page_stride);
+  NHS_GLOBAL const int32_t* resident = to_global(item ? item->resident : a.resident + (int64_t)b * a.page_stride);
   const int n_pages = item ? (int)item->n_pages : a.n_pages;
-  int32_t* const tags = item ? item->tags : a.tags + (int64_t)b * a.tags_stride;
-  int64_t* const lru_out = item ? item->lru : a.lru + (int64_t)b * a.lru_stride;
+  NHS_GLOBAL int32_t* const tags = to_global(item ? item->tags : a.tags + (int64_t)b * a.tags_stride);
+  NHS_GLOBAL int64_t* const lru_out = to_global(item ? item->lru : a.lru + (int64_t)b * a.lru_stride);
 
   // Loads that depend on nothing are issued first: the tags and lru of the
   // first kRegH * kResolveThreads hot rows (registers) and the hot block
   // table (LDS), so their latency overlaps the position lookups below.
-  const int32_t* tags_in = tags;
-  const int64_t* lru_in = lru_out;
+  NHS_GLOBAL const int32_t* tags_in = tags;
+  NHS_GLOBAL const int64_t* lru_in = lru_out;
   int32_t tag_r[kRegH];
   int64_t lru_r[kRegH];
 #pragma unroll
@@ -290,26 +309,51 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   }
   const int hot_blocks = (H + P - 1) / P;
   const bool hot_cached = hot_blocks <= kHotCache;
-  const int32_t* hot = item ? item->hot : a.hot + (int64_t)b * a.hot_stride;
+  NHS_GLOBAL const int32_t* hot = to_global(item ? item->hot : a.hot + (int64_t)b * a.hot_stride);
+  // Tables staged in LDS: the hot block table and, when they fit, the page
+  // tables, so the lookups below wait for no second global load. With the
+  // fused selection, wave 0 stages nothing: its LDS writes would wait for
+  // these loads before it could rank the scores.
+  const int stager = KPL > 0 ? (int)tid - kWave : (int)tid;
+  const int stagers = KPL > 0 ? kResolveThreads - kWave : kResolveThreads;
   if (hot_cached)
-    for (int i = tid; i < hot_blocks; i += kResolveThreads) sh.hot[i] = hot[i];
+    for (int i = stager; i >= 0 && i < hot_blocks; i += stagers) sh.hot[i] = hot[i];
+  const bool staged = n_pages >= 1 && n_pages <= kTableCache;
+  if (staged)
+    for (int i = stager; i >= 0 && i < n_pages; i += stagers) {
+      sh.u.e.src[i] = source[i];
+      sh.u.e.res[i] = resident[i];
+    }
+
+  // ---- 0. fused selection --------------------------------------------------
+  if constexpr (KPL > 0) {
+    const int count = page_count(a.lengths, a.length, b, P, a.max_pages);
+    if (tid < kWave) wave_rank<KPL>(sv, count, a.top_pages, a.mode, a.keep_sink, a.forced_key, sh.u.e.chosen);
+    __syncthreads();
+    for (int i = tid; i < a.top_pages; i += kResolveThreads) a.pages_out[(int64_t)b * a.top_pages + i] = sh.u.e.chosen[i];
+  }
 
   // ---- 1. keys; sorted unless a pair is inverted ---------------------------
   // A thread owns the contiguous run j0 .. j0 + per - 1 of sorted entries.
   // Selector output is already in order (ascending positions, -1 padding at
   // the end maps to `length`), so the page table lookups for the entries in
-  // input order are issued right away and kept when no pair is inverted.
+  // input order are issued right away (after the barrier, from LDS, when the
+  // tables are staged) and kept when no pair is inverted. The fused
+  // selection's positions are in order by construction: pages ascending,
+  // and only the last page (count - 1, the highest chosen) or the padding
+  // pages hold positions at or past the length.
   const int per = (n + kResolveThreads - 1) / kResolveThreads;  // <= kKPerThread
   const int j0 = tid * per;
   uint64_t key[kKPerThread];
   int64_t src[kKPerThread], res[kKPerThread];
   auto lookup = [&](int q) {
+    if (n_pages < 1) return;  // no pages: every entry stays unset (-1)
     const int64_t lg = (int64_t)(key[q] >> 32);
     // Positions are < 2^31 (int32 host tags); page = min(lg / P, n_pages - 1).
     const uint32_t pg = a.page_div.div((uint32_t)lg);
-    const int64_t page = pg < (uint32_t)(n_pages - 1) ? (int64_t)pg : (int64_t)(n_pages - 1);
-    src[q] = source[page];
-    res[q] = resident[page];
+    const int page = pg < (uint32_t)(n_pages - 1) ? (int)pg : n_pages - 1;
+    src[q] = staged ? sh.u.e.src[page] : source[page];
+    res[q] = staged ? sh.u.e.res[page] : resident[page];
   };
 #pragma unroll
   for (int q = 0; q < kKPerThread; ++q) {
@@ -317,31 +361,47 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     key[q] = ~0ull;
     src[q] = res[q] = -1;
     if (q < per && j < n) {
-      const int64_t raw = a.positions_i64
-                              ? static_cast<const int64_t*>(a.positions)[(int64_t)b * a.positions_stride + j]
+      int64_t raw;
+      if constexpr (KPL > 0) {
+        const uint32_t jp = a.page_div.div((uint32_t)j);
+        const int32_t p = sh.u.e.chosen[jp];
+        const int64_t t = (int64_t)p * P + (int64_t)((uint32_t)j - jp * (uint32_t)P);
+        raw = (p >= 0 && t < length) ? t : -1;
+        a.positions_out[(int64_t)b * n + j] = (int32_t)raw;
+      } else {
+        raw = a.positions_i64 ? static_cast<const int64_t*>(a.positions)[(int64_t)b * a.positions_stride + j]
                               : (int64_t) static_cast<const int32_t*>(a.positions)[(int64_t)b * a.positions_stride + j];
+      }
       const int64_t norm = (raw >= 0 && raw < length) ? raw : length;
       key[q] = ((uint64_t)norm << 32) | (uint32_t)j;
-      sh.u.keys[j] = key[q];
-      lookup(q);
+      sh.u.e.keys[j] = key[q];
+      if (!staged) lookup(q);
     }
   }
-  for (int i = n + tid; i < kp; i += kResolveThreads) sh.u.keys[i] = ~0ull;  // sort padding
+  for (int i = n + tid; i < kp; i += kResolveThreads) sh.u.e.keys[i] = ~0ull;  // sort padding
   __syncthreads();
-  int inverted = 0;
-  for (int i = tid; i + 1 < n; i += kResolveThreads) inverted |= sh.u.keys[i] > sh.u.keys[i + 1];
-  const bool sorted = !__syncthreads_or(inverted);
+  bool sorted = true;
+  if constexpr (KPL == 0) {
+    int inverted = 0;
+    for (int i = tid; i + 1 < n; i += kResolveThreads) inverted |= sh.u.e.keys[i] > sh.u.e.keys[i + 1];
+    sorted = !__syncthreads_or(inverted);
+  }
+  if (sorted && staged) {
+#pragma unroll
+    for (int q = 0; q < kKPerThread; ++q)
+      if (q < per && j0 + q < n) lookup(q);
+  }
   if (!sorted) {
     for (int k = 2; k <= kp; k <<= 1) {
       for (int j = k >> 1; j > 0; j >>= 1) {
         for (int i = tid; i < kp; i += kResolveThreads) {
           int ixj = i ^ j;
           if (ixj > i) {
-            uint64_t x = sh.u.keys[i], y = sh.u.keys[ixj];
+            uint64_t x = sh.u.e.keys[i], y = sh.u.e.keys[ixj];
             bool up = (i & k) == 0;
             if ((x > y) == up) {
-              sh.u.keys[i] = y;
-              sh.u.keys[ixj] = x;
+              sh.u.e.keys[i] = y;
+              sh.u.e.keys[ixj] = x;
             }
           }
         }
@@ -352,7 +412,7 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     for (int q = 0; q < kKPerThread; ++q) {
       const int j = j0 + q;
       if (q < per && j < n) {
-        key[q] = sh.u.keys[j];
+        key[q] = sh.u.e.keys[j];
         lookup(q);
       }
     }
@@ -373,7 +433,7 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
     if (q < per && j < n) {
       int64_t lg = (int64_t)(key[q] >> 32);
       in_idx[q] = (int32_t)(key[q] & 0xffffffffu);
-      run_start[q] = j == 0 || (int64_t)(sh.u.keys[j - 1] >> 32) != lg;
+      run_start[q] = j == 0 || (int64_t)(sh.u.e.keys[j - 1] >> 32) != lg;
       bool unique = lg < length && run_start[q];
       uint32_t pg = a.page_div.div((uint32_t)lg);
       int32_t o = (int32_t)((uint32_t)lg - pg * (uint32_t)P);
@@ -540,7 +600,7 @@ struct LargeShared {
   uint16_t victims[kMaxH];
   uint32_t prot[kMaxH / 32];
   int32_t red[4][kWaves * 8];
-  int32_t wcount[2][kRankGroup][kWaves][4];
+  int32_t wcount[2][kRankGroup][kWaves];
   int32_t hot[kHotCache];
 };
 
@@ -557,12 +617,12 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_large_kernel(ResolveA
   const int64_t length = a.lengths ? a.lengths[b] : a.length;
 
   const nhs_layer_item* item = a.items ? a.items + b : nullptr;
-  const int32_t* source = item ? item->source : a.source + (int64_t)b * a.page_stride;
-  const int32_t* resident = item ? item->resident : a.resident + (int64_t)b * a.page_stride;
+  NHS_GLOBAL const int32_t* source = to_global(item ? item->source : a.source + (int64_t)b * a.page_stride);
+  NHS_GLOBAL const int32_t* resident = to_global(item ? item->resident : a.resident + (int64_t)b * a.page_stride);
   const int n_pages = item ? (int)item->n_pages : a.n_pages;
-  int32_t* const tags = item ? item->tags : a.tags + (int64_t)b * a.tags_stride;
-  int64_t* const lru_out = item ? item->lru : a.lru + (int64_t)b * a.lru_stride;
-  const int32_t* hot = item ? item->hot : a.hot + (int64_t)b * a.hot_stride;
+  NHS_GLOBAL int32_t* const tags = to_global(item ? item->tags : a.tags + (int64_t)b * a.tags_stride);
+  NHS_GLOBAL int64_t* const lru_out = to_global(item ? item->lru : a.lru + (int64_t)b * a.lru_stride);
+  NHS_GLOBAL const int32_t* hot = to_global(item ? item->hot : a.hot + (int64_t)b * a.hot_stride);
   const int hot_blocks = (H + P - 1) / P;
   const bool hot_cached = hot_blocks <= kHotCache;
   if (hot_cached)
@@ -836,7 +896,7 @@ extern "C" int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions,
   a.tags_stride = tags_stride;
   a.lru = lru;
   a.lru_stride = lru_stride;
-  launch(n <= kMaxK ? resolve_rows_kernel : resolve_large_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0,
+  launch(n <= kMaxK ? resolve_rows_kernel<0> : resolve_large_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0,
          (hipStream_t)stream, ev.start, ev.stop, a);
   return launch_status(who);
 }
@@ -858,7 +918,101 @@ extern "C" int nhs_resolve_items(int32_t batch, int32_t n, const void* positions
   fill_common(a, n, positions, positions_i64, positions_stride, hot_rows, lengths, 0, page_size, physical, miss_host,
               miss_device, plan_stride, counts, counts_total);
   a.items = items;
-  launch(n <= kMaxK ? resolve_rows_kernel : resolve_large_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0,
+  launch(n <= kMaxK ? resolve_rows_kernel<0> : resolve_large_kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0,
          (hipStream_t)stream, ev.start, ev.stop, a);
   return launch_status(who);
+}
+
+// ---- fused selection + resolution ------------------------------------------
+
+namespace nhs {
+
+// The fused launch: resolve_rows_kernel<8 or 16> over `batch` items whose
+// positions are their selections. Rejects shapes beyond one wave's
+// selection or the LDS-held entries with NHS_ERR_UNSUPPORTED, so that a
+// caller can fall back to a selector launch and a resolver launch.
+static int launch_select_resolve(const char* who, ResolveArgs& a, int32_t batch, const float* scores,
+                                 int32_t max_pages, int32_t mode, int32_t top_pages, int32_t keep_sink,
+                                 int32_t* pages, int32_t* positions, hipStream_t stream, const LaunchEvents& ev) {
+  if (!scores || !pages || !positions) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
+  if (mode != kModeQuest && mode != kModeMean) return fail(NHS_ERR_INVALID, "%s: mode is 0 (Quest) or 1 (mean)", who);
+  if (max_pages < 1 || top_pages < 1) return fail(NHS_ERR_INVALID, "%s: need max_pages, top_pages >= 1", who);
+  const int wave_pages = max_pages > top_pages ? max_pages : top_pages;
+  if (wave_pages > kFusedMaxPages || (int64_t)top_pages * a.page_size > kMaxK)
+    return fail(NHS_ERR_UNSUPPORTED, "%s: max(max_pages, top_pages) <= %d and top_pages * page_size <= %d required",
+                who, kFusedMaxPages, kMaxK);
+  a.scores = scores;
+  a.max_pages = max_pages;
+  a.top_pages = top_pages;
+  a.keep_sink = keep_sink;
+  a.mode = mode;
+  a.forced_key = mode == kModeQuest ? kForcedQuest : kRequiredMean;
+  a.pages_out = pages;
+  a.positions_out = positions;
+  if (batch == 0) return NHS_OK;
+  launch(wave_pages <= kWave * 8 ? resolve_rows_kernel<8> : resolve_rows_kernel<16>, dim3((unsigned)batch),
+         dim3(kResolveThreads), 0, stream, ev.start, ev.stop, a);
+  return launch_status(who);
+}
+
+}  // namespace nhs
+
+extern "C" int nhs_select_resolve_rows(int32_t batch, const float* scores, int32_t max_pages, int32_t mode,
+                                       int32_t top_pages, int32_t keep_sink, const int32_t* source,
+                                       const int32_t* resident, int64_t page_table_stride, int32_t n_pages,
+                                       const int32_t* hot, int64_t hot_stride, int32_t* tags, int64_t tags_stride,
+                                       int64_t* lru, int64_t lru_stride, int32_t hot_rows, const int64_t* lengths,
+                                       int64_t length, int32_t page_size, int32_t* pages, int32_t* positions,
+                                       int64_t* physical, int64_t* miss_host, int64_t* miss_device,
+                                       int64_t plan_stride, int64_t* counts, int64_t* counts_total, void* stream) {
+  using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
+  const char* who = "nhs_select_resolve_rows";
+  if (top_pages < 1 || page_size < 1 || (int64_t)top_pages * page_size > kLargeMaxK)
+    return fail(NHS_ERR_INVALID, "%s: need top_pages, page_size >= 1", who);
+  const int32_t n = top_pages * page_size;
+  int st = check_resolve(who, batch, n, scores, hot_rows, lengths, length, page_size, physical, miss_host,
+                         miss_device, plan_stride, counts);
+  if (st != NHS_OK) return st;
+  if (!source || !resident || !hot || !tags || !lru) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
+  if (n_pages < 1) return fail(NHS_ERR_INVALID, "%s: need n, n_pages, hot_rows, page_size >= 1", who);
+  ResolveArgs a;
+  fill_common(a, n, nullptr, 0, 0, hot_rows, lengths, length, page_size, physical, miss_host, miss_device,
+              plan_stride, counts, counts_total);
+  a.source = source;
+  a.resident = resident;
+  a.page_stride = page_table_stride;
+  a.n_pages = n_pages;
+  a.hot = hot;
+  a.hot_stride = hot_stride;
+  a.tags = tags;
+  a.tags_stride = tags_stride;
+  a.lru = lru;
+  a.lru_stride = lru_stride;
+  return launch_select_resolve(who, a, batch, scores, max_pages, mode, top_pages, keep_sink, pages, positions,
+                               (hipStream_t)stream, ev);
+}
+
+extern "C" int nhs_select_resolve_items(int32_t batch, const float* scores, int32_t max_pages, int32_t mode,
+                                        int32_t top_pages, int32_t keep_sink, const nhs_layer_item* items,
+                                        int32_t hot_rows, const int64_t* lengths, int32_t page_size, int32_t* pages,
+                                        int32_t* positions, int64_t* physical, int64_t* miss_host,
+                                        int64_t* miss_device, int64_t plan_stride, int64_t* counts,
+                                        int64_t* counts_total, void* stream) {
+  using namespace nhs;
+  const LaunchEvents ev = take_launch_events();
+  const char* who = "nhs_select_resolve_items";
+  if (top_pages < 1 || page_size < 1 || (int64_t)top_pages * page_size > kLargeMaxK)
+    return fail(NHS_ERR_INVALID, "%s: need top_pages, page_size >= 1", who);
+  const int32_t n = top_pages * page_size;
+  int st = check_resolve(who, batch, n, scores, hot_rows, lengths, 0, page_size, physical, miss_host, miss_device,
+                         plan_stride, counts);
+  if (st != NHS_OK) return st;
+  if (!items || !lengths) return fail(NHS_ERR_INVALID, "%s: null items or lengths", who);
+  ResolveArgs a;
+  fill_common(a, n, nullptr, 0, 0, hot_rows, lengths, 0, page_size, physical, miss_host, miss_device, plan_stride,
+              counts, counts_total);
+  a.items = items;
+  return launch_select_resolve(who, a, batch, scores, max_pages, mode, top_pages, keep_sink, pages, positions,
+                               (hipStream_t)stream, ev);
 }

@@ -19,7 +19,7 @@
 // expanded to token positions.
 #include <math.h>
 
-#include "nhs_common.h"
+#include "select_common.h"
 
 #pragma clang fp contract(off)
 
@@ -36,8 +36,6 @@ constexpr int kSelectWaveThreads = 256;  // one-wave selection; 4 waves expand t
 // head, d)) and KV-head sums fit the 160 KiB of LDS a workgroup may use.
 constexpr size_t kMaxQuestLds = 160 * 1024;
 constexpr int kMaxQuestFold = 16384;  // kv_heads * head_dim, for the message
-
-enum { kModeQuest = 0, kModeMean = 1 };
 
 struct ScoreArgs {
   const void* q;
@@ -69,13 +67,6 @@ __device__ __forceinline__ void bounds_of(const ScoreArgs& a, int b, const char*
     lo = static_cast<const char*>(a.lo) + (int64_t)b * a.b_bs * T::bytes;
     hi = static_cast<const char*>(a.hi) + (int64_t)b * a.b_bs * T::bytes;
   }
-}
-
-__device__ __forceinline__ int page_count(const int64_t* lengths, int64_t length, int b, int page_size, int max_pages) {
-  int64_t len = lengths ? lengths[b] : length;
-  if (len <= 0) return 0;
-  int64_t c = (len + page_size - 1) / page_size;
-  return (int)(c < max_pages ? c : max_pages);
 }
 
 // Quest bounds score: (sum_h sum_d torch.maximum(q*lo, q*hi)) / q_heads.
@@ -394,11 +385,12 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
     for (int s = 0; s < S; ++s) {
       const int p = wave_first + s * ppw + page_local;
       const int pc = p < count ? p : wave_first;  // lanes past the end reread a live page
-      const uint4* lp = reinterpret_cast<const uint4*>(lo + ((int64_t)pc * page_elems + lane_off) * T::bytes);
-      const uint4* hp = reinterpret_cast<const uint4*>(hi + ((int64_t)pc * page_elems + lane_off) * T::bytes);
+      const int64_t at = ((int64_t)pc * page_elems + lane_off) * T::bytes;
+      NHS_GLOBAL const u32x4_t* lp = to_global(reinterpret_cast<const u32x4_t*>(lo + at));
+      NHS_GLOBAL const u32x4_t* hp = to_global(reinterpret_cast<const u32x4_t*>(hi + at));
 #pragma unroll
       for (int v = 0; v < W / 4; ++v) {
-        const uint4 x = lp[v], y = hp[v];
+        const u32x4_t x = lp[v], y = hp[v];
         mn[s][4 * v] = x.x, mn[s][4 * v + 1] = x.y, mn[s][4 * v + 2] = x.z, mn[s][4 * v + 3] = x.w;
         mx[s][4 * v] = y.x, mx[s][4 * v + 1] = y.y, mx[s][4 * v + 2] = y.z, mx[s][4 * v + 3] = y.w;
       }
@@ -536,23 +528,6 @@ __global__ __launch_bounds__(kScoreThreads) void mean_score_kernel(ScoreArgs a) 
   }
 }
 
-// Keys in descending rank order. Numbers map to 0x007fffff .. 0xff800000
-// (+inf); NaN ranks above every number, as in torch.topk. Quest's forced
-// pages are +inf in the reference (selection.py:86-89), so NaN pages outrank
-// them: they take kForcedQuest, just below NaN. The mean selector adds its
-// required pages outside the top-k (selection.py:138-145): kRequiredMean,
-// above NaN.
-constexpr uint32_t kKeyNaN = 0xfffffffeu;
-constexpr uint32_t kForcedQuest = 0xfffffffdu;
-constexpr uint32_t kRequiredMean = 0xffffffffu;
-
-__device__ __forceinline__ uint32_t order_key(float s) {
-  if (s != s) return kKeyNaN;
-  uint32_t u = __float_as_uint(s);
-  if (u == 0x80000000u) u = 0u;  // -0.0 ties with +0.0
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 struct SelectArgs {
   const float* scores;
   const int64_t* lengths;
@@ -680,19 +655,8 @@ __global__ __launch_bounds__(THREADS) void select_topk_kernel(SelectArgs a) {
   }
 }
 
-// Up to kWave * KPL pages: the selection runs in one wave, with no LDS and no
-// barrier until the output. Page q * kWave + lane sits in slot q of that lane.
-// The key of the k-th best page, the largest x with at least top_pages keys
-// >= x, is found bit by bit, most significant first: at each bit the wave
-// counts the keys >= the prefix found so far with that bit set (a compare, a
-// ballot and a popcount per slot) and keeps the bit when the count reaches
-// top_pages. Every key above it is taken, ties at it go to the lowest pages,
-// and the chosen pages come out in ascending order (ranks from mbcnt). The
-// other waves join for the page -> token expansion.
-__device__ __forceinline__ int lanes_below(uint64_t mask) {
-  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
-
+// Up to kWave * KPL pages: wave 0 selects (wave_select), then the four waves
+// expand the chosen pages to token positions.
 template <int KPL>
 __global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectArgs a) {
   __shared__ int32_t chosen[kWave * KPL];
@@ -700,63 +664,9 @@ __global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectA
   const int b = blockIdx.x;
   const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
   const int64_t len = a.lengths ? a.lengths[b] : a.length;
-  if (tid < kWave) {
-    const int lane = tid;
-    // the score loads are issued before the page count arrives (pages past
-    // max_pages read page 0; values past count are never used, and none are
-    // when every page is kept)
-    const float* sc = a.scores + (int64_t)b * a.max_pages;
-    float sv[KPL];
-#pragma unroll
-    for (int q = 0; q < KPL; ++q) sv[q] = sc[q * kWave + lane < a.max_pages ? q * kWave + lane : 0];
-    bool sel[KPL];
-#pragma unroll
-    for (int q = 0; q < KPL; ++q) sel[q] = q * kWave + lane < count;
-    if (a.top_pages < count) {
-      const bool second = a.mode == kModeQuest ? (a.keep_sink && a.top_pages > 1 && count > 1) : a.top_pages > 1;
-      // pages past count keep key 0, below every score's key (>= 0x007fffff),
-      // so no prefix tested below (it always has a bit set) matches them
-      uint32_t key[KPL];
-#pragma unroll
-      for (int q = 0; q < KPL; ++q) {
-        const int p = q * kWave + lane;
-        key[q] = p >= count ? 0u : (p == count - 1 || (second && p == 0)) ? a.forced_key : order_key(sv[q]);
-      }
-      // prefix = the largest key x with at least top_pages keys >= x, i.e.
-      // the key of the k-th best page
-      uint32_t prefix = 0u;
-#pragma unroll
-      for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t cand = prefix | (1u << bit);
-        int c = 0;
-#pragma unroll
-        for (int q = 0; q < KPL; ++q) c += __popcll(__ballot(key[q] >= cand));
-        if (c >= a.top_pages) prefix = cand;
-      }
-      int above = 0;
-#pragma unroll
-      for (int q = 0; q < KPL; ++q) above += __popcll(__ballot(key[q] > prefix));
-      // every page above that key is taken, then the first `need` pages with
-      // that key in page order (slot, then lane)
-      const int need = a.top_pages - above;
-      int before = 0;
-#pragma unroll
-      for (int q = 0; q < KPL; ++q) {
-        const bool tie = key[q] == prefix;
-        const uint64_t m = __ballot(tie);
-        sel[q] = key[q] > prefix || (tie && before + lanes_below(m) < need);
-        before += __popcll(m);
-      }
-    }
-    int n_sel = 0;
-#pragma unroll
-    for (int q = 0; q < KPL; ++q) {
-      const uint64_t m = __ballot(sel[q]);
-      if (sel[q]) chosen[n_sel + lanes_below(m)] = q * kWave + lane;
-      n_sel += __popcll(m);
-    }
-    for (int i = n_sel + lane; i < a.top_pages; i += kWave) chosen[i] = -1;
-  }
+  if (tid < kWave)
+    wave_select<KPL>(a.scores + (int64_t)b * a.max_pages, a.max_pages, count, a.top_pages, a.mode, a.keep_sink,
+                     a.forced_key, chosen);
   __syncthreads();
   int32_t* pages = a.pages + (int64_t)b * a.top_pages;
   for (int i = tid; i < a.top_pages; i += kSelectWaveThreads) pages[i] = chosen[i];
@@ -890,7 +800,8 @@ static int check_select_common(const char* who, int32_t batch, const void* query
                                int32_t kv_heads, int32_t head_dim, const int64_t* lengths, int64_t length,
                                int32_t page_size, int32_t max_pages, int32_t top_pages, float* scores,
                                int32_t* pages, int32_t* positions) {
-  if (!query || !scores || !pages || !positions) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
+  if (!query || !scores) return fail(NHS_ERR_INVALID, "%s: null pointer", who);
+  if (!pages != !positions) return fail(NHS_ERR_INVALID, "%s: pages and positions are both given or both null", who);
   if (!valid_dtype(q_dtype)) return fail(NHS_ERR_INVALID, "%s: bad query dtype", who);
   if (batch < 0 || q_heads < 1 || kv_heads < 1 || head_dim < 1 || page_size < 1 || max_pages < 1 ||
       top_pages < 1 || q_heads % kv_heads)
@@ -1048,11 +959,12 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
   }
   if (top_pages < max_pages) {  // scores are not needed when every page is kept
     if (!kernel) return fail(NHS_ERR_UNSUPPORTED, "%s: no scoring kernel", who);
-    launch(kernel, grid, block, lds, s, ev.start, nullptr, a);
+    launch(kernel, grid, block, lds, s, ev.start, pages ? nullptr : ev.stop, a);
     ev.start = nullptr;  // the start event belongs to the first kernel
     st = launch_status(who);
     if (st != NHS_OK) return st;
   }
+  if (!pages) return NHS_OK;  // scores only
   SelectArgs sa;
   sa.scores = scores;
   sa.lengths = lengths;
@@ -1135,16 +1047,18 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
   dim3 grid((unsigned)((max_pages + kPagesPerBlock - 1) / kPagesPerBlock), (unsigned)batch);
   size_t lds = ((size_t)kv_heads * head_dim + (size_t)kScoreWaves * kv_heads) * sizeof(float);
   if (top_pages < max_pages) {
+    hipEvent_t stop = pages ? nullptr : ev.stop;
     if (vec)
-      launch(mean_score_kernel<4>, grid, dim3(kScoreThreads), lds, s, ev.start, nullptr, a);
+      launch(mean_score_kernel<4>, grid, dim3(kScoreThreads), lds, s, ev.start, stop, a);
     else if (E == 1)
-      launch(mean_score_kernel<1>, grid, dim3(kScoreThreads), lds, s, ev.start, nullptr, a);
+      launch(mean_score_kernel<1>, grid, dim3(kScoreThreads), lds, s, ev.start, stop, a);
     else
-      launch(mean_score_kernel<0>, grid, dim3(kScoreThreads), lds, s, ev.start, nullptr, a);
+      launch(mean_score_kernel<0>, grid, dim3(kScoreThreads), lds, s, ev.start, stop, a);
     ev.start = nullptr;
     st = launch_status(who);
     if (st != NHS_OK) return st;
   }
+  if (!pages) return NHS_OK;  // scores only
   SelectArgs sa;
   sa.scores = scores;
   sa.lengths = lengths;

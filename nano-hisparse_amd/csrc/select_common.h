@@ -1,0 +1,128 @@
+// Page ranking shared by the selectors (select.hip) and the fused select +
+// resolve kernel (resolve.hip): order-preserving keys of the page scores and
+// the one-wave top-k of up to kWave * KPL pages.
+#pragma once
+
+#include "nhs_common.h"
+
+namespace nhs {
+
+enum { kModeQuest = 0, kModeMean = 1 };
+
+// Keys in descending rank order. Numbers map to 0x007fffff .. 0xff800000
+// (+inf); NaN ranks above every number, as in torch.topk. Quest's forced
+// pages are +inf in the reference (selection.py:86-89), so NaN pages outrank
+// them: they take kForcedQuest, just below NaN. The mean selector adds its
+// required pages outside the top-k (selection.py:138-145): kRequiredMean,
+// above NaN.
+constexpr uint32_t kKeyNaN = 0xfffffffeu;
+constexpr uint32_t kForcedQuest = 0xfffffffdu;
+constexpr uint32_t kRequiredMean = 0xffffffffu;
+
+__device__ __forceinline__ uint32_t order_key(float s) {
+  if (s != s) return kKeyNaN;
+  uint32_t u = __float_as_uint(s);
+  if (u == 0x80000000u) u = 0u;  // -0.0 ties with +0.0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Pages of request b: ceil(length / page_size), at most max_pages.
+__device__ __forceinline__ int page_count(const int64_t* lengths, int64_t length, int b, int page_size, int max_pages) {
+  int64_t len = lengths ? lengths[b] : length;
+  if (len <= 0) return 0;
+  int64_t c = (len + page_size - 1) / page_size;
+  return (int)(c < max_pages ? c : max_pages);
+}
+
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// Top-k of up to kWave * KPL pages in one wave, with no LDS and no barrier:
+// page q * kWave + lane sits in slot q of that lane. The key of the k-th best
+// page, the largest x with at least top_pages keys >= x, is found bit by bit,
+// most significant first: at each bit the wave counts the keys >= the prefix
+// found so far with that bit set (a compare, a ballot and a popcount per
+// slot) and keeps the bit when the count reaches top_pages. Every key above
+// it is taken, ties at it go to the lowest pages, and the chosen pages come
+// out in ascending order (ranks from mbcnt), then -1 up to top_pages.
+// Called by the 64 lanes of one wave: wave_scores loads the request's scores
+// sc (pages < max(max_pages, 1); pages past max_pages read page 0, values
+// past count are never used, and none are when every page is kept), and
+// wave_rank selects from them into chosen (kWave * KPL entries). A caller
+// issues the score loads early, so that waiting for them does not also wait
+// for loads issued after them.
+template <int KPL>
+__device__ __forceinline__ void wave_scores(const float* sc, int max_pages, float (&sv)[KPL]) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int q = 0; q < KPL; ++q) sv[q] = sc[q * kWave + lane < max_pages ? q * kWave + lane : 0];
+}
+
+template <int KPL>
+__device__ __forceinline__ void wave_rank(const float (&sv)[KPL], int count, int top_pages, int mode, int keep_sink,
+                                          uint32_t forced_key, int32_t* chosen) {
+  const int lane = threadIdx.x & (kWave - 1);
+  bool sel[KPL];
+#pragma unroll
+  for (int q = 0; q < KPL; ++q) sel[q] = q * kWave + lane < count;
+  if (top_pages < count) {
+    const bool second = mode == kModeQuest ? (keep_sink && top_pages > 1 && count > 1) : top_pages > 1;
+    // pages past count keep key 0, below every score's key (>= 0x007fffff),
+    // so no prefix tested below (it always has a bit set) matches them
+    uint32_t key[KPL];
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) {
+      const int p = q * kWave + lane;
+      key[q] = p >= count ? 0u : (p == count - 1 || (second && p == 0)) ? forced_key : order_key(sv[q]);
+    }
+    // prefix = the largest key x with at least top_pages keys >= x, i.e.
+    // the key of the k-th best page
+    uint32_t prefix = 0u;
+#pragma unroll
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = prefix | (1u << bit);
+      // all KPL ballots are formed before any is counted, so the compares
+      // write separate mask registers and issue back to back
+      uint64_t m[KPL];
+#pragma unroll
+      for (int q = 0; q < KPL; ++q) m[q] = __ballot(key[q] >= cand);
+      int c = 0;
+#pragma unroll
+      for (int q = 0; q < KPL; ++q) c += __popcll(m[q]);
+      if (c >= top_pages) prefix = cand;
+    }
+    int above = 0;
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) above += __popcll(__ballot(key[q] > prefix));
+    // every page above that key is taken, then the first `need` pages with
+    // that key in page order (slot, then lane)
+    const int need = top_pages - above;
+    int before = 0;
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) {
+      const bool tie = key[q] == prefix;
+      const uint64_t m = __ballot(tie);
+      sel[q] = key[q] > prefix || (tie && before + lanes_below(m) < need);
+      before += __popcll(m);
+    }
+  }
+  int n_sel = 0;
+#pragma unroll
+  for (int q = 0; q < KPL; ++q) {
+    const uint64_t m = __ballot(sel[q]);
+    if (sel[q]) chosen[n_sel + lanes_below(m)] = q * kWave + lane;
+    n_sel += __popcll(m);
+  }
+  for (int i = n_sel + lane; i < top_pages; i += kWave) chosen[i] = -1;
+}
+
+template <int KPL>
+__device__ __forceinline__ void wave_select(const float* sc, int max_pages, int count, int top_pages, int mode,
+                                            int keep_sink, uint32_t forced_key, int32_t* chosen) {
+  float sv[KPL];
+  wave_scores<KPL>(sc, max_pages, sv);
+  wave_rank<KPL>(sv, count, top_pages, mode, keep_sink, forced_key, chosen);
+}
+
+}  // namespace nhs

@@ -65,6 +65,15 @@ SIGNATURES = {
         [_i32, _i32, _p, _i32, _i64, _p, _i32, _p, _i32, _p, _p, _p, _i64, _p, _p, _p],
         ctypes.c_int,
     ),
+    "nhs_select_resolve_rows": (
+        [_i32, _p, _i32, _i32, _i32, _i32, _p, _p, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _i32, _p, _i64, _i32,
+         _p, _p, _p, _p, _p, _i64, _p, _p, _p],
+        ctypes.c_int,
+    ),
+    "nhs_select_resolve_items": (
+        [_i32, _p, _i32, _i32, _i32, _i32, _p, _i32, _p, _i32, _p, _p, _p, _p, _p, _i64, _p, _p, _p],
+        ctypes.c_int,
+    ),
     "nhs_add_rmsnorm": ([_i32, _i32, _i32, _p, _p, _i32, _p, ctypes.c_float, _p, _p], ctypes.c_int),
     "nhs_rope": ([_i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p], ctypes.c_int),
     "nhs_silu_mul": ([_i32, _i32, _i32, _p, _p, _p], ctypes.c_int),

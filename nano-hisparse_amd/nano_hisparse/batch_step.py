@@ -131,14 +131,24 @@ class SparseDecodeBatch:
                 rk.set_launch_events(*events[name][i])
 
         with torch.cuda.stream(compute):
+            # Quest scoring, then the selection and the resolve in one launch
+            # where it fits (else the selector and the resolver separately)
+            fused = rk.fused_select_fits(t.minimum.shape[1], self.top_pages, self.page_size)
             mark("quest")
-            _, positions, _ = rk.quest_batched(
-                query, t.minimum, t.maximum, t.lengths, self.page_size, self.top_pages, self.keep_sink
+            _, positions, scores = rk.quest_batched(
+                query, t.minimum, t.maximum, t.lengths, self.page_size, self.top_pages, self.keep_sink,
+                select=not fused,
             )
             mark("resolve")
-            physical, miss_host, miss_device, counts = rk.resolve_batched(
-                positions, t.source, t.resident, t.hot, t.tags, t.lru, t.lengths, self.page_size
-            )
+            if fused:
+                _, positions, physical, miss_host, miss_device, counts = rk.select_resolve_batched(
+                    scores, t.source, t.resident, t.hot, t.tags, t.lru, t.lengths, self.page_size, self.top_pages,
+                    self.keep_sink,
+                )
+            else:
+                physical, miss_host, miss_device, counts = rk.resolve_batched(
+                    positions, t.source, t.resident, t.hot, t.tags, t.lru, t.lengths, self.page_size
+                )
             if side:
                 resolved = torch.cuda.Event()
                 resolved.record(compute)

@@ -4,9 +4,12 @@ The reference decodes request by request (engine.py:111-121, model.py:
 182-221): per layer and request an append, a Quest selection, a resolve, a
 gather and an attention. BatchDecode runs the same stages for every request
 of the batch at once on a GPU cache: per layer one append launch
-(nhs_append_items), one Quest launch (nhs_quest_select_items), one resolver
-launch (nhs_resolve_items), one gather of the concatenated miss plans on the
-transfer stream and one attention launch over all requests' rows. Each
+(nhs_append_items), one Quest scoring launch (nhs_quest_select_items,
+scores only), one launch that selects the pages and resolves their rows
+(nhs_select_resolve_items; beyond its sizes a selector launch and a
+resolver launch, nhs_resolve_items), one gather of the concatenated miss
+plans on the transfer stream and one attention launch over all requests'
+rows. Each
 request keeps its own tables; the kernels read them through a device table
 of per-(request, layer) pointers built once per batch composition.
 
@@ -229,13 +232,23 @@ class BatchDecode:
             query = query.contiguous()
         items, lengths = self.items[layer], self.dev_lengths[1]
         tables = [cache.tables[rid, layer] for rid in self.ids]
-        _, positions, _ = rk.quest_items(
-            query, items, cfg.dtype, cfg.kv_heads, lengths, cfg.page_size, self.max_pages, top_pages, keep_sink
+        # Quest scoring, then the selection and the resolve in one launch
+        # where the shape fits (else the selector and the resolver)
+        fused = rk.fused_select_fits(self.max_pages, top_pages, cfg.page_size)
+        _, positions, scores = rk.quest_items(
+            query, items, cfg.dtype, cfg.kv_heads, lengths, cfg.page_size, self.max_pages, top_pages, keep_sink,
+            select=not fused,
         )
         _wait_all(store, store.compute, (t.ready for t in tables))
-        physical, miss_host, miss_device, _ = rk.resolve_items(
-            positions, items, cache.hot_config.hot_rows, lengths, cfg.page_size, counts_total=cache.row_stats
-        )
+        hot_rows = cache.hot_config.hot_rows
+        if fused:
+            _, positions, physical, miss_host, miss_device, _ = rk.select_resolve_items(
+                scores, items, hot_rows, lengths, cfg.page_size, top_pages, keep_sink, counts_total=cache.row_stats
+            )
+        else:
+            physical, miss_host, miss_device, _ = rk.resolve_items(
+                positions, items, hot_rows, lengths, cfg.page_size, counts_total=cache.row_stats
+            )
         if not self.overlap:
             rk.gather_plan(store.host_alias, cache.pool, miss_host.view(-1), miss_device.view(-1), cfg.page_size)
             for t in tables:

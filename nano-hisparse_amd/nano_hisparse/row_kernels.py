@@ -252,6 +252,32 @@ def attend_rows(query, pool, rows, config):
 # ---- resolver ---------------------------------------------------------------------
 
 
+def _lengths_arg(lengths, device):
+    if isinstance(lengths, torch.Tensor):
+        return lengths.to(device=device, dtype=torch.int64).contiguous(), 0
+    return None, int(lengths)
+
+
+def _check_tables(B, source, resident, hot, tags, lru, page_size):
+    """Validates the strided per-item tables; returns the hot row count."""
+    for name, t, dt in (("source", source, torch.int32), ("resident", resident, torch.int32),
+                        ("hot", hot, torch.int32), ("tags", tags, torch.int32), ("lru", lru, torch.int64)):
+        if t.dtype != dt or t.ndim != 2 or t.shape[0] != B or t.stride(1) != 1:
+            raise ValueError(f"{name} must be a [B, n] {dt} tensor with unit stride")
+    if source.shape != resident.shape or source.stride(0) != resident.stride(0):
+        raise ValueError("source and resident tables must have the same shape and strides")
+    H = tags.shape[1]
+    if lru.shape[1] != H or hot.shape[1] * page_size < H:
+        raise ValueError("tags/lru/hot table sizes disagree")
+    return H
+
+
+def _plan_outputs(B, K, device):
+    physical = torch.empty(B, K, dtype=torch.int64, device=device)
+    return physical, torch.empty_like(physical), torch.empty_like(physical), torch.empty(
+        B, 3, dtype=torch.int64, device=device)
+
+
 def resolve_batched(positions, source, resident, hot, tags, lru, lengths, page_size, counts_total=None):
     """Resolve B items at once; every table has a leading batch dimension.
 
@@ -265,25 +291,9 @@ def resolve_batched(positions, source, resident, hot, tags, lru, lengths, page_s
     B, K = positions.shape
     if positions.dtype not in (torch.int32, torch.int64) or positions.stride(1) != 1:
         raise ValueError("positions must be a [B, K] int32/int64 tensor with unit stride")
-    for name, t, dt in (("source", source, torch.int32), ("resident", resident, torch.int32),
-                        ("hot", hot, torch.int32), ("tags", tags, torch.int32), ("lru", lru, torch.int64)):
-        if t.dtype != dt or t.ndim != 2 or t.shape[0] != B or t.stride(1) != 1:
-            raise ValueError(f"{name} must be a [B, n] {dt} tensor with unit stride")
-    if source.shape != resident.shape or source.stride(0) != resident.stride(0):
-        raise ValueError("source and resident tables must have the same shape and strides")
-    H = tags.shape[1]
-    if lru.shape[1] != H or hot.shape[1] * page_size < H:
-        raise ValueError("tags/lru/hot table sizes disagree")
-    lengths_t = None
-    length = 0
-    if isinstance(lengths, torch.Tensor):
-        lengths_t = lengths.to(device=device, dtype=torch.int64).contiguous()
-    else:
-        length = int(lengths)
-    physical = torch.empty(B, K, dtype=torch.int64, device=device)
-    miss_host = torch.empty_like(physical)
-    miss_device = torch.empty_like(physical)
-    counts = torch.empty(B, 3, dtype=torch.int64, device=device)
+    H = _check_tables(B, source, resident, hot, tags, lru, page_size)
+    lengths_t, length = _lengths_arg(lengths, device)
+    physical, miss_host, miss_device, counts = _plan_outputs(B, K, device)
     lib = _hip.load()
     status = lib.nhs_resolve_rows(
         B, K, _ptr(positions), int(positions.dtype == torch.int64), positions.stride(0), _ptr(source),
@@ -312,17 +322,13 @@ def expand_columns(shared_rows, columns):
 # ---- selectors ---------------------------------------------------------------------
 
 
-def _lengths_arg(lengths, device):
-    if isinstance(lengths, torch.Tensor):
-        return lengths.to(device=device, dtype=torch.int64).contiguous(), 0
-    return None, int(lengths)
-
-
-def quest_batched(query, minimum, maximum, lengths, page_size, top_pages, keep_sink=True):
+def quest_batched(query, minimum, maximum, lengths, page_size, top_pages, keep_sink=True, select=True):
     """Quest selection for B requests: query [B, Hq, D]; minimum/maximum
     [B, n_pages, Hkv, D] (the per-page bounds of each request). Returns
     (pages [B, top_pages] int32 ascending with -1 padding, positions
-    [B, top_pages*P] int32 ascending with -1 padding, scores [B, n_pages])."""
+    [B, top_pages*P] int32 ascending with -1 padding, scores [B, n_pages]);
+    select=False computes the scores only (pages and positions None), for
+    select_resolve_batched."""
     device = _require_gpu("quest_selection", query, minimum, maximum)
     B, Hq, D = query.shape
     if minimum.shape != maximum.shape or minimum.ndim != 4 or minimum.shape[0] != B or minimum.shape[3] != D:
@@ -334,8 +340,7 @@ def quest_batched(query, minimum, maximum, lengths, page_size, top_pages, keep_s
     n_pages, kv_heads = minimum.shape[1], minimum.shape[2]
     lengths_t, length = _lengths_arg(lengths, device)
     scores = torch.empty(B, n_pages, dtype=torch.float32, device=device)
-    pages = torch.empty(B, top_pages, dtype=torch.int32, device=device)
-    positions = torch.empty(B, top_pages * page_size, dtype=torch.int32, device=device)
+    pages, positions = _selection_outputs(B, top_pages, page_size, device, select)
     lib = _hip.load()
     status = lib.nhs_quest_select(
         B, _ptr(query), dtype_code(query.dtype), query.stride(0), query.stride(1), _ptr(minimum), _ptr(maximum),
@@ -346,8 +351,16 @@ def quest_batched(query, minimum, maximum, lengths, page_size, top_pages, keep_s
     return pages, positions, scores
 
 
-def mean_batched(query, summaries, lengths, page_size, top_pages):
-    """Page-mean selection for B requests; summaries [B, n_pages, Hkv, D] fp32."""
+def _selection_outputs(B, top_pages, page_size, device, select):
+    if not select:
+        return None, None
+    return (torch.empty(B, top_pages, dtype=torch.int32, device=device),
+            torch.empty(B, top_pages * page_size, dtype=torch.int32, device=device))
+
+
+def mean_batched(query, summaries, lengths, page_size, top_pages, select=True):
+    """Page-mean selection for B requests; summaries [B, n_pages, Hkv, D] fp32.
+    select=False computes the scores only, as in quest_batched."""
     device = _require_gpu("select_pages", query, summaries)
     B, Hq, D = query.shape
     if summaries.ndim != 4 or summaries.dtype != torch.float32 or summaries.shape[0] != B:
@@ -357,8 +370,7 @@ def mean_batched(query, summaries, lengths, page_size, top_pages):
     n_pages, kv_heads = summaries.shape[1], summaries.shape[2]
     lengths_t, length = _lengths_arg(lengths, device)
     scores = torch.empty(B, n_pages, dtype=torch.float32, device=device)
-    pages = torch.empty(B, top_pages, dtype=torch.int32, device=device)
-    positions = torch.empty(B, top_pages * page_size, dtype=torch.int32, device=device)
+    pages, positions = _selection_outputs(B, top_pages, page_size, device, select)
     lib = _hip.load()
     status = lib.nhs_mean_select(
         B, _ptr(query), dtype_code(query.dtype), query.stride(0), query.stride(1), _ptr(summaries),
@@ -411,15 +423,16 @@ def append_items(k, v, pool, host, items, lengths):
     _hip.check(status, "nhs_append_items")
 
 
-def quest_items(query, items, bounds_dtype, kv_heads, lengths, page_size, max_pages, top_pages, keep_sink=True):
-    """quest_batched over per-item bounds; returns (pages, positions, scores)."""
+def quest_items(query, items, bounds_dtype, kv_heads, lengths, page_size, max_pages, top_pages, keep_sink=True,
+                select=True):
+    """quest_batched over per-item bounds; returns (pages, positions, scores)
+    (select=False: scores only)."""
     device = _require_gpu("quest_items", query, items, lengths)
     B, Hq, D = query.shape
     if query.stride(2) != 1 or items.shape[0] != B or lengths.shape[0] != B:
         raise ValueError("query rows must be contiguous, with one item and one length per request")
     scores = torch.empty(B, max_pages, dtype=torch.float32, device=device)
-    pages = torch.empty(B, top_pages, dtype=torch.int32, device=device)
-    positions = torch.empty(B, top_pages * page_size, dtype=torch.int32, device=device)
+    pages, positions = _selection_outputs(B, top_pages, page_size, device, select)
     lib = _hip.load()
     status = lib.nhs_quest_select_items(
         B, _ptr(query), dtype_code(query.dtype), query.stride(0), query.stride(1), _ptr(items),
@@ -451,6 +464,67 @@ def resolve_items(positions, items, hot_rows, lengths, page_size, counts_total=N
     )
     _hip.check(status, "nhs_resolve_items")
     return physical, miss_host, miss_device, counts
+
+
+# ---- fused selection + resolution ---------------------------------------------------
+
+FUSED_MAX_PAGES = 1024  # pages one wave ranks (nhs_select_resolve_*)
+FUSED_MAX_POSITIONS = 4096  # top_pages * page_size held in LDS
+MODES = {"quest": 0, "mean": 1}
+
+
+def fused_select_fits(max_pages, top_pages, page_size):
+    """Whether nhs_select_resolve_* takes this shape (else a selector launch
+    and a resolver launch do the same work)."""
+    return max(max_pages, top_pages) <= FUSED_MAX_PAGES and top_pages * page_size <= FUSED_MAX_POSITIONS
+
+
+def select_resolve_batched(scores, source, resident, hot, tags, lru, lengths, page_size, top_pages, keep_sink=True,
+                           mode="quest", counts_total=None):
+    """The selection of quest_batched / mean_batched (mode) on their
+    scores-only output, then resolve_batched on the chosen positions, in one
+    launch. Returns (pages, positions, physical, miss_host, miss_device,
+    counts), bit-identical to the two calls."""
+    device = _require_gpu("select_resolve", scores, source, resident, hot, tags, lru)
+    B, max_pages = scores.shape
+    if scores.dtype != torch.float32 or not scores.is_contiguous():
+        raise ValueError("scores must be a contiguous [B, max_pages] float32 tensor")
+    H = _check_tables(B, source, resident, hot, tags, lru, page_size)
+    lengths_t, length = _lengths_arg(lengths, device)
+    K = top_pages * page_size
+    pages, positions = _selection_outputs(B, top_pages, page_size, device, True)
+    physical, miss_host, miss_device, counts = _plan_outputs(B, K, device)
+    lib = _hip.load()
+    status = lib.nhs_select_resolve_rows(
+        B, _ptr(scores), max_pages, MODES[mode], top_pages, int(bool(keep_sink)), _ptr(source), _ptr(resident),
+        source.stride(0), source.shape[1], _ptr(hot), hot.stride(0), _ptr(tags), tags.stride(0), _ptr(lru),
+        lru.stride(0), H, _ptr(lengths_t), length, page_size, _ptr(pages), _ptr(positions), _ptr(physical),
+        _ptr(miss_host), _ptr(miss_device), K, _ptr(counts), _ptr(counts_total), _stream(device),
+    )
+    _hip.check(status, "nhs_select_resolve_rows")
+    return pages, positions, physical, miss_host, miss_device, counts
+
+
+def select_resolve_items(scores, items, hot_rows, lengths, page_size, top_pages, keep_sink=True, mode="quest",
+                         counts_total=None):
+    """select_resolve_batched over per-item tables (nhs_select_resolve_items)."""
+    device = _require_gpu("select_resolve_items", scores, items, lengths)
+    B, max_pages = scores.shape
+    if scores.dtype != torch.float32 or not scores.is_contiguous():
+        raise ValueError("scores must be a contiguous [B, max_pages] float32 tensor")
+    if items.shape[0] != B or lengths.shape[0] != B:
+        raise ValueError("one item and one length per request")
+    K = top_pages * page_size
+    pages, positions = _selection_outputs(B, top_pages, page_size, device, True)
+    physical, miss_host, miss_device, counts = _plan_outputs(B, K, device)
+    lib = _hip.load()
+    status = lib.nhs_select_resolve_items(
+        B, _ptr(scores), max_pages, MODES[mode], top_pages, int(bool(keep_sink)), _ptr(items), hot_rows,
+        _ptr(lengths), page_size, _ptr(pages), _ptr(positions), _ptr(physical), _ptr(miss_host),
+        _ptr(miss_device), K, _ptr(counts), _ptr(counts_total), _stream(device),
+    )
+    _hip.check(status, "nhs_select_resolve_items")
+    return pages, positions, physical, miss_host, miss_device, counts
 
 
 # ---- elementwise stages of the batched decode layer -------------------------------------

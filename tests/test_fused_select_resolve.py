@@ -1,0 +1,122 @@
+"""The fused selection + resolution launch (nhs_select_resolve_rows / _items)
+against the selector launch followed by the resolver launch on the same
+scores and tables: chosen pages, positions, physical rows, miss plans,
+counts and the tags / LRU post-state must be bit-identical, step after step
+as the hot rows evolve. Both are pinned to the oracle elsewhere (the
+selector and resolver tests, and the Llama-3-8B-width batched decode test,
+which runs this launch); this file pins the fusion itself.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from nano_hisparse import row_kernels as rk
+from test_gpu_kernels import make_resolver_state
+
+
+def log_case(**kw):
+    print("case:", kw, flush=True)
+
+
+def test_fused_select_fits_the_documented_limits():
+    assert rk.fused_select_fits(512, 32, 64)
+    assert rk.fused_select_fits(1024, 64, 64)  # 16 pages per lane, 4096 positions
+    assert not rk.fused_select_fits(1025, 32, 64)
+    assert not rk.fused_select_fits(40, 1025, 1)
+    assert not rk.fused_select_fits(512, 65, 64)
+
+
+CASES = [
+    # mode, B, Hq, Hkv, D, P, n_pages, top, H, keep_sink, nan_pages, steps
+    ("quest", 16, 32, 8, 128, 64, 512, 32, 2048, True, 0, 3),  # Llama-3-8B heads at 32K context
+    ("quest", 4, 32, 8, 128, 64, 1024, 64, 4096, True, 0, 2),  # 16 pages per lane, 4096 positions
+    ("quest", 3, 8, 2, 64, 16, 700, 100, 1500, False, 5, 3),  # NaN pages, no sink
+    ("quest", 2, 8, 2, 64, 16, 200, 8, 300, True, 20, 2),  # more NaN pages than the budget: last page may lose
+    ("quest", 2, 4, 2, 64, 16, 40, 100, 300, True, 0, 2),  # budget above the page count: -1 padding
+    ("quest", 3, 4, 2, 32, 7, 300, 1, 64, True, 2, 3),  # one page, odd page size
+    ("mean", 4, 8, 2, 64, 32, 400, 20, 700, True, 3, 3),  # page-mean selector
+    ("mean", 2, 4, 1, 32, 16, 900, 1, 128, True, 0, 2),
+]
+
+
+def _scores_inputs(g, mode, B, Hq, Hkv, D, n_pages, nan_pages, dtype):
+    if mode == "quest":
+        a = torch.randn(B, n_pages, Hkv, D, generator=g)
+        c = torch.randn(B, n_pages, Hkv, D, generator=g)
+        mu = 0.5 * torch.randn(B, n_pages, 1, 1, generator=g)
+        lo, hi = torch.minimum(a, c) + mu, torch.maximum(a, c) + mu
+        for b in range(B):
+            for p in torch.randperm(n_pages - 2, generator=g)[:nan_pages].tolist():
+                hi[b, p + 1, 0, 0] = float("nan")
+        return lo.to(dtype), hi.to(dtype)
+    summ = torch.randn(B, n_pages, Hkv, D, generator=g) + 0.5 * torch.randn(B, n_pages, 1, 1, generator=g)
+    for b in range(B):
+        for p in torch.randperm(n_pages - 2, generator=g)[:nan_pages].tolist():
+            summ[b, p + 1, 0, 0] = float("nan")
+    return (summ,)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode,B,Hq,Hkv,D,P,n_pages,top,H,keep_sink,nan_pages,steps", CASES)
+def test_fused_select_resolve_equals_select_then_resolve(gpu, mode, B, Hq, Hkv, D, P, n_pages, top, H, keep_sink,
+                                                         nan_pages, steps):
+    log_case(test="select-resolve", mode=mode, B=B, n_pages=n_pages, top=top, P=P, H=H, nan_pages=nan_pages)
+    assert rk.fused_select_fits(n_pages, top, P)
+    rng = np.random.default_rng(n_pages * 7 + top)
+    g = torch.Generator().manual_seed(n_pages + top)
+    dtype = torch.bfloat16 if mode == "quest" else torch.float32
+    bounds = [t.to(gpu) for t in _scores_inputs(g, mode, B, Hq, Hkv, D, n_pages, nan_pages, dtype)]
+    source, resident, hot, tags, lru = make_resolver_state(rng, B, H, P, n_pages, 2 * n_pages,
+                                                           n_pages + -(-H // P) + 8, 0.4, 0.6)
+    g_src, g_res, g_hot = (torch.from_numpy(x).to(gpu) for x in (source, resident, hot))
+    # three copies of the mutable hot state: two-launch path, fused strided, fused per-item
+    state = [(torch.from_numpy(tags).to(gpu), torch.from_numpy(lru).to(gpu)) for _ in range(3)]
+    lengths = torch.from_numpy(rng.integers(max(1, (n_pages - 3) * P), n_pages * P + 1, size=B)).to(gpu)
+    lengths[0] = min(int(lengths[0]), 5 * P + 3)  # a short request: fewer pages than max_pages
+    items = rk.layer_items([[dict(source=g_src[b], resident=g_res[b], hot=g_hot[b], tags=state[2][0][b],
+                                  lru=state[2][1][b], minimum=g_src[b], maximum=g_src[b], summaries=g_src[b],
+                                  n_pages=n_pages) for b in range(B)]], gpu)[0]
+    totals = [torch.zeros(3, dtype=torch.int64, device=gpu) for _ in range(3)]
+    for step in range(steps):
+        q = torch.randn(B, Hq, D, generator=g).to(gpu, dtype if mode == "quest" else torch.bfloat16)
+        if mode == "quest":
+            pages, positions, _ = rk.quest_batched(q, *bounds, lengths, P, top, keep_sink)
+            _, none, scores = rk.quest_batched(q, *bounds, lengths, P, top, keep_sink, select=False)
+        else:
+            pages, positions, _ = rk.mean_batched(q, *bounds, lengths, P, top)
+            _, none, scores = rk.mean_batched(q, *bounds, lengths, P, top, select=False)
+        assert none is None
+        (tags_a, lru_a), (tags_b, lru_b), (tags_c, lru_c) = state
+        want = rk.resolve_batched(positions, g_src, g_res, g_hot, tags_a, lru_a, lengths, P, counts_total=totals[0])
+        got = rk.select_resolve_batched(scores, g_src, g_res, g_hot, tags_b, lru_b, lengths, P, top, keep_sink, mode,
+                                        counts_total=totals[1])
+        got_items = rk.select_resolve_items(scores, items, H, lengths, P, top, keep_sink, mode,
+                                            counts_total=totals[2])
+        torch.cuda.synchronize()
+        for name, x, y in zip(("pages", "positions", "physical", "miss_host", "miss_device", "counts"),
+                              (pages, positions) + tuple(want), got):
+            assert torch.equal(x, y), (step, name)
+        for x, y in zip(got, got_items):
+            assert torch.equal(x, y), step
+        for t in (tags_b, tags_c):
+            assert torch.equal(t, tags_a), step
+        for t in (lru_b, lru_c):
+            assert torch.equal(t, lru_a), step
+    assert torch.equal(totals[0], totals[1]) and torch.equal(totals[0], totals[2])
+
+
+@pytest.mark.gpu
+def test_fused_select_resolve_rejects_shapes_beyond_one_wave(gpu):
+    log_case(test="select-resolve-limits")
+    B, H, P = 1, 64, 64
+    scores = torch.zeros(B, 1025, dtype=torch.float32, device=gpu)
+    tabs = [torch.zeros(B, 1025, dtype=torch.int32, device=gpu) for _ in range(2)]
+    hot = torch.zeros(B, 1, dtype=torch.int32, device=gpu)
+    tags = torch.full((B, H), -1, dtype=torch.int32, device=gpu)
+    lru = torch.arange(H, device=gpu)[None].clone()
+    with pytest.raises(RuntimeError, match="1024"):
+        rk.select_resolve_batched(scores, *tabs, hot, tags, lru, 1025 * P, P, 32)
+    with pytest.raises(RuntimeError, match="4096"):
+        rk.select_resolve_batched(scores[:, :512], tabs[0][:, :512], tabs[1][:, :512], hot, tags, lru, 512 * P, P,
+                                  65)

@@ -314,18 +314,26 @@ def test_llama8b_width_batched_decode_matches_the_oracle_per_layer(gpu, monkeypa
             seen["resolve"] = rk_resolve(*a, **k)
             return seen["resolve"]
 
-        monkeypatch.setattr(rk, "quest_items", quest_items)
-        monkeypatch.setattr(rk, "resolve_items", resolve_items)
+        def select_resolve_items(*a, **k):
+            seen["fused"] = rk_fused(*a, **k)
+            return seen["fused"]
+
+        hooks = {"quest_items": quest_items, "resolve_items": resolve_items,
+                 "select_resolve_items": select_resolve_items}
+        for name, f in hooks.items():
+            monkeypatch.setattr(rk, name, f)
         try:
             handle = orig_select(self, layer, query, top_pages, keep_sink)
         finally:
-            monkeypatch.setattr(rk, "quest_items", rk_quest)
-            monkeypatch.setattr(rk, "resolve_items", rk_resolve)
+            for name, f in originals.items():
+                monkeypatch.setattr(rk, name, f)
         torch.cuda.synchronize()
         _, e_pages, e_pos = oracle.quest_select(q, mn, mx, lengths, P, top_pages, keep_sink)
-        pages, positions, _ = seen["quest"]
+        # this shape takes the fused selection + resolve launch
+        assert "fused" in seen and "resolve" not in seen
+        pages, positions = seen["fused"][:2]
         assert torch.equal(pages.cpu(), e_pages) and torch.equal(positions.cpu(), e_pos), layer
-        physical, mh, md, counts = (t.cpu().numpy() for t in seen["resolve"])
+        physical, mh, md, counts = (t.cpu().numpy() for t in seen["fused"][2:])
         for b, t in enumerate(tables):
             want = oracle.resolve_rows(e_pos[b].numpy(), src[b], res[b], hot[b], tags[b], lru[b],
                                        int(lengths[b]), P)
@@ -346,7 +354,8 @@ def test_llama8b_width_batched_decode_matches_the_oracle_per_layer(gpu, monkeypa
         assert (out.cpu().float() - want).abs().max().item() <= 2e-2
         return out
 
-    rk_quest, rk_resolve = rk.quest_items, rk.resolve_items
+    rk_quest, rk_resolve, rk_fused = rk.quest_items, rk.resolve_items, rk.select_resolve_items
+    originals = {"quest_items": rk_quest, "resolve_items": rk_resolve, "select_resolve_items": rk_fused}
     monkeypatch.setattr(batched.BatchDecode, "select", select)
     monkeypatch.setattr(batched.BatchDecode, "finish", finish)
     for _ in range(steps):
