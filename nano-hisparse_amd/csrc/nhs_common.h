@@ -70,7 +70,6 @@ struct FastDiv {
 // also count against the LDS wait counter, so every wait for an LDS result
 // would also wait for them.
 #define NHS_GLOBAL __attribute__((address_space(1)))
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));  // copyable from any address space
 template <typename T>
 __device__ __forceinline__ NHS_GLOBAL T* to_global(T* p) {
   return (NHS_GLOBAL T*)p;

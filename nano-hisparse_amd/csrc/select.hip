@@ -145,27 +145,25 @@ __device__ __forceinline__ uint32_t nan_bits(uint32_t w) {
   }
 }
 
-// The rare test of one lane's chunk (n elements) of one page whose group has
-// a zero or infinite query: each element's query heads and bounds are
-// re-read from memory and tested for 0 * inf (zero_inf_product). q_off is
-// the element index of the group's first head at the chunk's first element.
+// For a lane whose query chunk has zero / infinite elements (masks zero_m,
+// inf_m): whether one 32-bit word of a page's lower and upper bounds
+// (elements e0 .. e0 + 4 / T::bytes - 1, packed in T) meets them in 0 * inf,
+// as zero_inf_product() per element, on the packed bits: a +-inf or +-0
+// bound element against a zero_m or inf_m bit.
 template <typename T>
-__device__ __forceinline__ bool zero_inf_chunk(const ScoreArgs& a, int64_t q_off, int group, const char* lo,
-                                                        const char* hi, int64_t b_off, int n) {
-#pragma unroll 1
-  for (int e = 0; e < n; ++e) {
-    bool zero_q = false, inf_q = false;
-#pragma unroll 1
-    for (int g = 0; g < group; ++g) {
-      const float q = load_elem(a.q, a.q_dtype, q_off + (int64_t)g * a.q_hs + e);
-      zero_q |= q == 0.f;
-      inf_q |= __builtin_isinf(q);
-    }
-    if ((zero_q || inf_q) &&
-        zero_inf_product(load_elem(lo, T::dtype, b_off + e), load_elem(hi, T::dtype, b_off + e), zero_q, inf_q))
-      return true;
+__device__ __forceinline__ uint32_t zero_inf_word(uint32_t zero_m, uint32_t inf_m, uint32_t lo_w, uint32_t hi_w,
+                                                  int e0) {
+  constexpr int per = 4 / T::bytes;  // elements per word
+  constexpr uint32_t kMag = T::bytes == 4 ? 0x7fffffffu : 0x7fffu;
+  constexpr uint32_t kInf = T::bytes == 4 ? 0x7f800000u : T::dtype == NHS_BF16 ? 0x7f80u : 0x7c00u;
+  uint32_t bad = 0u;
+#pragma unroll
+  for (int i = 0; i < per; ++i) {
+    const uint32_t l = (lo_w >> (16 * i)) & kMag, h = (hi_w >> (16 * i)) & kMag;
+    const uint32_t zq = (zero_m >> (e0 + i)) & 1u, iq = (inf_m >> (e0 + i)) & 1u;
+    bad |= ((zq && (l == kInf || h == kInf)) || (iq && (l == 0u || h == 0u))) ? 1u : 0u;
   }
-  return false;
+  return bad;
 }
 
 // The per-lane grouped sums and the side bits of its E elements.
@@ -174,17 +172,21 @@ struct GroupedQuery {
   static_assert(E <= 32, "side masks hold one bit per element");
   float pos[E], neg[E];
   uint32_t has_pos = 0, has_neg = 0;  // bit e: a head of the group is > 0 (not > 0) at element e
-  // a head's query is +-0 or +-inf somewhere in the chunk (one bit: per-element
-  // masks cost ~28 VGPRs; the rare lanes with it re-test from memory)
+  uint32_t zero_m = 0, inf_m = 0;      // bit e: a head of the group is +-0 (+-inf) at element e
+  // zero_m | inf_m != 0, kept as its own bit: a kernel may park the two masks
+  // in LDS for the rare lanes that test bounds against them (holding them
+  // in registers through the slots cost ~20 VGPRs at group 7)
   uint32_t special = 0;
   __device__ __forceinline__ void set(int e, float p, float n, uint32_t side) {
     pos[e] = p, neg[e] = n;
     has_pos |= ((side & kSidePos) ? 1u : 0u) << e;
     has_neg |= ((side & kSideNeg) ? 1u : 0u) << e;
-    special |= (side & (kSideZero | kSideInf)) ? 1u : 0u;
+    zero_m |= ((side & kSideZero) ? 1u : 0u) << e;
+    inf_m |= ((side & kSideInf) ? 1u : 0u) << e;
+    special = (zero_m | inf_m) ? 1u : 0u;
   }
   __device__ __forceinline__ void clear_if_idle(bool live) {
-    // padding lanes add exactly +0
+    // padding lanes add exactly +0 (their zero_m / inf_m are never read)
     if (!live) has_pos = has_neg = special = 0u;
   }
   // qv: the lane's slices of the group's query heads (heads >= group are ignored)
@@ -385,12 +387,11 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
     for (int s = 0; s < S; ++s) {
       const int p = wave_first + s * ppw + page_local;
       const int pc = p < count ? p : wave_first;  // lanes past the end reread a live page
-      const int64_t at = ((int64_t)pc * page_elems + lane_off) * T::bytes;
-      NHS_GLOBAL const u32x4_t* lp = to_global(reinterpret_cast<const u32x4_t*>(lo + at));
-      NHS_GLOBAL const u32x4_t* hp = to_global(reinterpret_cast<const u32x4_t*>(hi + at));
+      const uint4* lp = reinterpret_cast<const uint4*>(lo + ((int64_t)pc * page_elems + lane_off) * T::bytes);
+      const uint4* hp = reinterpret_cast<const uint4*>(hi + ((int64_t)pc * page_elems + lane_off) * T::bytes);
 #pragma unroll
       for (int v = 0; v < W / 4; ++v) {
-        const u32x4_t x = lp[v], y = hp[v];
+        const uint4 x = lp[v], y = hp[v];
         mn[s][4 * v] = x.x, mn[s][4 * v + 1] = x.y, mn[s][4 * v + 2] = x.z, mn[s][4 * v + 3] = x.w;
         mx[s][4 * v] = y.x, mx[s][4 * v + 1] = y.y, mx[s][4 * v + 2] = y.z, mx[s][4 * v + 3] = y.w;
       }
@@ -419,6 +420,13 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
     load_bounds();
     gq.init(qv, G, data);
   }
+  // the zero / infinite query masks wait in LDS (this lane's own slot) for
+  // the rare lanes that need them below
+  __shared__ uint32_t zi_masks[kPageThreads][2];
+  if (gq.special) {
+    zi_masks[threadIdx.x][0] = gq.zero_m;
+    zi_masks[threadIdx.x][1] = gq.inf_m;
+  }
   const int lpr = 1 << a.lpr_log2;
   const int page_lane0 = page_local * lanes_per_page;
   // every slot is scored first (slots past count hold a live page's bounds
@@ -426,18 +434,31 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   // together: each group of 8 heads issues its lane reads for every slot
   // before the adds, which stay sequential in head order
   // A slot's chunk sums to NaN when it holds a NaN bound, or a bound that
-  // meets a zero or infinite query in 0 * inf. The latter is rare: only the
-  // elements flagged in has_zero / has_inf are tested, re-read from memory.
+  // meets a zero or infinite query in 0 * inf. The latter is rare: a lane
+  // whose query chunk has a zero or infinite element reads its masks back
+  // and re-reads the slot's bounds 16 bytes at a time (holding the masks or
+  // every slot's bounds for the test cost ~20 VGPRs at group 7).
   float t[S], total[S];
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     float x = gq.template chunk_packed<T>(mn[s], mx[s]);
     x = gq.template nan_bound<T>(mn[s], mx[s]) ? __uint_as_float(0x7fc00000u) : x;
     if (gq.special) {
+      const uint32_t zero_m = zi_masks[threadIdx.x][0], inf_m = zi_masks[threadIdx.x][1];
       const int p = wave_first + s * ppw + page_local;
-      const int64_t boff = (int64_t)(p < count ? p : wave_first) * page_elems + lane_off;
-      if (zero_inf_chunk<T>(a, (int64_t)b * a.q_bs + (int64_t)kh * G * a.q_hs + sub * E, G, lo, hi, boff, E))
-        x = __uint_as_float(0x7fc00000u);
+      const int64_t at = ((int64_t)(p < count ? p : wave_first) * page_elems + lane_off) * T::bytes;
+      const uint4* lp = reinterpret_cast<const uint4*>(lo + at);
+      const uint4* hp = reinterpret_cast<const uint4*>(hi + at);
+      uint32_t bad = 0u;
+#pragma unroll 1
+      for (int v = 0; v < W / 4; ++v) {
+        const uint4 l = lp[v], h = hp[v];
+        const int e0 = v * 16 / T::bytes, d = 4 / T::bytes;
+        bad |= zero_inf_word<T>(zero_m, inf_m, l.x, h.x, e0) | zero_inf_word<T>(zero_m, inf_m, l.y, h.y, e0 + d) |
+               zero_inf_word<T>(zero_m, inf_m, l.z, h.z, e0 + 2 * d) |
+               zero_inf_word<T>(zero_m, inf_m, l.w, h.w, e0 + 3 * d);
+      }
+      if (bad) x = __uint_as_float(0x7fc00000u);
     }
     t[s] = group_sum(x, lpr);
     total[s] = 0.f;
