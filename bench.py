@@ -34,6 +34,9 @@ against the GPU's. The default line ends with `model_decode`: the
 whole-model decode below at 16 timed steps.
 Prints one JSON line.
 
+`--workload attention-shapes` times the row attention alone, cold, at four
+batch shapes (run_attention_shapes), one JSON line per shape.
+
 `--copy-calibration` instead runs a plain 256 MiB device-to-device copy three
 times: the known-size kernel that scales the FETCH_SIZE / WRITE_SIZE
 counters of a rocprofv3 --pmc run to bytes.
@@ -80,7 +83,8 @@ def parse_args():
     ap.add_argument("--side-stream", action="store_true",
                     help="run the gather on a side stream ordered by events (the default with --chunks > 1)")
     ap.add_argument("--copy-calibration", action="store_true", help="run the PMC calibration copy and exit")
-    ap.add_argument("--workload", choices=("kernel", "miss-heavy", "model", "resolver-stress"), default="kernel",
+    ap.add_argument("--workload", choices=("kernel", "miss-heavy", "model", "resolver-stress", "attention-shapes"),
+                    default="kernel",
                     help="kernel: one-layer sparse decode step (default); miss-heavy: the same step at batch 4, "
                     "128K context, 4096-row budget, ~90%% of rows gathered; model: whole-model batched decode")
     ap.add_argument("--warm-steps", type=int, default=None,
@@ -341,6 +345,74 @@ def traffic_from_profile(kernel_tag, name="sparse_decode_b16_ctx32k_pmc_traffic.
     return None
 
 
+ATTENTION_SHAPES = {
+    # name: (requests, query heads, KV heads, head_dim, page size, rows per request)
+    "b16-32q8kv-2048rows": (16, 32, 8, 128, 64, 2048),  # the default workload's attention
+    "b4-32q8kv-4096rows": (4, 32, 8, 128, 64, 4096),  # the miss-heavy step: 128K context, top-64 pages
+    "b8-32q8kv-2048rows": (8, 32, 8, 128, 64, 2048),  # the model decode's per-layer attention
+    "b64-28q4kv-1024rows": (64, 28, 4, 128, 32, 1024),  # Qwen2-7B heads, top-32 pages of 32
+}
+
+
+def run_attention_shapes(args):
+    """Cold row attention alone at four batch shapes. Per shape, n disjoint
+    sets of whole pages of distinct pool blocks (bf16 N(0,1) K/V) are
+    cycled, n chosen so that at least 512 MB of other rows (twice the
+    256 MB Infinity Cache) are read between two visits of a set. The first
+    visits are untimed (--warmup launches, at least n), then --steps timed
+    launches are stamped with their own dispatch events, then 10 launches
+    of one set repeated (warm). One JSON line per shape."""
+    import torch
+
+    from nano_hisparse import _hip
+    from nano_hisparse import row_kernels as rk
+
+    _hip.load()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    for name, (B, Hq, Hkv, D, P, N) in ATTENTION_SHAPES.items():
+        pages = N // P
+        nbytes = B * N * 2 * Hkv * D * 2 + B * (2 * Hq * D * 2 + 8 * N)
+        n_sets = max(4, -(-(512 << 20) // nbytes) + 1)
+        blocks = n_sets * B * pages
+        pool = torch.empty(blocks, 2, P, Hkv, D, dtype=torch.bfloat16, device=dev)
+        for i in range(0, blocks, 512):
+            pool[i:i + 512].normal_(generator=g)
+        perm = torch.randperm(blocks, generator=g, device=dev)
+        sets = []
+        for k in range(n_sets):
+            blk = perm[k * B * pages:(k + 1) * B * pages].view(B, pages)
+            sets.append((blk[:, :, None] * P + torch.arange(P, device=dev)).view(B, N).sort(1).values.long())
+        q = torch.randn(B, Hq, D, generator=g, device=dev).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        for i in range(max(args.warmup, n_sets)):
+            rk.attend_batched(q, pool, sets[i % n_sets], P, out=out)
+        events = [rk.timing_events() for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        for i, ev in enumerate(events):
+            rk.set_launch_events(*ev)
+            rk.attend_batched(q, pool, sets[i % n_sets], P, out=out)
+        torch.cuda.synchronize()
+        cold = [1e3 * a.elapsed_time(b) for a, b in events]
+        warm_events = [rk.timing_events() for _ in range(10)]
+        for ev in warm_events:
+            rk.set_launch_events(*ev)
+            rk.attend_batched(q, pool, sets[0], P, out=out)
+        torch.cuda.synchronize()
+        warm = [1e3 * a.elapsed_time(b) for a, b in warm_events]
+        us, wus = sum(cold) / len(cold), sum(warm) / len(warm)
+        print(json.dumps({
+            "metric": "cold row-attention launch time", "shape": name, "unit": "us", "value": round(us, 2),
+            "higher_is_better": False, "steps": args.steps, "warmup": args.warmup, "algorithmic_bytes": nbytes,
+            "achieved_gbs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e6 / (HBM_PEAK / 1e12), 4),
+            "warm_us": round(wus, 2), "warm_frac": round(nbytes / wus / 1e6 / (HBM_PEAK / 1e12), 4),
+            "config": {"requests": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "page_size": P,
+                       "rows_per_request": N, "dtype": "bf16", "row_sets_cycled": n_sets},
+        }), flush=True)
+        del pool, sets
+        torch.cuda.empty_cache()
+
+
 def run_resolver_stress(args):
     """Quest selection + row resolution for 64 requests with Qwen2-7B heads
     (28 query / 4 KV heads x 128, bf16), contexts uniform in [4096, 65536]
@@ -599,6 +671,9 @@ def main():
         return
     if args.workload == "resolver-stress":
         run_resolver_stress(args)
+        return
+    if args.workload == "attention-shapes":
+        run_attention_shapes(args)
         return
     import torch
 
