@@ -166,72 +166,108 @@ __device__ __forceinline__ uint32_t zero_inf_word(uint32_t zero_m, uint32_t inf_
   return bad;
 }
 
-// The per-lane grouped sums and the side bits of its E elements.
+// The per-lane grouped sums of E elements. pos[e] adds the group's query
+// values > 0 and neg[e] the others (NaN included), in head order from +0.0;
+// a side with no contributor stays +0.0 and neither sum is ever -0.0. The
+// fold uses the NaN-propagating maximum / minimum: maximum(q, 0) is q > 0 ?
+// q : +0 and minimum(q, 0) is q > 0 ? +0 : q, except that a NaN q makes
+// both sums NaN (the chunk is NaN either way).
+//
+// Which heads contribute is recovered from the sums where it matters: a head
+// of the group is > 0 at e iff pos[e] > 0, and one is < 0 or NaN iff
+// !(neg[e] >= 0). A side holding only +-0 queries sums to +0 and reads as
+// no contributor; it can only change the chunk against an infinite bound,
+// where the 0 * inf test makes the chunk NaN anyway.
 template <int E, int G>
 struct GroupedQuery {
-  static_assert(E <= 32, "side masks hold one bit per element");
   float pos[E], neg[E];
-  uint32_t has_pos = 0, has_neg = 0;  // bit e: a head of the group is > 0 (not > 0) at element e
-  uint32_t zero_m = 0, inf_m = 0;      // bit e: a head of the group is +-0 (+-inf) at element e
-  // zero_m | inf_m != 0, kept as its own bit: a kernel may park the two masks
-  // in LDS for the rare lanes that test bounds against them (holding them
-  // in registers through the slots cost ~20 VGPRs at group 7)
-  uint32_t special = 0;
-  __device__ __forceinline__ void set(int e, float p, float n, uint32_t side) {
-    pos[e] = p, neg[e] = n;
-    has_pos |= ((side & kSidePos) ? 1u : 0u) << e;
-    has_neg |= ((side & kSideNeg) ? 1u : 0u) << e;
-    zero_m |= ((side & kSideZero) ? 1u : 0u) << e;
-    inf_m |= ((side & kSideInf) ? 1u : 0u) << e;
-    special = (zero_m | inf_m) ? 1u : 0u;
+  static __device__ __forceinline__ void add(float q, float& p, float& n) {
+    p = p + __builtin_elementwise_maximum(q, 0.f);
+    n = n + __builtin_elementwise_minimum(q, 0.f);
   }
   __device__ __forceinline__ void clear_if_idle(bool live) {
-    // padding lanes add exactly +0 (their zero_m / inf_m are never read)
-    if (!live) has_pos = has_neg = special = 0u;
+    // padding lanes add exactly +0 against finite bounds
+    if (!live) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) pos[e] = neg[e] = 0.f;
+    }
   }
-  // qv: the lane's slices of the group's query heads (heads >= group are ignored)
-  __device__ __forceinline__ void init(const float (&qv)[G][E], int group, bool live) {
+  // Folds EF elements of the lane's query slices into pos / neg[0 .. EF)
+  // (heads >= group are ignored).
+  template <int EF>
+  __device__ __forceinline__ void fold(const float (&qv)[G][EF], int group) {
 #pragma clang fp contract(off)
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
+    for (int e = 0; e < EF; ++e) {
       float p = 0.f, n = 0.f;
-      uint32_t side = 0u;
 #pragma unroll
       for (int g = 0; g < G; ++g)
-        if (g < group) fold_query(qv[g][e], p, n, side);
-      set(e, p, n, side);
+        if (g < group) add(qv[g][e], p, n);
+      pos[e] = p, neg[e] = n;
     }
-    clear_if_idle(live);
   }
-  // init() from the heads' slices kept packed in T (widened element by element)
-  // (all G heads are in the group)
-  template <typename T>
-  __device__ __forceinline__ void init_packed(const uint32_t (&qw)[G][E * T::bytes / 4], bool live) {
+  // fold() from the heads' slices kept packed in T (widened element by
+  // element; all G heads are in the group)
+  template <typename T, int EF>
+  __device__ __forceinline__ void fold_packed(const uint32_t (&qw)[G][EF * T::bytes / 4]) {
 #pragma clang fp contract(off)
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
+    for (int e = 0; e < EF; ++e) {
       float p = 0.f, n = 0.f;
-      uint32_t side = 0u;
 #pragma unroll
-      for (int g = 0; g < G; ++g) fold_query(packed_elem<T, E>(qw[g], e), p, n, side);
-      set(e, p, n, side);
+      for (int g = 0; g < G; ++g) add(packed_elem<T, EF>(qw[g], e), p, n);
+      pos[e] = p, neg[e] = n;
     }
-    clear_if_idle(live);
   }
-  // this lane's chunk sum for one page's bounds kept packed in T
+  // For a wave whose lanes l and l + 32 hold the same query chunk: lane l
+  // folded its first E / 2 elements and lane l + 32 the other E / 2 into
+  // pos / neg[0 .. E / 2). v_permlane32_swap of a register with itself
+  // gives every lane the lower half-wave's value and the upper one's.
+  __device__ __forceinline__ void join_halves() {
+#pragma unroll
+    for (int e = 0; e < E / 2; ++e) {
+      const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(pos[e]), __float_as_uint(pos[e]), false, false);
+      const auto n = __builtin_amdgcn_permlane32_swap(__float_as_uint(neg[e]), __float_as_uint(neg[e]), false, false);
+      pos[e] = __uint_as_float(p[0]), pos[E / 2 + e] = __uint_as_float(p[1]);
+      neg[e] = __uint_as_float(n[0]), neg[E / 2 + e] = __uint_as_float(n[1]);
+    }
+  }
+  // The chunk sum for one page's bounds kept packed in T, every bound
+  // multiplied: t = fma(lo, neg, t), t = fma(hi, pos, t). Against finite,
+  // ordered bounds (lo <= hi) and finite sums it equals chunk_exact() bit
+  // for bit: an unused bound meets a +0 sum and adds +-0, which leaves t
+  // unchanged since t is never -0. Any infinite or NaN bound or sum makes it
+  // non-finite (inf * a nonzero sum is inf, inf * +0 is NaN). inverted is
+  // set when some hi < lo.
   template <typename T>
-  __device__ __forceinline__ float chunk_packed(const uint32_t (&mn)[E * T::bytes / 4],
-                                                const uint32_t (&mx)[E * T::bytes / 4]) const {
+  __device__ __forceinline__ float chunk_fast(const uint32_t (&mn)[E * T::bytes / 4],
+                                              const uint32_t (&mx)[E * T::bytes / 4], bool& inverted) const {
+    float x = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float lo = packed_elem<T, E>(mn, e), hi = packed_elem<T, E>(mx, e);
+      inverted |= hi < lo;
+      x = __builtin_fmaf(lo, neg[e], x);
+      x = __builtin_fmaf(hi, pos[e], x);
+    }
+    return x;
+  }
+  // The chunk sum with the reference's semantics before its NaN and 0 * inf
+  // tests: bounds ordered (a = hi, b = lo when hi < lo), t = fma(a', neg, t)
+  // then t = fma(b', pos, t), where a' (b') is 0 when no head of the group
+  // is < 0 or NaN (> 0) at e.
+  template <typename T>
+  __device__ __forceinline__ float chunk_exact(const uint32_t (&mn)[E * T::bytes / 4],
+                                               const uint32_t (&mx)[E * T::bytes / 4]) const {
     float x = 0.f;
 #pragma unroll
     for (int e = 0; e < E; ++e)
-      x = quest_fma2(x, packed_elem<T, E>(mn, e), packed_elem<T, E>(mx, e), pos[e], neg[e], (has_pos >> e) & 1u,
-                     (has_neg >> e) & 1u);
+      x = quest_fma2(x, packed_elem<T, E>(mn, e), packed_elem<T, E>(mx, e), pos[e], neg[e], pos[e] > 0.f,
+                     !(neg[e] >= 0.f));
     return x;
   }
-  // Nonzero when the chunk of one page's bounds makes the reference's
-  // torch.maximum NaN: a NaN bound, or 0 * inf against a zero or infinite
-  // query. Integer tests on the packed bits.
+  // Nonzero when the chunk of one page's bounds holds a NaN (integer tests
+  // on the packed bits).
   template <typename T>
   __device__ __forceinline__ uint32_t nan_bound(const uint32_t (&mn)[E * T::bytes / 4],
                                                 const uint32_t (&mx)[E * T::bytes / 4]) const {
@@ -350,7 +386,7 @@ constexpr int kPageWaves = kPageThreads / kWave;
 // against 49 us at Qwen2-7B heads).
 __host__ __device__ constexpr int page_slots(int group) { return group <= 4 ? 2 : 4; }
 
-template <typename T, int E, int G>
+template <typename T, int E, int G, bool SPLIT>
 __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
@@ -373,10 +409,16 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   // the waves a SIMD holds). The bounds of every slot are requested before
   // the query slices are used, so the two memory latencies overlap.
   constexpr int W = E * T::bytes / 4;  // 32-bit words of a lane's 32-byte chunk
+  // SPLIT (a page takes 32 lanes, so lanes l and l + 32 hold the same query
+  // chunk): a lane folds half of its chunk, lanes 32..63 the second half,
+  // and the halves are joined across the wave.
+  constexpr int EF = SPLIT ? E / 2 : E;  // elements folded per lane
+  constexpr int WF = EF * T::bytes / 4;
+  const int fold_off = SPLIT ? (lane >> 5) * EF : 0;
   int64_t qi[G];
 #pragma unroll
   for (int g = 0; g < G; ++g)
-    qi[g] = (int64_t)b * a.q_bs + (data ? (int64_t)(kh * G + g) * a.q_hs + sub * E : 0);
+    qi[g] = (int64_t)b * a.q_bs + (data ? (int64_t)(kh * G + g) * a.q_hs + sub * E + fold_off : 0);
   const char *lo, *hi;
   bounds_of<T>(a, b, lo, hi);
   const int64_t page_elems = (int64_t)a.kv_heads * a.head_dim;
@@ -399,68 +441,90 @@ __global__ __launch_bounds__(kPageThreads) void quest_page_kernel(ScoreArgs a) {
   };
   GroupedQuery<E, G> gq;  // G is the group size here: nothing to mask
   if (a.q_vec && a.q_dtype == T::dtype) {
-    uint32_t qw[G][W];
+    uint32_t qw[G][WF];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const uint4* qp = reinterpret_cast<const uint4*>(static_cast<const char*>(a.q) + qi[g] * T::bytes);
 #pragma unroll
-      for (int v = 0; v < W / 4; ++v) {
+      for (int v = 0; v < WF / 4; ++v) {
         const uint4 x = qp[v];
         qw[g][4 * v] = x.x, qw[g][4 * v + 1] = x.y, qw[g][4 * v + 2] = x.z, qw[g][4 * v + 3] = x.w;
       }
     }
     load_bounds();
-    gq.template init_packed<T>(qw, data);
+    gq.template fold_packed<T, EF>(qw);
   } else {
-    float qv[G][E];
+    float qv[G][EF];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < E; ++e) qv[g][e] = load_elem(a.q, a.q_dtype, qi[g] + (data ? e : 0));
+      for (int e = 0; e < EF; ++e) qv[g][e] = load_elem(a.q, a.q_dtype, qi[g] + (data ? e : 0));
     load_bounds();
-    gq.init(qv, G, data);
+    gq.template fold<EF>(qv, G);
   }
-  // the zero / infinite query masks wait in LDS (this lane's own slot) for
-  // the rare lanes that need them below
-  __shared__ uint32_t zi_masks[kPageThreads][2];
-  if (gq.special) {
-    zi_masks[threadIdx.x][0] = gq.zero_m;
-    zi_masks[threadIdx.x][1] = gq.inf_m;
-  }
+  if constexpr (SPLIT) gq.join_halves();
+  gq.clear_if_idle(data);
   const int lpr = 1 << a.lpr_log2;
   const int page_lane0 = page_local * lanes_per_page;
   // every slot is scored first (slots past count hold a live page's bounds
   // and are not stored), then the KV-head sums of all slots are formed
   // together: each group of 8 heads issues its lane reads for every slot
-  // before the adds, which stay sequential in head order
-  // A slot's chunk sums to NaN when it holds a NaN bound, or a bound that
-  // meets a zero or infinite query in 0 * inf. The latter is rare: a lane
-  // whose query chunk has a zero or infinite element reads its masks back
-  // and re-reads the slot's bounds 16 bytes at a time (holding the masks or
-  // every slot's bounds for the test cost ~20 VGPRs at group 7).
+  // before the adds, which stay sequential in head order.
   float t[S], total[S];
+  uint32_t slow = 0u;  // bit s: slot s needs the exact chunk sum
 #pragma unroll
   for (int s = 0; s < S; ++s) {
-    float x = gq.template chunk_packed<T>(mn[s], mx[s]);
-    x = gq.template nan_bound<T>(mn[s], mx[s]) ? __uint_as_float(0x7fc00000u) : x;
-    if (gq.special) {
-      const uint32_t zero_m = zi_masks[threadIdx.x][0], inf_m = zi_masks[threadIdx.x][1];
+    bool inverted = false;
+    t[s] = gq.template chunk_fast<T>(mn[s], mx[s], inverted);
+    slow |= (!__builtin_isfinite(t[s]) || inverted ? 1u : 0u) << s;
+  }
+  // A lane whose fast chunk sum is not finite, or whose bounds are inverted,
+  // recomputes it exactly; only infinite or NaN bounds or query values,
+  // inverted bounds or an overflow lead here. The chunk is NaN when a bound
+  // is NaN, or when a bound meets a zero or infinite query element in
+  // 0 * inf. The bounds and the query's zero / infinite elements are re-read
+  // from memory, so this path holds no registers through the fast one.
+  if (slow) {
+    uint32_t zero_m = 0u, inf_m = 0u;  // bit e: a head of the group is +-0 (+-inf) at element e
+    if (data) {
+#pragma unroll 1
+      for (int g = 0; g < G; ++g) {
+        const int64_t q0 = (int64_t)b * a.q_bs + (int64_t)(kh * G + g) * a.q_hs + sub * E;
+#pragma unroll 4
+        for (int e = 0; e < E; ++e) {
+          const float q = load_elem(a.q, a.q_dtype, q0 + e);
+          zero_m |= (q == 0.f ? 1u : 0u) << e;
+          inf_m |= (__builtin_isinf(q) ? 1u : 0u) << e;
+        }
+      }
+    }
+#pragma unroll 1
+    for (int s = 0; s < S; ++s) {
+      if (!((slow >> s) & 1u)) continue;
       const int p = wave_first + s * ppw + page_local;
       const int64_t at = ((int64_t)(p < count ? p : wave_first) * page_elems + lane_off) * T::bytes;
       const uint4* lp = reinterpret_cast<const uint4*>(lo + at);
       const uint4* hp = reinterpret_cast<const uint4*>(hi + at);
-      uint32_t bad = 0u;
-#pragma unroll 1
+      uint32_t lw[W], hw[W];
+#pragma unroll
       for (int v = 0; v < W / 4; ++v) {
-        const uint4 l = lp[v], h = hp[v];
-        const int e0 = v * 16 / T::bytes, d = 4 / T::bytes;
-        bad |= zero_inf_word<T>(zero_m, inf_m, l.x, h.x, e0) | zero_inf_word<T>(zero_m, inf_m, l.y, h.y, e0 + d) |
-               zero_inf_word<T>(zero_m, inf_m, l.z, h.z, e0 + 2 * d) |
-               zero_inf_word<T>(zero_m, inf_m, l.w, h.w, e0 + 3 * d);
+        const uint4 x = lp[v], y = hp[v];
+        lw[4 * v] = x.x, lw[4 * v + 1] = x.y, lw[4 * v + 2] = x.z, lw[4 * v + 3] = x.w;
+        hw[4 * v] = y.x, hw[4 * v + 1] = y.y, hw[4 * v + 2] = y.z, hw[4 * v + 3] = y.w;
       }
+      float x = gq.template chunk_exact<T>(lw, hw);
+      uint32_t bad = gq.template nan_bound<T>(lw, hw);
+#pragma unroll
+      for (int w = 0; w < W; ++w) bad |= zero_inf_word<T>(zero_m, inf_m, lw[w], hw[w], w * (4 / T::bytes));
       if (bad) x = __uint_as_float(0x7fc00000u);
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2)
+        if (s2 == s) t[s2] = x;
     }
-    t[s] = group_sum(x, lpr);
+  }
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    t[s] = group_sum(t[s], lpr);
     total[s] = 0.f;
   }
   for (int h0 = 0; h0 < a.kv_heads; h0 += 8) {
@@ -937,9 +1001,13 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
     a.pages_per_block = kPageWaves * page_slots(a.group) * ppw;
     grid = dim3((unsigned)((max_pages + a.pages_per_block - 1) / a.pages_per_block), (unsigned)batch);
     block = dim3(kPageThreads);
-    switch (bounds_dtype * 16 + a.group) {  // instantiated for every group size: no masked heads
-#define NHS_PAGE_CASE(DT, TY, EE, GG) \
-  case DT * 16 + GG: kernel = quest_page_kernel<TY, EE, GG>; break;
+    // SPLIT when a page takes exactly half a wave: the two half-waves fold
+    // the same query chunks, so each folds half of them
+    const int split = lanes_per_page == kWave / 2 ? 1 : 0;
+    switch ((bounds_dtype * 16 + a.group) * 2 + split) {  // instantiated for every group size: no masked heads
+#define NHS_PAGE_CASE(DT, TY, EE, GG)                                                  \
+  case (DT * 16 + GG) * 2: kernel = quest_page_kernel<TY, EE, GG, false>; break;      \
+  case (DT * 16 + GG) * 2 + 1: kernel = quest_page_kernel<TY, EE, GG, true>; break;
 #define NHS_PAGE_GS(DT, TY, EE)                                                                         \
   NHS_PAGE_CASE(DT, TY, EE, 1) NHS_PAGE_CASE(DT, TY, EE, 2) NHS_PAGE_CASE(DT, TY, EE, 3) NHS_PAGE_CASE(DT, TY, EE, 4) \
   NHS_PAGE_CASE(DT, TY, EE, 5) NHS_PAGE_CASE(DT, TY, EE, 6) NHS_PAGE_CASE(DT, TY, EE, 7) NHS_PAGE_CASE(DT, TY, EE, 8)

@@ -281,7 +281,10 @@ def _bounds(g, B, n_pages, Hkv, D, dtype, offsets=False):
     [
         (torch.bfloat16, torch.bfloat16, 16, 32, 8, 128, 64, 512, 32, True),  # 32K context, 32 pages
         (torch.bfloat16, torch.bfloat16, 4, 32, 8, 128, 64, 2048, 64, True),  # 128K context, 64 pages
-        (torch.bfloat16, torch.bfloat16, 8, 28, 4, 128, 32, 2048, 32, True),
+        (torch.bfloat16, torch.bfloat16, 8, 28, 4, 128, 32, 2048, 32, True),  # 32 lanes per page: half-wave fold
+        (torch.bfloat16, torch.float32, 2, 28, 4, 128, 32, 700, 20, True),  # half-wave fold of an fp32 query
+        (torch.float32, torch.float32, 2, 12, 4, 64, 16, 300, 20, True),  # fp32 bounds, half-wave fold, group 3
+        (torch.float16, torch.float32, 2, 10, 2, 256, 16, 300, 20, True),  # fp16 bounds, half-wave fold, group 5
         (torch.float32, torch.float32, 3, 4, 2, 64, 16, 40, 8, True),
         (torch.float32, torch.float32, 2, 4, 2, 64, 16, 40, 8, False),
         (torch.float16, torch.float32, 2, 6, 2, 24, 7, 30, 5, True),
@@ -326,6 +329,8 @@ def test_quest_select_bit_exact(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, n_pages, 
         (torch.bfloat16, 32, 8, 128, 0, 8, False),  # page kernel, group 4
         (torch.bfloat16, 32, 8, 128, 3, 8, False),  # NaN pages below the budget
         (torch.bfloat16, 28, 4, 128, 8, 8, False),  # group 7: NaN pages fill the budget
+        (torch.bfloat16, 28, 4, 128, 3, 8, True),  # group 7 (half-wave fold), an infinite query
+        (torch.float32, 12, 4, 64, 3, 6, True),  # fp32, half-wave fold
         (torch.bfloat16, 8, 2, 64, 11, 8, False),  # more NaN pages than slots
         (torch.float32, 8, 2, 64, 3, 6, False),  # fp32 page kernel
         (torch.float16, 6, 2, 128, 3, 6, False),  # fp16, group 3
