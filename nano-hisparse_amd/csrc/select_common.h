@@ -43,9 +43,10 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 // page, the largest x with at least top_pages keys >= x, is found bit by bit,
 // most significant first: at each bit the wave counts the keys >= the prefix
 // found so far with that bit set (a compare, a ballot and a popcount per
-// slot) and keeps the bit when the count reaches top_pages. Every key above
-// it is taken, ties at it go to the lowest pages, and the chosen pages come
-// out in ascending order (ranks from mbcnt), then -1 up to top_pages.
+// slot) and keeps the bit when the count reaches top_pages; it stops early
+// once exactly top_pages keys are >= the prefix. Every key above the prefix
+// is taken, ties at it go to the lowest pages, and the chosen pages come out
+// in ascending order (ranks from mbcnt), then -1 up to top_pages.
 // Called by the 64 lanes of one wave: wave_scores loads the request's scores
 // sc (pages < max(max_pages, 1); pages past max_pages read page 0, values
 // past count are never used, and none are when every page is kept), and
@@ -77,7 +78,8 @@ __device__ __forceinline__ void wave_rank(const float (&sv)[KPL], int count, int
       key[q] = p >= count ? 0u : (p == count - 1 || (second && p == 0)) ? forced_key : order_key(sv[q]);
     }
     // prefix = the largest key x with at least top_pages keys >= x, i.e.
-    // the key of the k-th best page
+    // the key of the k-th best page (or, after an early stop, a smaller x
+    // with exactly top_pages keys >= x)
     uint32_t prefix = 0u;
 #pragma unroll
     for (int bit = 31; bit >= 0; --bit) {
@@ -91,6 +93,10 @@ __device__ __forceinline__ void wave_rank(const float (&sv)[KPL], int count, int
 #pragma unroll
       for (int q = 0; q < KPL; ++q) c += __popcll(m[q]);
       if (c >= top_pages) prefix = cand;
+      // Exactly top_pages keys >= cand: they are the selection whatever the
+      // k-th key's lower bits, and the tie step below takes every key equal
+      // to the prefix, so the search can stop (c is the same in every lane).
+      if (c == top_pages) break;
     }
     int above = 0;
 #pragma unroll
