@@ -740,19 +740,11 @@ __global__ __launch_bounds__(THREADS) void select_topk_kernel(SelectArgs a) {
   }
 }
 
-// Up to kWave * KPL pages: wave 0 selects (wave_select), then the four waves
-// expand the chosen pages to token positions.
-template <int KPL>
-__global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectArgs a) {
-  __shared__ int32_t chosen[kWave * KPL];
+// Writes request b's chosen pages (top_pages entries, -1 padded, in LDS) to
+// pages and expands them to token positions (-1 past the request's length),
+// with the kSelectWaveThreads threads of the workgroup.
+__device__ __forceinline__ void write_selection(const SelectArgs& a, int b, const int32_t* chosen, int64_t len) {
   const int tid = threadIdx.x;
-  const int b = blockIdx.x;
-  const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
-  const int64_t len = a.lengths ? a.lengths[b] : a.length;
-  if (tid < kWave)
-    wave_select<KPL>(a.scores + (int64_t)b * a.max_pages, a.max_pages, count, a.top_pages, a.mode, a.keep_sink,
-                     a.forced_key, chosen);
-  __syncthreads();
   int32_t* pages = a.pages + (int64_t)b * a.top_pages;
   for (int i = tid; i < a.top_pages; i += kSelectWaveThreads) pages[i] = chosen[i];
   const int P = a.page_size;
@@ -779,6 +771,112 @@ __global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectA
       pos[i] = (p >= 0 && t < len) ? (int32_t)t : -1;
     }
   }
+}
+
+// Up to kWave * KPL pages: wave 0 selects (wave_select), then the four waves
+// expand the chosen pages to token positions.
+template <int KPL>
+__global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectArgs a) {
+  __shared__ int32_t chosen[kWave * KPL];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
+  const int64_t len = a.lengths ? a.lengths[b] : a.length;
+  if (tid < kWave)
+    wave_select<KPL>(a.scores + (int64_t)b * a.max_pages, a.max_pages, count, a.top_pages, a.mode, a.keep_sink,
+                     a.forced_key, chosen);
+  __syncthreads();
+  write_selection(a, b, chosen, len);
+}
+
+// Up to 4 * kWave * KPL pages and kWavesMaxTop chosen: each of the four waves
+// ranks its own kWave * KPL pages (wave_topk) and keeps its best
+// min(top_pages, its pages) in LDS as candidates, in page order; wave 0 then
+// ranks the candidates, KPL2 per lane. A page outside its wave's best
+// top_pages has top_pages pages before it in (key descending, page
+// ascending) order, so the candidates hold the whole selection; and since
+// they stay in page order, ties still go to the lowest pages. The four waves
+// then expand the chosen pages to token positions.
+constexpr int kWavesMaxTop = 256;
+template <int KPL, int KPL2>
+__global__ __launch_bounds__(kSelectWaveThreads) void select_waves_kernel(SelectArgs a) {
+  constexpr int NW = kSelectWaveThreads / kWave;
+  static_assert(NW == 4, "candidate offsets below assume four waves");
+  __shared__ uint32_t cand_key[NW][kWavesMaxTop];
+  __shared__ int32_t cand_page[NW][kWavesMaxTop];
+  __shared__ int n_cand[NW];
+  __shared__ int32_t chosen[kWavesMaxTop];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  const int b = blockIdx.x;
+  const int base = wave * kWave * KPL;
+  // the score loads are issued before the page count arrives (pages past
+  // max_pages read page 0; values past count are never used)
+  const float* sc = a.scores + (int64_t)b * a.max_pages;
+  float sv[KPL];
+#pragma unroll
+  for (int q = 0; q < KPL; ++q) {
+    const int p = base + q * kWave + lane;
+    sv[q] = sc[p < a.max_pages ? p : 0];
+  }
+  const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
+  const int64_t len = a.lengths ? a.lengths[b] : a.length;
+  const int top = a.top_pages;
+  if (top >= count) {
+    // every page is kept (count <= top <= kWavesMaxTop)
+    for (int i = tid; i < top; i += kSelectWaveThreads) chosen[i] = i < count ? i : -1;
+  } else {
+    const int mine = min(max(count - base, 0), kWave * KPL);  // this wave's pages
+    uint32_t key[KPL];
+    bool sel[KPL];
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) {
+      const int p = base + q * kWave + lane;
+      key[q] = page_key(sv[q], p, count, a.mode, a.keep_sink, top, a.forced_key);
+      sel[q] = p < count;
+    }
+    if (top < mine) wave_topk<KPL>(key, top, sel);
+    int n = 0;
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) {
+      const uint64_t m = __ballot(sel[q]);
+      if (sel[q]) {
+        const int i = n + lanes_below(m);
+        cand_key[wave][i] = key[q];
+        cand_page[wave][i] = base + q * kWave + lane;
+      }
+      n += __popcll(m);
+    }
+    if (lane == 0) n_cand[wave] = n;
+    __syncthreads();
+    if (wave == 0) {
+      // candidate j in page order: wave w's i-th, j = (its waves before) + i
+      const int n0 = n_cand[0], n1 = n0 + n_cand[1], n2 = n1 + n_cand[2], n3 = n2 + n_cand[3];
+      uint32_t key2[KPL2];
+      int32_t page2[KPL2];
+      bool sel2[KPL2];
+#pragma unroll
+      for (int q = 0; q < KPL2; ++q) {
+        const int j = q * kWave + lane;
+        const int w = j < n0 ? 0 : j < n1 ? 1 : j < n2 ? 2 : 3;
+        const int i = j - (w == 0 ? 0 : w == 1 ? n0 : w == 2 ? n1 : n2);
+        sel2[q] = j < n3;
+        key2[q] = sel2[q] ? cand_key[w][i] : 0u;
+        page2[q] = sel2[q] ? cand_page[w][i] : -1;
+      }
+      if (top < n3) wave_topk<KPL2>(key2, top, sel2);
+      int n_sel = 0;
+#pragma unroll
+      for (int q = 0; q < KPL2; ++q) {
+        const uint64_t m = __ballot(sel2[q]);
+        if (sel2[q]) chosen[n_sel + lanes_below(m)] = page2[q];
+        n_sel += __popcll(m);
+      }
+      for (int i = n_sel + lane; i < top; i += kWave) chosen[i] = -1;
+    }
+  }
+  __syncthreads();
+  write_selection(a, b, chosen, len);
 }
 
 // Any page count (beyond the register kernels' 16384): every pass recomputes
@@ -931,6 +1029,18 @@ static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, con
     launch(select_wave_kernel<8>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
   else if (wave_pages <= kWave * 16)
     launch(select_wave_kernel<16>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
+  else if (wave_pages <= 4 * kWave * 16 && s.top_pages <= kWavesMaxTop) {
+    // four waves' candidates, at most 4 * top_pages of them
+    const int c = 4 * s.top_pages;
+    void (*k)(SelectArgs) = nullptr;
+    if (wave_pages <= 4 * kWave * 8)
+      k = c <= 2 * kWave ? select_waves_kernel<8, 2> : c <= 4 * kWave ? select_waves_kernel<8, 4>
+        : c <= 8 * kWave ? select_waves_kernel<8, 8> : select_waves_kernel<8, 16>;
+    else
+      k = c <= 2 * kWave ? select_waves_kernel<16, 2> : c <= 4 * kWave ? select_waves_kernel<16, 4>
+        : c <= 8 * kWave ? select_waves_kernel<16, 8> : select_waves_kernel<16, 16>;
+    launch(k, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
+  }
   else if (s.max_pages <= 256 * kMaxSelectPerThread)
     launch(select_topk_kernel<256>, dim3((unsigned)batch), dim3(256), 0, stream, start, stop, s);
   else

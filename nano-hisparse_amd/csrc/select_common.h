@@ -60,6 +60,61 @@ __device__ __forceinline__ void wave_scores(const float* sc, int max_pages, floa
   for (int q = 0; q < KPL; ++q) sv[q] = sc[q * kWave + lane < max_pages ? q * kWave + lane : 0];
 }
 
+// Marks sel[q] for the top_pages best keys of a wave (slot q of lane l is
+// item q * kWave + l): the largest prefix x with at least top_pages keys >= x
+// is found bit by bit; every key above it is taken, then the ties at it in
+// item order. Items without a key hold 0, below every real key (>= 0x007fffff),
+// and top_pages must be below the number of real keys, so the prefix always
+// has a bit set and no 0 key matches or ties with it.
+template <int KPL>
+__device__ __forceinline__ void wave_topk(const uint32_t (&key)[KPL], int top_pages, bool (&sel)[KPL]) {
+  // prefix = the largest key x with at least top_pages keys >= x, i.e. the
+  // key of the k-th best item (or, after an early stop, a smaller x with
+  // exactly top_pages keys >= x)
+  uint32_t prefix = 0u;
+#pragma unroll
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = prefix | (1u << bit);
+    // all KPL ballots are formed before any is counted, so the compares
+    // write separate mask registers and issue back to back
+    uint64_t m[KPL];
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) m[q] = __ballot(key[q] >= cand);
+    int c = 0;
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) c += __popcll(m[q]);
+    if (c >= top_pages) prefix = cand;
+    // Exactly top_pages keys >= cand: they are the selection whatever the
+    // k-th key's lower bits, and the tie step below takes every key equal
+    // to the prefix, so the search can stop (c is the same in every lane).
+    if (c == top_pages) break;
+  }
+  int above = 0;
+#pragma unroll
+  for (int q = 0; q < KPL; ++q) above += __popcll(__ballot(key[q] > prefix));
+  // every item above that key is taken, then the first `need` items with
+  // that key in item order (slot, then lane)
+  const int need = top_pages - above;
+  int before = 0;
+#pragma unroll
+  for (int q = 0; q < KPL; ++q) {
+    const bool tie = key[q] == prefix;
+    const uint64_t m = __ballot(tie);
+    sel[q] = key[q] > prefix || (tie && before + lanes_below(m) < need);
+    before += __popcll(m);
+  }
+}
+
+// The key of page p of a request of count pages whose score is sv: 0 at or
+// past count, forced_key for the forced pages (the last page; the first too
+// when Quest keeps the sink, or always for the mean selector when
+// top_pages > 1), else order_key(sv).
+__device__ __forceinline__ uint32_t page_key(float sv, int p, int count, int mode, int keep_sink, int top_pages,
+                                             uint32_t forced_key) {
+  const bool second = mode == kModeQuest ? (keep_sink && top_pages > 1 && count > 1) : top_pages > 1;
+  return p >= count ? 0u : (p == count - 1 || (second && p == 0)) ? forced_key : order_key(sv);
+}
+
 template <int KPL>
 __device__ __forceinline__ void wave_rank(const float (&sv)[KPL], int count, int top_pages, int mode, int keep_sink,
                                           uint32_t forced_key, int32_t* chosen) {
@@ -68,50 +123,11 @@ __device__ __forceinline__ void wave_rank(const float (&sv)[KPL], int count, int
 #pragma unroll
   for (int q = 0; q < KPL; ++q) sel[q] = q * kWave + lane < count;
   if (top_pages < count) {
-    const bool second = mode == kModeQuest ? (keep_sink && top_pages > 1 && count > 1) : top_pages > 1;
-    // pages past count keep key 0, below every score's key (>= 0x007fffff),
-    // so no prefix tested below (it always has a bit set) matches them
     uint32_t key[KPL];
 #pragma unroll
-    for (int q = 0; q < KPL; ++q) {
-      const int p = q * kWave + lane;
-      key[q] = p >= count ? 0u : (p == count - 1 || (second && p == 0)) ? forced_key : order_key(sv[q]);
-    }
-    // prefix = the largest key x with at least top_pages keys >= x, i.e.
-    // the key of the k-th best page (or, after an early stop, a smaller x
-    // with exactly top_pages keys >= x)
-    uint32_t prefix = 0u;
-#pragma unroll
-    for (int bit = 31; bit >= 0; --bit) {
-      const uint32_t cand = prefix | (1u << bit);
-      // all KPL ballots are formed before any is counted, so the compares
-      // write separate mask registers and issue back to back
-      uint64_t m[KPL];
-#pragma unroll
-      for (int q = 0; q < KPL; ++q) m[q] = __ballot(key[q] >= cand);
-      int c = 0;
-#pragma unroll
-      for (int q = 0; q < KPL; ++q) c += __popcll(m[q]);
-      if (c >= top_pages) prefix = cand;
-      // Exactly top_pages keys >= cand: they are the selection whatever the
-      // k-th key's lower bits, and the tie step below takes every key equal
-      // to the prefix, so the search can stop (c is the same in every lane).
-      if (c == top_pages) break;
-    }
-    int above = 0;
-#pragma unroll
-    for (int q = 0; q < KPL; ++q) above += __popcll(__ballot(key[q] > prefix));
-    // every page above that key is taken, then the first `need` pages with
-    // that key in page order (slot, then lane)
-    const int need = top_pages - above;
-    int before = 0;
-#pragma unroll
-    for (int q = 0; q < KPL; ++q) {
-      const bool tie = key[q] == prefix;
-      const uint64_t m = __ballot(tie);
-      sel[q] = key[q] > prefix || (tie && before + lanes_below(m) < need);
-      before += __popcll(m);
-    }
+    for (int q = 0; q < KPL; ++q)
+      key[q] = page_key(sv[q], q * kWave + lane, count, mode, keep_sink, top_pages, forced_key);
+    wave_topk<KPL>(key, top_pages, sel);
   }
   int n_sel = 0;
 #pragma unroll

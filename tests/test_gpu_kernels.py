@@ -291,6 +291,8 @@ def _bounds(g, B, n_pages, Hkv, D, dtype, offsets=False):
         (torch.float32, torch.float32, 2, 2, 1, 2, 2, 3, 2, False),  # head_dim 2 (element lanes)
         (torch.bfloat16, torch.bfloat16, 2, 8, 2, 64, 16, 9000, 300, True),
         (torch.bfloat16, torch.bfloat16, 3, 8, 2, 64, 16, 1000, 40, True),  # one-wave select, 16 keys per lane
+        (torch.bfloat16, torch.bfloat16, 3, 8, 2, 64, 16, 3000, 200, True),  # four-wave select, 16 keys per lane
+        (torch.float32, torch.float32, 2, 4, 2, 16, 5, 1500, 150, False),  # four-wave select, 8 keys per lane
         (torch.float32, torch.float32, 2, 4, 2, 16, 5, 513, 64, False),
         (torch.float32, torch.float32, 2, 4, 2, 64, 16, 40, 100, True),  # budget above the page count: -1 padding
         (torch.bfloat16, torch.bfloat16, 2, 96, 8, 128, 64, 300, 16, True),  # 12 query heads per KV head
@@ -367,9 +369,40 @@ def test_quest_special_values_match_oracle_and_reference(gpu, dtype, Hq, Hkv, D,
         check_page_set(pages[b].cpu(), reference_ranked(qb, lob, hib, int(lengths[b]), P, top), top)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("n_pages,top,P,nan_pages", [(1500, 64, 16, 0), (3000, 200, 16, 3), (4096, 256, 8, 0),
+                                                     (2100, 1, 16, 5), (1800, 33, 16, 40), (1025, 17, 4, 2)])
+def test_quest_select_ties_beyond_one_wave(gpu, n_pages, top, P, nan_pages):
+    """Beyond 1024 pages (the four-wave selector up to 4096): each request's
+    pages repeat six distinct bound rows, so pages tie in large groups across
+    all four waves, and request 2 holds NaN pages (tied above every number,
+    more of them than the budget in some cases). Pages, positions and scores
+    equal the oracle's: ties go to the lowest pages."""
+    log_case(test="quest-ties", n_pages=n_pages, top=top, P=P, nan_pages=nan_pages)
+    B, Hq, Hkv, D = 3, 8, 2, 64
+    g = torch.Generator().manual_seed(n_pages * 3 + top)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16)
+    lo6, hi6 = _bounds(g, B, 6, Hkv, D, torch.bfloat16, offsets=True)
+    idx = torch.randint(0, 6, (B, n_pages), generator=g)
+    mn = torch.stack([lo6[b, idx[b]] for b in range(B)])
+    mx = torch.stack([hi6[b, idx[b]] for b in range(B)])
+    for p in (torch.randperm(n_pages - 2, generator=g)[:nan_pages] + 1).tolist():
+        mx[2, p, 0, 5] = float("nan")
+    lengths = torch.tensor([n_pages * P, (n_pages - 300) * P - 1, n_pages * P - 3])
+    e_scores, e_pages, e_pos = oracle.quest_select(q, mn, mx, lengths, P, top, True)
+    pages, pos, scores = rk.quest_batched(q.to(gpu), mn.to(gpu), mx.to(gpu), lengths.to(gpu), P, top, True)
+    assert torch.equal(pages.cpu(), e_pages)
+    assert torch.equal(pos.cpu(), e_pos)
+    for b in range(B):
+        count = -(-int(lengths[b]) // P)
+        assert torch.equal(scores.cpu()[b, :count].view(torch.int32), e_scores[b, :count].view(torch.int32))
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,D,P,n_pages,top", [(4, 32, 8, 128, 64, 512, 32), (3, 4, 2, 8, 4, 20, 1),
                                                       (2, 4, 2, 8, 4, 20, 2), (2, 6, 3, 24, 5, 33, 7),
                                                       (2, 4, 2, 16, 8, 700, 50),
+                                                      (2, 4, 2, 16, 8, 2500, 100),  # four-wave select
+                                                      (2, 4, 2, 16, 8, 1100, 256),
                                                       (2, 24, 2, 100, 16, 60, 8),  # GQA 12, 25 lanes of 16 bytes
                                                       (2, 8, 2, 300, 16, 40, 6),  # 5 elements per lane
                                                       (1, 8, 2, 16, 2, 20000, 64)])  # beyond 16384 pages
