@@ -418,7 +418,9 @@ def run_resolver_stress(args):
     (28 query / 4 KV heads x 128, bf16), contexts uniform in [4096, 65536]
     (seeded), pages of 32, 32 pages = 1024 rows selected, 2048 hot rows per
     request all occupied (every step replaces LRU rows), fresh queries every
-    step; prints one JSON line (the step is selection + resolve only)."""
+    step; prints one JSON line (the step is selection + resolve only: Quest
+    scoring, then selection + resolution in one launch when the shape fits
+    it, as the batched decode runs them)."""
     import numpy as np
     import torch
 
@@ -465,9 +467,19 @@ def run_resolver_stress(args):
     totals = torch.zeros(3, dtype=torch.int64, device=device)
     ev = [[rk.timing_events(), rk.timing_events()] for _ in range(args.steps)]
 
+    # as the batched decode runs them: Quest scoring, then the selection
+    # inside the resolver launch when the shape fits it
+    fused = rk.fused_select_fits(n_pages, top, P)
+
     def step(i, events=None):
         if events:
             rk.set_launch_events(*events[0])
+        if fused:
+            _, _, scores = rk.quest_batched(queries[i], minimum, maximum, g_len, P, top, select=False)
+            if events:
+                rk.set_launch_events(*events[1])
+            return rk.select_resolve_batched(scores, g_src, g_res, g_hot, g_tags, g_lru, g_len, P, top,
+                                             counts_total=totals)[2]
         _, positions, _ = rk.quest_batched(queries[i], minimum, maximum, g_len, P, top)
         if events:
             rk.set_launch_events(*events[1])
@@ -519,13 +531,17 @@ def run_resolver_stress(args):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "resolver stress: Quest selection + row resolution (no gather/attention) for 64 requests, "
+            "workload": "resolver stress: Quest selection + row resolution (no gather/attention; the selection "
+            "inside the resolver launch, as the batched decode runs it) for 64 requests, "
             "Qwen2-7B heads 28q/4kv/128, bf16, contexts uniform in [4096, 65536], page 32, 1024 rows selected, "
             "2048 hot rows per request fully occupied, fresh queries every step",
             "batch": B,
             "parallelism": "single GPU",
         },
+        # fused: "quest" is the scoring launch and "resolve" the selection +
+        # resolution launch; otherwise Quest scoring + selection, then the resolver
         "kernel_us": {"quest": round(quest_us, 2), "resolve": round(resolve_us, 2)},
+        "fused_selection": fused,
         "rows_per_step": {"resident_hits": resident_hits, "hot_hits": hot_hits, "misses": misses},
         # attention over the same selections, timed separately (not part of value)
         "attention": {"launch_us": round(attn_us, 2), "algorithmic_bytes": attn_bytes,

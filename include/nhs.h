@@ -312,8 +312,9 @@ int nhs_resolve_items(int32_t batch, int32_t n, const void* positions, int32_t p
  * positions[b, :n] (n = top_pages * page_size) exactly as the selector
  * does, then nhs_resolve_rows on those n positions (int32, in order). Every
  * output is bit-identical to the selector launch followed by the resolver
- * launch. Requires max(max_pages, top_pages) <= 1024 and n <= 4096, else
- * returns NHS_ERR_UNSUPPORTED (the two launches handle any size). Tables,
+ * launch. Requires max(max_pages, top_pages) <= 1024, or max_pages <= 4096
+ * with top_pages <= 256, and n <= 4096, else returns NHS_ERR_UNSUPPORTED
+ * (the two launches handle any size). Tables,
  * outputs and plan_stride as nhs_resolve_rows; the selection stays in LDS,
  * so no launch boundary and no global round trip separate the two steps.
  * Replaces the sequence quest_selection / select_pages then resolve_rows

@@ -4,10 +4,11 @@
 //
 // The semantics are those of resolve_rows (nano_hisparse/row_index.py:62-140),
 // restated as LDS passes instead of sorts over the hot rows:
-//  0. (resolve_rows_kernel<KPL > 0>, nhs_select_resolve_*) wave 0 selects the
-//     top_pages best pages of the item's scores as the selectors do
-//     (wave_select, select_common.h) while the other waves stage the tables;
-//     the chosen pages expanded to tokens are the positions.
+//  0. (resolve_rows_kernel<KPL > 0>, nhs_select_resolve_*) wave 0 (or, beyond
+//     1024 pages, waves 0-3) selects the top_pages best pages of the item's
+//     scores as the selectors do (wave_rank / four_wave_rank,
+//     select_common.h) while the other waves stage the tables; the chosen
+//     pages expanded to tokens are the positions.
 //  1. keys (norm << 32 | input index), norm = raw if 0 <= raw < length else
 //     length, bitonic-sorted in LDS unless already in order: sorted order =
 //     ascending logical, and the first entry of each run of equal positions
@@ -44,7 +45,8 @@ constexpr int kHotCache = 1024; // hot blocks staged in LDS at entry
 constexpr int kWaves = kResolveThreads / 64;
 constexpr int kRankGroup = 4;   // 1024-slot chunks ranked per barrier
 constexpr int kTableCache = 2048;  // page table entries staged in LDS at entry
-constexpr int kFusedMaxPages = kWave * 16;  // pages the fused select ranks in one wave
+constexpr int kFusedWavePages = kWave * 16;      // pages the fused select ranks in one wave
+constexpr int kFusedMaxPages = 4 * kFusedWavePages;  // ... in four waves (at most kWavesMaxTop chosen)
 
 struct ResolveArgs {
   int n;  // positions per item
@@ -88,7 +90,7 @@ struct ResolveShared {
       uint64_t keys[kMaxK];           // phase 1-2
       int32_t src[kTableCache];       // the item's page tables, when they fit
       int32_t res[kTableCache];
-      int32_t chosen[kFusedMaxPages]; // fused selection: chosen pages, ascending, -1 padded
+      int32_t chosen[kFusedWavePages]; // fused selection: chosen pages, ascending, -1 padded
     } e;
     struct {
       int32_t hkey[kHashCap];  // phase 3-4: wanted host rows
@@ -276,13 +278,16 @@ __device__ __forceinline__ int hash_find(const int32_t* hkey, int32_t key) {
   }
 }
 
-// KPL = 0: the positions are read from a.positions. KPL = 8 or 16: wave 0
-// first selects the top_pages best of the request's page scores
-// (wave_select over up to kWave * KPL pages, as the selectors do) and the
-// positions are the chosen pages expanded to tokens, written to pages_out
-// and positions_out as the selectors write them; they come out sorted.
-template <int KPL>
+// KPL = 0: the positions are read from a.positions. KPL = 8 or 16: the
+// workgroup first selects the top_pages best of the request's page scores
+// as the selectors do (KPL2 = 0: wave 0, wave_rank over up to kWave * KPL
+// pages; KPL2 > 0: waves 0-3, four_wave_rank over up to 4 * kWave * KPL
+// pages with KPL2 candidates per lane) and the positions are the chosen
+// pages expanded to tokens, written to pages_out and positions_out as the
+// selectors write them; they come out sorted.
+template <int KPL, int KPL2 = 0>
 __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveArgs a) {
+  constexpr int kSelectors = KPL == 0 ? 0 : KPL2 > 0 ? 4 : 1;  // waves that rank the scores
   __shared__ ResolveShared sh;
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
@@ -292,10 +297,11 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   const int64_t length = a.lengths ? a.lengths[b] : a.length;
   int kp = 1;
   while (kp < n) kp <<= 1;
-  // fused selection: wave 0's score loads go first
+  // fused selection: the ranking waves' score loads go first
   float sv[KPL > 0 ? KPL : 1];
   if constexpr (KPL > 0)
-    if (tid < kWave) wave_scores<KPL>(a.scores + (int64_t)b * a.max_pages, a.max_pages, sv);
+    if (tid < kSelectors * kWave)
+      wave_scores_at<KPL>(a.scores + (int64_t)b * a.max_pages, a.max_pages, (int)(tid / kWave) * kWave * KPL, sv);
 
   // This item's tables: from its entry in the item table, or strided.
   const nhs_layer_item* item = a.items ? a.items + b : nullptr;
@@ -323,10 +329,10 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   NHS_GLOBAL const int32_t* hot = to_global(item ? item->hot : a.hot + (int64_t)b * a.hot_stride);
   // Tables staged in LDS: the hot block table and, when they fit, the page
   // tables, so the lookups below wait for no second global load. With the
-  // fused selection, wave 0 stages nothing: its LDS writes would wait for
-  // these loads before it could rank the scores.
-  const int stager = KPL > 0 ? (int)tid - kWave : (int)tid;
-  const int stagers = KPL > 0 ? kResolveThreads - kWave : kResolveThreads;
+  // fused selection, the ranking waves stage nothing: their LDS writes would
+  // wait for these loads before they could rank the scores.
+  const int stager = (int)tid - kSelectors * kWave;
+  const int stagers = kResolveThreads - kSelectors * kWave;
   if (hot_cached)
     for (int i = stager; i >= 0 && i < hot_blocks; i += stagers) sh.hot[i] = hot[i];
   const bool staged = n_pages >= 1 && n_pages <= kTableCache;
@@ -339,7 +345,15 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_rows_kernel(ResolveAr
   // ---- 0. fused selection --------------------------------------------------
   if constexpr (KPL > 0) {
     const int count = page_count(a.lengths, a.length, b, P, a.max_pages);
-    if (tid < kWave) wave_rank<KPL>(sv, count, a.top_pages, a.mode, a.keep_sink, a.forced_key, sh.u.e.chosen);
+    if constexpr (KPL2 == 0) {
+      if (tid < kWave) wave_rank<KPL>(sv, count, a.top_pages, a.mode, a.keep_sink, a.forced_key, sh.u.e.chosen);
+    } else {
+      // the candidates live in the key array, unused until phase 1
+      static_assert(sizeof(sh.u.e.keys) >= 8 * 4 * kWavesMaxTop, "candidates fit the key array");
+      uint32_t* cand = reinterpret_cast<uint32_t*>(sh.u.e.keys);
+      four_wave_rank<KPL, KPL2>(sv, count, a.top_pages, a.mode, a.keep_sink, a.forced_key, cand,
+                                reinterpret_cast<int32_t*>(cand + 4 * kWavesMaxTop), sh.red[0], sh.u.e.chosen);
+    }
     __syncthreads();
     for (int i = tid; i < a.top_pages; i += kResolveThreads) a.pages_out[(int64_t)b * a.top_pages + i] = sh.u.e.chosen[i];
   }
@@ -938,10 +952,11 @@ extern "C" int nhs_resolve_items(int32_t batch, int32_t n, const void* positions
 
 namespace nhs {
 
-// The fused launch: resolve_rows_kernel<8 or 16> over `batch` items whose
-// positions are their selections. Rejects shapes beyond one wave's
-// selection or the LDS-held entries with NHS_ERR_UNSUPPORTED, so that a
-// caller can fall back to a selector launch and a resolver launch.
+// The fused launch: resolve_rows_kernel<8 or 16, ...> over `batch` items
+// whose positions are their selections. Rejects shapes beyond the fused
+// selection (1024 pages, or 4096 with at most kWavesMaxTop chosen) or the
+// LDS-held entries with NHS_ERR_UNSUPPORTED, so that a caller can fall back
+// to a selector launch and a resolver launch.
 static int launch_select_resolve(const char* who, ResolveArgs& a, int32_t batch, const float* scores,
                                  int32_t max_pages, int32_t mode, int32_t top_pages, int32_t keep_sink,
                                  int32_t* pages, int32_t* positions, hipStream_t stream, const LaunchEvents& ev) {
@@ -949,9 +964,12 @@ static int launch_select_resolve(const char* who, ResolveArgs& a, int32_t batch,
   if (mode != kModeQuest && mode != kModeMean) return fail(NHS_ERR_INVALID, "%s: mode is 0 (Quest) or 1 (mean)", who);
   if (max_pages < 1 || top_pages < 1) return fail(NHS_ERR_INVALID, "%s: need max_pages, top_pages >= 1", who);
   const int wave_pages = max_pages > top_pages ? max_pages : top_pages;
-  if (wave_pages > kFusedMaxPages || (int64_t)top_pages * a.page_size > kMaxK)
-    return fail(NHS_ERR_UNSUPPORTED, "%s: max(max_pages, top_pages) <= %d and top_pages * page_size <= %d required",
-                who, kFusedMaxPages, kMaxK);
+  if ((wave_pages > kFusedWavePages && (wave_pages > kFusedMaxPages || top_pages > kWavesMaxTop)) ||
+      (int64_t)top_pages * a.page_size > kMaxK)
+    return fail(NHS_ERR_UNSUPPORTED,
+                "%s: max(max_pages, top_pages) <= %d, or max_pages <= %d with top_pages <= %d, and top_pages * "
+                "page_size <= %d required",
+                who, kFusedWavePages, kFusedMaxPages, kWavesMaxTop, kMaxK);
   a.scores = scores;
   a.max_pages = max_pages;
   a.top_pages = top_pages;
@@ -961,8 +979,17 @@ static int launch_select_resolve(const char* who, ResolveArgs& a, int32_t batch,
   a.pages_out = pages;
   a.positions_out = positions;
   if (batch == 0) return NHS_OK;
-  launch(wave_pages <= kWave * 8 ? resolve_rows_kernel<8> : resolve_rows_kernel<16>, dim3((unsigned)batch),
-         dim3(kResolveThreads), 0, stream, ev.start, ev.stop, a);
+  void (*kernel)(ResolveArgs);
+  const bool few = top_pages <= kWave;  // the four waves' <= 4 * top_pages candidates fit 4 per lane
+  if (wave_pages <= kWave * 8)
+    kernel = resolve_rows_kernel<8>;
+  else if (wave_pages <= kFusedWavePages)
+    kernel = resolve_rows_kernel<16>;
+  else if (wave_pages <= 4 * kWave * 8)
+    kernel = few ? resolve_rows_kernel<8, 4> : resolve_rows_kernel<8, 16>;
+  else
+    kernel = few ? resolve_rows_kernel<16, 4> : resolve_rows_kernel<16, 16>;
+  launch(kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0, stream, ev.start, ev.stop, a);
   return launch_status(who);
 }
 

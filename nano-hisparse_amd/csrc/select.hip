@@ -789,92 +789,23 @@ __global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectA
   write_selection(a, b, chosen, len);
 }
 
-// Up to 4 * kWave * KPL pages and kWavesMaxTop chosen: each of the four waves
-// ranks its own kWave * KPL pages (wave_topk) and keeps its best
-// min(top_pages, its pages) in LDS as candidates, in page order; wave 0 then
-// ranks the candidates, KPL2 per lane. A page outside its wave's best
-// top_pages has top_pages pages before it in (key descending, page
-// ascending) order, so the candidates hold the whole selection; and since
-// they stay in page order, ties still go to the lowest pages. The four waves
-// then expand the chosen pages to token positions.
-constexpr int kWavesMaxTop = 256;
+// Up to 4 * kWave * KPL pages and kWavesMaxTop chosen: the four waves rank
+// (four_wave_rank), then expand the chosen pages to token positions.
 template <int KPL, int KPL2>
 __global__ __launch_bounds__(kSelectWaveThreads) void select_waves_kernel(SelectArgs a) {
-  constexpr int NW = kSelectWaveThreads / kWave;
-  static_assert(NW == 4, "candidate offsets below assume four waves");
-  __shared__ uint32_t cand_key[NW][kWavesMaxTop];
-  __shared__ int32_t cand_page[NW][kWavesMaxTop];
-  __shared__ int n_cand[NW];
+  static_assert(kSelectWaveThreads == 4 * kWave, "four_wave_rank ranks with four waves");
+  __shared__ uint32_t cand_key[4 * kWavesMaxTop];
+  __shared__ int32_t cand_page[4 * kWavesMaxTop];
+  __shared__ int n_cand[4];
   __shared__ int32_t chosen[kWavesMaxTop];
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1), wave = tid / kWave;
   const int b = blockIdx.x;
-  const int base = wave * kWave * KPL;
-  // the score loads are issued before the page count arrives (pages past
-  // max_pages read page 0; values past count are never used)
-  const float* sc = a.scores + (int64_t)b * a.max_pages;
+  // the score loads are issued before the page count arrives
   float sv[KPL];
-#pragma unroll
-  for (int q = 0; q < KPL; ++q) {
-    const int p = base + q * kWave + lane;
-    sv[q] = sc[p < a.max_pages ? p : 0];
-  }
+  wave_scores_at<KPL>(a.scores + (int64_t)b * a.max_pages, a.max_pages, (int)(threadIdx.x / kWave) * kWave * KPL, sv);
   const int count = page_count(a.lengths, a.length, b, a.page_size, a.max_pages);
   const int64_t len = a.lengths ? a.lengths[b] : a.length;
-  const int top = a.top_pages;
-  if (top >= count) {
-    // every page is kept (count <= top <= kWavesMaxTop)
-    for (int i = tid; i < top; i += kSelectWaveThreads) chosen[i] = i < count ? i : -1;
-  } else {
-    const int mine = min(max(count - base, 0), kWave * KPL);  // this wave's pages
-    uint32_t key[KPL];
-    bool sel[KPL];
-#pragma unroll
-    for (int q = 0; q < KPL; ++q) {
-      const int p = base + q * kWave + lane;
-      key[q] = page_key(sv[q], p, count, a.mode, a.keep_sink, top, a.forced_key);
-      sel[q] = p < count;
-    }
-    if (top < mine) wave_topk<KPL>(key, top, sel);
-    int n = 0;
-#pragma unroll
-    for (int q = 0; q < KPL; ++q) {
-      const uint64_t m = __ballot(sel[q]);
-      if (sel[q]) {
-        const int i = n + lanes_below(m);
-        cand_key[wave][i] = key[q];
-        cand_page[wave][i] = base + q * kWave + lane;
-      }
-      n += __popcll(m);
-    }
-    if (lane == 0) n_cand[wave] = n;
-    __syncthreads();
-    if (wave == 0) {
-      // candidate j in page order: wave w's i-th, j = (its waves before) + i
-      const int n0 = n_cand[0], n1 = n0 + n_cand[1], n2 = n1 + n_cand[2], n3 = n2 + n_cand[3];
-      uint32_t key2[KPL2];
-      int32_t page2[KPL2];
-      bool sel2[KPL2];
-#pragma unroll
-      for (int q = 0; q < KPL2; ++q) {
-        const int j = q * kWave + lane;
-        const int w = j < n0 ? 0 : j < n1 ? 1 : j < n2 ? 2 : 3;
-        const int i = j - (w == 0 ? 0 : w == 1 ? n0 : w == 2 ? n1 : n2);
-        sel2[q] = j < n3;
-        key2[q] = sel2[q] ? cand_key[w][i] : 0u;
-        page2[q] = sel2[q] ? cand_page[w][i] : -1;
-      }
-      if (top < n3) wave_topk<KPL2>(key2, top, sel2);
-      int n_sel = 0;
-#pragma unroll
-      for (int q = 0; q < KPL2; ++q) {
-        const uint64_t m = __ballot(sel2[q]);
-        if (sel2[q]) chosen[n_sel + lanes_below(m)] = page2[q];
-        n_sel += __popcll(m);
-      }
-      for (int i = n_sel + lane; i < top; i += kWave) chosen[i] = -1;
-    }
-  }
+  four_wave_rank<KPL, KPL2>(sv, count, a.top_pages, a.mode, a.keep_sink, a.forced_key, cand_key, cand_page, n_cand,
+                            chosen);
   __syncthreads();
   write_selection(a, b, chosen, len);
 }

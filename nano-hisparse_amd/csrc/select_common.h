@@ -53,11 +53,21 @@ __device__ __forceinline__ int lanes_below(uint64_t mask) {
 // wave_rank selects from them into chosen (kWave * KPL entries). A caller
 // issues the score loads early, so that waiting for them does not also wait
 // for loads issued after them.
+// The scores of pages base + q * kWave + lane (slot q); pages past
+// max_pages read page 0.
 template <int KPL>
-__device__ __forceinline__ void wave_scores(const float* sc, int max_pages, float (&sv)[KPL]) {
+__device__ __forceinline__ void wave_scores_at(const float* sc, int max_pages, int base, float (&sv)[KPL]) {
   const int lane = threadIdx.x & (kWave - 1);
 #pragma unroll
-  for (int q = 0; q < KPL; ++q) sv[q] = sc[q * kWave + lane < max_pages ? q * kWave + lane : 0];
+  for (int q = 0; q < KPL; ++q) {
+    const int p = base + q * kWave + lane;
+    sv[q] = sc[p < max_pages ? p : 0];
+  }
+}
+
+template <int KPL>
+__device__ __forceinline__ void wave_scores(const float* sc, int max_pages, float (&sv)[KPL]) {
+  wave_scores_at<KPL>(sc, max_pages, 0, sv);
 }
 
 // Marks sel[q] for the top_pages best keys of a wave (slot q of lane l is
@@ -137,6 +147,83 @@ __device__ __forceinline__ void wave_rank(const float (&sv)[KPL], int count, int
     n_sel += __popcll(m);
   }
   for (int i = n_sel + lane; i < top_pages; i += kWave) chosen[i] = -1;
+}
+
+// Top-k of up to 4 * kWave * KPL pages, at most kWavesMaxTop chosen, by four
+// waves: each ranks its own kWave * KPL pages (wave_topk) and keeps its best
+// min(top_pages, its pages) as candidates in LDS, in page order; after a
+// barrier wave 0 ranks the candidates, KPL2 per lane (KPL2 * kWave >=
+// 4 * top_pages). A page outside its wave's best top_pages has top_pages
+// pages before it in (key descending, page ascending) order, so the
+// candidates hold the whole selection; and since they stay in page order,
+// ties still go to the lowest pages.
+// Called by every thread of a workgroup of at least four waves (it holds
+// one barrier). Wave w < 4 passes the scores of pages w * kWave * KPL +
+// q * kWave + lane in sv (wave_scores_at); other waves' sv are unused.
+// cand_key and cand_page hold 4 * kWavesMaxTop entries each and n_cand 4, in
+// LDS. Wave 0 writes chosen (top_pages entries, ascending, -1 padded),
+// complete after the caller's next barrier.
+constexpr int kWavesMaxTop = 256;
+template <int KPL, int KPL2>
+__device__ __forceinline__ void four_wave_rank(const float (&sv)[KPL], int count, int top_pages, int mode,
+                                               int keep_sink, uint32_t forced_key, uint32_t* cand_key,
+                                               int32_t* cand_page, int* n_cand, int32_t* chosen) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int top = top_pages;
+  if (top < count && wave < 4) {
+    const int base = wave * kWave * KPL;
+    const int mine = min(max(count - base, 0), kWave * KPL);  // this wave's pages
+    uint32_t key[KPL];
+    bool sel[KPL];
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) {
+      const int p = base + q * kWave + lane;
+      key[q] = page_key(sv[q], p, count, mode, keep_sink, top, forced_key);
+      sel[q] = p < count;
+    }
+    if (top < mine) wave_topk<KPL>(key, top, sel);
+    int n = 0;
+#pragma unroll
+    for (int q = 0; q < KPL; ++q) {
+      const uint64_t m = __ballot(sel[q]);
+      if (sel[q]) {
+        const int i = wave * kWavesMaxTop + n + lanes_below(m);
+        cand_key[i] = key[q];
+        cand_page[i] = base + q * kWave + lane;
+      }
+      n += __popcll(m);
+    }
+    if (lane == 0) n_cand[wave] = n;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  if (top >= count) {  // every page is kept
+    for (int i = lane; i < top; i += kWave) chosen[i] = i < count ? i : -1;
+    return;
+  }
+  // candidate j in page order: wave w's i-th, j = (the waves before) + i
+  const int n0 = n_cand[0], n1 = n0 + n_cand[1], n2 = n1 + n_cand[2], n3 = n2 + n_cand[3];
+  uint32_t key2[KPL2];
+  int32_t page2[KPL2];
+  bool sel2[KPL2];
+#pragma unroll
+  for (int q = 0; q < KPL2; ++q) {
+    const int j = q * kWave + lane;
+    const int w = j < n0 ? 0 : j < n1 ? 1 : j < n2 ? 2 : 3;
+    const int i = w * kWavesMaxTop + j - (w == 0 ? 0 : w == 1 ? n0 : w == 2 ? n1 : n2);
+    sel2[q] = j < n3;
+    key2[q] = sel2[q] ? cand_key[i] : 0u;
+    page2[q] = sel2[q] ? cand_page[i] : -1;
+  }
+  if (top < n3) wave_topk<KPL2>(key2, top, sel2);
+  int n_sel = 0;
+#pragma unroll
+  for (int q = 0; q < KPL2; ++q) {
+    const uint64_t m = __ballot(sel2[q]);
+    if (sel2[q]) chosen[n_sel + lanes_below(m)] = page2[q];
+    n_sel += __popcll(m);
+  }
+  for (int i = n_sel + lane; i < top; i += kWave) chosen[i] = -1;
 }
 
 template <int KPL>

@@ -468,7 +468,9 @@ def resolve_items(positions, items, hot_rows, lengths, page_size, counts_total=N
 
 # ---- fused selection + resolution ---------------------------------------------------
 
-FUSED_MAX_PAGES = 1024  # pages one wave ranks (nhs_select_resolve_*)
+FUSED_WAVE_PAGES = 1024  # pages one wave ranks (nhs_select_resolve_*)
+FUSED_MAX_PAGES = 4096  # pages four waves rank, choosing at most FUSED_MAX_TOP
+FUSED_MAX_TOP = 256
 FUSED_MAX_POSITIONS = 4096  # top_pages * page_size held in LDS
 MODES = {"quest": 0, "mean": 1}
 
@@ -476,7 +478,9 @@ MODES = {"quest": 0, "mean": 1}
 def fused_select_fits(max_pages, top_pages, page_size):
     """Whether nhs_select_resolve_* takes this shape (else a selector launch
     and a resolver launch do the same work)."""
-    return max(max_pages, top_pages) <= FUSED_MAX_PAGES and top_pages * page_size <= FUSED_MAX_POSITIONS
+    pages = max(max_pages, top_pages)
+    ranked = pages <= FUSED_WAVE_PAGES or (pages <= FUSED_MAX_PAGES and top_pages <= FUSED_MAX_TOP)
+    return ranked and top_pages * page_size <= FUSED_MAX_POSITIONS
 
 
 def select_resolve_batched(scores, source, resident, hot, tags, lru, lengths, page_size, top_pages, keep_sink=True,

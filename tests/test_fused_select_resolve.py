@@ -22,7 +22,11 @@ def log_case(**kw):
 def test_fused_select_fits_the_documented_limits():
     assert rk.fused_select_fits(512, 32, 64)
     assert rk.fused_select_fits(1024, 64, 64)  # 16 pages per lane, 4096 positions
-    assert not rk.fused_select_fits(1025, 32, 64)
+    assert rk.fused_select_fits(1024, 1024, 4)  # one wave: any budget up to its pages
+    assert rk.fused_select_fits(1025, 32, 64)  # four waves
+    assert rk.fused_select_fits(4096, 256, 16)
+    assert not rk.fused_select_fits(4097, 32, 64)
+    assert not rk.fused_select_fits(2048, 257, 8)  # four waves choose at most 256
     assert not rk.fused_select_fits(40, 1025, 1)
     assert not rk.fused_select_fits(512, 65, 64)
 
@@ -37,6 +41,12 @@ CASES = [
     ("quest", 3, 4, 2, 32, 7, 300, 1, 64, True, 2, 3),  # one page, odd page size
     ("mean", 4, 8, 2, 64, 32, 400, 20, 700, True, 3, 3),  # page-mean selector
     ("mean", 2, 4, 1, 32, 16, 900, 1, 128, True, 0, 2),
+    # beyond 1024 pages: four waves rank, 4 or 16 candidates per lane
+    ("quest", 4, 32, 8, 128, 64, 2048, 64, 4096, True, 0, 2),  # Llama-3-8B heads at 128K context
+    ("quest", 8, 28, 4, 128, 32, 2048, 32, 2048, True, 3, 2),  # Qwen2-7B heads at 64K context, NaN pages
+    ("quest", 3, 8, 2, 64, 4, 1500, 150, 700, False, 0, 3),  # 16 candidates per lane, no sink
+    ("mean", 2, 4, 1, 32, 16, 3000, 200, 4096, True, 4, 2),  # 16 pages per lane
+    ("quest", 2, 8, 2, 64, 16, 4096, 9, 300, True, 12, 2),  # more NaN pages than the budget
 ]
 
 
@@ -107,16 +117,19 @@ def test_fused_select_resolve_equals_select_then_resolve(gpu, mode, B, Hq, Hkv, 
 
 
 @pytest.mark.gpu
-def test_fused_select_resolve_rejects_shapes_beyond_one_wave(gpu):
+def test_fused_select_resolve_rejects_shapes_beyond_its_selection(gpu):
     log_case(test="select-resolve-limits")
-    B, H, P = 1, 64, 64
-    scores = torch.zeros(B, 1025, dtype=torch.float32, device=gpu)
-    tabs = [torch.zeros(B, 1025, dtype=torch.int32, device=gpu) for _ in range(2)]
-    hot = torch.zeros(B, 1, dtype=torch.int32, device=gpu)
+    B, H, P = 1, 64, 8
+    scores = torch.zeros(B, 4097, dtype=torch.float32, device=gpu)
+    tabs = [torch.zeros(B, 4097, dtype=torch.int32, device=gpu) for _ in range(2)]
+    hot = torch.zeros(B, 8, dtype=torch.int32, device=gpu)
     tags = torch.full((B, H), -1, dtype=torch.int32, device=gpu)
     lru = torch.arange(H, device=gpu)[None].clone()
-    with pytest.raises(RuntimeError, match="1024"):
-        rk.select_resolve_batched(scores, *tabs, hot, tags, lru, 1025 * P, P, 32)
-    with pytest.raises(RuntimeError, match="4096"):
+    with pytest.raises(RuntimeError, match="4096"):  # too many pages
+        rk.select_resolve_batched(scores, *tabs, hot, tags, lru, 4097 * P, P, 32)
+    with pytest.raises(RuntimeError, match="256"):  # four waves choose at most 256
+        rk.select_resolve_batched(scores[:, :2048], tabs[0][:, :2048], tabs[1][:, :2048], hot, tags, lru, 2048 * P,
+                                  P, 257)
+    with pytest.raises(RuntimeError, match="4096"):  # more positions than the LDS holds
         rk.select_resolve_batched(scores[:, :512], tabs[0][:, :512], tabs[1][:, :512], hot, tags, lru, 512 * P, P,
-                                  65)
+                                  513)
