@@ -133,3 +133,46 @@ def test_fused_select_resolve_rejects_shapes_beyond_its_selection(gpu):
     with pytest.raises(RuntimeError, match="4096"):  # more positions than the LDS holds
         rk.select_resolve_batched(scores[:, :512], tabs[0][:, :512], tabs[1][:, :512], hot, tags, lru, 512 * P, P,
                                   513)
+
+
+@pytest.mark.gpu
+def test_fused_four_wave_selection_replays_in_a_captured_graph(gpu):
+    """The four-wave fused launch (2048 pages, as the resolver-stress bench
+    replays it) captured once into a HIP graph and replayed step after step,
+    with eager work and a synchronization between the replays: every
+    replay's outputs and the evolving tags / LRU equal eager launches on a
+    copy of the same state."""
+    log_case(test="select-resolve-graph")
+    B, Hq, Hkv, D, P, n_pages, top, H = 3, 8, 2, 64, 16, 2048, 40, 1024
+    assert rk.fused_select_fits(n_pages, top, P) and n_pages > rk.FUSED_WAVE_PAGES
+    rng = np.random.default_rng(11)
+    g = torch.Generator().manual_seed(11)
+    lo, hi = (t.to(gpu) for t in _scores_inputs(g, "quest", B, Hq, Hkv, D, n_pages, 2, torch.bfloat16))
+    source, resident, hot, tags, lru = make_resolver_state(rng, B, H, P, n_pages, 2 * n_pages,
+                                                           n_pages + -(-H // P) + 8, 0.4, 0.6)
+    g_src, g_res, g_hot = (torch.from_numpy(x).to(gpu) for x in (source, resident, hot))
+    # three copies of the hot state: warm-up, graph, eager
+    (tags_w, lru_w), (tags_g, lru_g), (tags_e, lru_e) = [
+        (torch.from_numpy(tags).to(gpu), torch.from_numpy(lru).to(gpu)) for _ in range(3)]
+    lengths = torch.from_numpy(rng.integers((n_pages - 3) * P, n_pages * P + 1, size=B)).to(gpu)
+    scores = []
+    for _ in range(4):
+        q = torch.randn(B, Hq, D, generator=g).to(gpu, torch.bfloat16)
+        scores.append(rk.quest_batched(q, lo, hi, lengths, P, top, select=False)[2])
+    static = scores[0].clone()
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        rk.select_resolve_batched(static, g_src, g_res, g_hot, tags_w, lru_w, lengths, P, top)
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        outs = rk.select_resolve_batched(static, g_src, g_res, g_hot, tags_g, lru_g, lengths, P, top)
+    for step in range(4):
+        static.copy_(scores[step])
+        graph.replay()
+        want = rk.select_resolve_batched(scores[step], g_src, g_res, g_hot, tags_e, lru_e, lengths, P, top)
+        torch.cuda.synchronize()
+        for name, x, y in zip(("pages", "positions", "physical", "miss_host", "miss_device", "counts"), outs, want):
+            assert torch.equal(x, y), (step, name)
+        assert torch.equal(tags_g, tags_e) and torch.equal(lru_g, lru_e), step
