@@ -4,11 +4,11 @@
 //
 // The semantics are those of resolve_rows (nano_hisparse/row_index.py:62-140),
 // restated as LDS passes instead of sorts over the hot rows:
-//  0. (resolve_rows_kernel<KPL > 0>, nhs_select_resolve_*) wave 0 (or, beyond
-//     1024 pages, waves 0-3) selects the top_pages best pages of the item's
-//     scores as the selectors do (wave_rank / four_wave_rank,
-//     select_common.h) while the other waves stage the tables; the chosen
-//     pages expanded to tokens are the positions.
+//  0. (resolve_rows_kernel<KPL > 0>, nhs_select_resolve_*) waves 0-3 (wave 0
+//     alone when more than 256 pages are chosen) select the top_pages best
+//     pages of the item's scores as the selectors do (four_wave_rank /
+//     wave_rank, select_common.h) while the other waves stage the tables;
+//     the chosen pages expanded to tokens are the positions.
 //  1. keys (norm << 32 | input index), norm = raw if 0 <= raw < length else
 //     length, bitonic-sorted in LDS unless already in order: sorted order =
 //     ascending logical, and the first entry of each run of equal positions
@@ -952,8 +952,10 @@ extern "C" int nhs_resolve_items(int32_t batch, int32_t n, const void* positions
 
 namespace nhs {
 
-// The fused launch: resolve_rows_kernel<8 or 16, ...> over `batch` items
-// whose positions are their selections. Rejects shapes beyond the fused
+// The fused launch: resolve_rows_kernel<KPL, KPL2> over `batch` items whose
+// positions are their selections: four ranking waves (KPL pages per lane
+// each, KPL2 candidates per lane) when at most kWavesMaxTop pages are
+// chosen, else one (up to 1024 pages). Rejects shapes beyond the fused
 // selection (1024 pages, or 4096 with at most kWavesMaxTop chosen) or the
 // LDS-held entries with NHS_ERR_UNSUPPORTED, so that a caller can fall back
 // to a selector launch and a resolver launch.
@@ -980,15 +982,19 @@ static int launch_select_resolve(const char* who, ResolveArgs& a, int32_t batch,
   a.positions_out = positions;
   if (batch == 0) return NHS_OK;
   void (*kernel)(ResolveArgs);
-  const bool few = top_pages <= kWave;  // the four waves' <= 4 * top_pages candidates fit 4 per lane
-  if (wave_pages <= kWave * 8)
-    kernel = resolve_rows_kernel<8>;
-  else if (wave_pages <= kFusedWavePages)
-    kernel = resolve_rows_kernel<16>;
+  // four ranking waves whenever at most kWavesMaxTop are chosen; candidates
+  // per lane for their <= 4 * top_pages candidates
+  const int c = 4 * top_pages;
+  if (top_pages > kWavesMaxTop)
+    kernel = wave_pages <= kWave * 8 ? resolve_rows_kernel<8> : resolve_rows_kernel<16>;
+  else if (wave_pages <= 4 * kWave * 2)
+    kernel = c <= 2 * kWave ? resolve_rows_kernel<2, 2> : c <= 4 * kWave ? resolve_rows_kernel<2, 4> : resolve_rows_kernel<2, 16>;
+  else if (wave_pages <= 4 * kWave * 4)
+    kernel = c <= 2 * kWave ? resolve_rows_kernel<4, 2> : c <= 4 * kWave ? resolve_rows_kernel<4, 4> : resolve_rows_kernel<4, 16>;
   else if (wave_pages <= 4 * kWave * 8)
-    kernel = few ? resolve_rows_kernel<8, 4> : resolve_rows_kernel<8, 16>;
+    kernel = c <= 2 * kWave ? resolve_rows_kernel<8, 2> : c <= 4 * kWave ? resolve_rows_kernel<8, 4> : resolve_rows_kernel<8, 16>;
   else
-    kernel = few ? resolve_rows_kernel<16, 4> : resolve_rows_kernel<16, 16>;
+    kernel = c <= 2 * kWave ? resolve_rows_kernel<16, 2> : c <= 4 * kWave ? resolve_rows_kernel<16, 4> : resolve_rows_kernel<16, 16>;
   launch(kernel, dim3((unsigned)batch), dim3(kResolveThreads), 0, stream, ev.start, ev.stop, a);
   return launch_status(who);
 }

@@ -41,6 +41,9 @@ CASES = [
     ("quest", 3, 4, 2, 32, 7, 300, 1, 64, True, 2, 3),  # one page, odd page size
     ("mean", 4, 8, 2, 64, 32, 400, 20, 700, True, 3, 3),  # page-mean selector
     ("mean", 2, 4, 1, 32, 16, 900, 1, 128, True, 0, 2),
+    # more than 256 chosen: wave 0 ranks alone, 8 or 16 pages per lane
+    ("quest", 2, 8, 2, 64, 4, 900, 300, 1400, True, 3, 2),
+    ("mean", 2, 4, 1, 32, 2, 500, 400, 900, True, 0, 2),
     # beyond 1024 pages: four waves rank, 4 or 16 candidates per lane
     ("quest", 4, 32, 8, 128, 64, 2048, 64, 4096, True, 0, 2),  # Llama-3-8B heads at 128K context
     ("quest", 8, 28, 4, 128, 32, 2048, 32, 2048, True, 3, 2),  # Qwen2-7B heads at 64K context, NaN pages
