@@ -773,8 +773,9 @@ __device__ __forceinline__ void write_selection(const SelectArgs& a, int b, cons
   }
 }
 
-// Up to kWave * KPL pages: wave 0 selects (wave_select), then the four waves
-// expand the chosen pages to token positions.
+// Up to kWave * KPL pages, for more than kWavesMaxTop chosen: wave 0 selects
+// (wave_select), then the four waves expand the chosen pages to token
+// positions.
 template <int KPL>
 __global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectArgs a) {
   __shared__ int32_t chosen[kWave * KPL];
@@ -789,8 +790,10 @@ __global__ __launch_bounds__(kSelectWaveThreads) void select_wave_kernel(SelectA
   write_selection(a, b, chosen, len);
 }
 
-// Up to 4 * kWave * KPL pages and kWavesMaxTop chosen: the four waves rank
-// (four_wave_rank), then expand the chosen pages to token positions.
+// Up to 4 * kWave * KPL pages and kWavesMaxTop chosen (the selectors' kernel
+// whenever at most kWavesMaxTop pages are chosen, up to 4096 pages): the
+// four waves rank (four_wave_rank), then expand the chosen pages to token
+// positions.
 template <int KPL, int KPL2>
 __global__ __launch_bounds__(kSelectWaveThreads) void select_waves_kernel(SelectArgs a) {
   static_assert(kSelectWaveThreads == 4 * kWave, "four_wave_rank ranks with four waves");
@@ -954,28 +957,34 @@ static int quest_chunk_elems(int head_dim, int esize) {
 static int launch_select(const SelectArgs& s, int batch, hipStream_t stream, const char* who, hipEvent_t start,
                          hipEvent_t stop) {
   const int wave_pages = s.max_pages > s.top_pages ? s.max_pages : s.top_pages;
-  if (wave_pages > NHS_MAX_SELECT_PAGES)
+  if (wave_pages > NHS_MAX_SELECT_PAGES) {
     launch(select_large_kernel, dim3((unsigned)batch), dim3(kSelectLargeThreads), 0, stream, start, stop, s);
-  else if (wave_pages <= kWave * 8)
-    launch(select_wave_kernel<8>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
-  else if (wave_pages <= kWave * 16)
-    launch(select_wave_kernel<16>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
-  else if (wave_pages <= 4 * kWave * 16 && s.top_pages <= kWavesMaxTop) {
-    // four waves' candidates, at most 4 * top_pages of them
+  } else if (wave_pages <= 4 * kWave * 16 && s.top_pages <= kWavesMaxTop) {
+    // four ranking waves (KPL pages per lane each) and their <= 4 * top_pages
+    // candidates, KPL2 per lane
     const int c = 4 * s.top_pages;
+    const int kpl = wave_pages <= 4 * kWave * 2 ? 2 : wave_pages <= 4 * kWave * 4 ? 4 : wave_pages <= 4 * kWave * 8 ? 8 : 16;
+    const int kpl2 = c <= 2 * kWave ? 2 : c <= 4 * kWave ? 4 : 16;
     void (*k)(SelectArgs) = nullptr;
-    if (wave_pages <= 4 * kWave * 8)
-      k = c <= 2 * kWave ? select_waves_kernel<8, 2> : c <= 4 * kWave ? select_waves_kernel<8, 4>
-        : c <= 8 * kWave ? select_waves_kernel<8, 8> : select_waves_kernel<8, 16>;
-    else
-      k = c <= 2 * kWave ? select_waves_kernel<16, 2> : c <= 4 * kWave ? select_waves_kernel<16, 4>
-        : c <= 8 * kWave ? select_waves_kernel<16, 8> : select_waves_kernel<16, 16>;
+    switch (kpl * 32 + kpl2) {
+#define NHS_WAVES_CASE(A, B) \
+  case A * 32 + B: k = select_waves_kernel<A, B>; break;
+      NHS_WAVES_CASE(2, 2) NHS_WAVES_CASE(2, 4) NHS_WAVES_CASE(2, 16)
+      NHS_WAVES_CASE(4, 2) NHS_WAVES_CASE(4, 4) NHS_WAVES_CASE(4, 16)
+      NHS_WAVES_CASE(8, 2) NHS_WAVES_CASE(8, 4) NHS_WAVES_CASE(8, 16)
+      NHS_WAVES_CASE(16, 2) NHS_WAVES_CASE(16, 4) NHS_WAVES_CASE(16, 16)
+#undef NHS_WAVES_CASE
+    }
     launch(k, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
-  }
-  else if (s.max_pages <= 256 * kMaxSelectPerThread)
+  } else if (wave_pages <= kWave * 8) {
+    launch(select_wave_kernel<8>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
+  } else if (wave_pages <= kWave * 16) {
+    launch(select_wave_kernel<16>, dim3((unsigned)batch), dim3(kSelectWaveThreads), 0, stream, start, stop, s);
+  } else if (s.max_pages <= 256 * kMaxSelectPerThread) {
     launch(select_topk_kernel<256>, dim3((unsigned)batch), dim3(256), 0, stream, start, stop, s);
-  else
+  } else {
     launch(select_topk_kernel<kSelectThreads>, dim3((unsigned)batch), dim3(kSelectThreads), 0, stream, start, stop, s);
+  }
   return launch_status(who);
 }
 

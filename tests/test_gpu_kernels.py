@@ -290,7 +290,9 @@ def _bounds(g, B, n_pages, Hkv, D, dtype, offsets=False):
         (torch.float16, torch.float32, 2, 6, 2, 24, 7, 30, 5, True),
         (torch.float32, torch.float32, 2, 2, 1, 2, 2, 3, 2, False),  # head_dim 2 (element lanes)
         (torch.bfloat16, torch.bfloat16, 2, 8, 2, 64, 16, 9000, 300, True),
-        (torch.bfloat16, torch.bfloat16, 3, 8, 2, 64, 16, 1000, 40, True),  # one-wave select, 16 keys per lane
+        (torch.bfloat16, torch.bfloat16, 3, 8, 2, 64, 16, 1000, 40, True),  # four-wave select, 4 keys per lane
+        (torch.bfloat16, torch.bfloat16, 2, 8, 2, 64, 4, 900, 300, True),  # 300 chosen: one-wave select, 16 per lane
+        (torch.bfloat16, torch.bfloat16, 2, 8, 2, 64, 4, 400, 260, False),  # 260 chosen: one-wave select, 8 per lane
         (torch.bfloat16, torch.bfloat16, 3, 8, 2, 64, 16, 3000, 200, True),  # four-wave select, 16 keys per lane
         (torch.float32, torch.float32, 2, 4, 2, 16, 5, 1500, 150, False),  # four-wave select, 8 keys per lane
         (torch.float32, torch.float32, 2, 4, 2, 16, 5, 513, 64, False),
