@@ -622,7 +622,7 @@ def model_decode(args, B, L, T, K, W):
     print(f"[bench] cache: {kv.gpu_pages} pool blocks ({kv.gpu_pages * kv.row_bytes * P / 2**30:.1f} GiB), "
           f"{kv.host_pages} host pages ({kv.host_pages * kv.row_bytes * P / 2**30:.1f} GiB pinned), "
           f"{time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
-    graph = bool(args.graph) and args.micro_batches == 1
+    graph = bool(args.graph)
     engine = Engine(model, cache, top_k=top, batch_decode=True, micro_batches=args.micro_batches, graph=graph)
     gen = torch.Generator().manual_seed(args.seed)
     for b in range(B):

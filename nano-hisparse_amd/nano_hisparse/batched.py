@@ -173,12 +173,31 @@ class BatchDecode:
         for t in tables:
             t.ready = None
 
+    def clear_reads(self):
+        """Make the compute and transfer streams wait now for the last read
+        of every table of the batch (all layers) and drop those events, so
+        that the launches that follow, gathers on the transfer stream
+        included, wait for none (as launches captured into a graph cannot);
+        end() records the step's own."""
+        store = self.cache.storage
+        tables = [self.cache.tables[rid, layer] for layer in range(self.layers) for rid in self.ids]
+        for stream in (store.compute, store.transfer):
+            _wait_all(store, stream, (t.last_use for t in tables))
+        for t in tables:
+            t.last_use = None
+
+    def forget_capture_events(self):
+        """Drop the events a captured (not executed) step left on the batch's
+        tables: they belong to the graph and are never recorded."""
+        for layer in range(self.layers):
+            for rid in self.ids:
+                t = self.cache.tables[rid, layer]
+                t.ready = t.last_use = None
+
     def account_replayed(self):
         """Host state of a step whose launches were replayed from a captured
         graph of a step over the same batch: every layer appended and
-        attended, gathers in order on the compute stream."""
-        if self.overlap:
-            raise RuntimeError("replayed steps gather on the compute stream")
+        attended (the graph's gathers ran inside it, in its order)."""
         for layer in range(self.layers):
             self._account_append(layer)
             self._attended.add(layer)
@@ -254,7 +273,8 @@ class BatchDecode:
             for t in tables:
                 t.ready = None  # in order on the compute stream
             return layer, query, physical, None
-        resolved = store.event(store.compute)
+        compute = store.active_compute()
+        resolved = store.event(compute)
         store.wait(store.transfer, resolved)
         _wait_all(store, store.transfer, (t.last_use for t in tables))
         with store.context(store.transfer):
@@ -271,7 +291,7 @@ class BatchDecode:
         """Attention over the selected rows once their gather is done."""
         layer, query, physical, gathered = handle
         cache, store = self.cache, self.cache.storage
-        store.wait(store.compute, gathered)
+        store.wait(store.active_compute(), gathered)
         out = rk.attend_batched(query, cache.pool, physical, cache.config.page_size)
         self._attended.add(layer)
         return out

@@ -275,16 +275,26 @@ class Model(nn.Module):
             raise ValueError("batched decode needs a positive Quest top_k")
         if micro_batches not in (1, 2):
             raise ValueError("micro_batches must be 1 or 2")
-        if graph:
-            if micro_batches != 1:
-                raise ValueError("graph replay runs one group")
-            return self._decode_batch_graph(tokens, request_ids, cache, top_k)
         n = len(tokens)
         if n < 2:
             micro_batches = 1
         cuts = [0, n] if micro_batches == 1 else [0, (n + 1) // 2, n]
+        if graph:
+            return self._decode_batch_graph(tokens, request_ids, cache, top_k, cuts)
         overlap = len(cuts) > 2
         groups = [_Group(self, tokens[a:b], request_ids[a:b], cache, overlap) for a, b in zip(cuts, cuts[1:])]
+        logits = self._run_groups(groups, top_k)
+        for g in groups:
+            g.step.end()
+        return logits
+
+    def _run_groups(self, groups, top_k):
+        """Every layer of one group, or of two groups half a layer apart (each
+        group's gather on the transfer stream beside the other's compute,
+        with the gather's grid capped meanwhile), then the final norm and the
+        lm_head; returns the logits."""
+        from . import row_kernels as rk
+
         fused = self._fused_projections()
         layers = self.model.layers
         if len(groups) == 1:
@@ -308,69 +318,82 @@ class Model(nn.Module):
                         b.pre(index + 1, layers[index + 1], fused[index + 1], top_k)
             finally:
                 rk.set_gather_workgroups(0)
-        for g in groups:
-            g.step.end()
-        x = torch.cat([g.x + g.delta for g in groups])
+        x = groups[0].x + groups[0].delta if len(groups) == 1 else torch.cat([g.x + g.delta for g in groups])
         return _linear(self.model.norm(x), self.lm_head.weight, self.lm_head.bias).float()
 
 
-    def _decode_batch_graph(self, tokens, request_ids, cache, top_k):
-        """decode_batch with the step's launches (every layer, the final norm
-        and the lm_head) captured once per batch composition into a HIP graph
-        and replayed from then on.
+    def _decode_batch_graph(self, tokens, request_ids, cache, top_k, cuts):
+        """decode_batch with the step's launches (every layer of every group,
+        the final norm and the lm_head) captured once per batch composition
+        into a HIP graph and replayed from then on. With two groups (cuts
+        [0, m, n]) the capture holds both groups' schedule: each gather is a
+        branch forked from the capture stream by an event and joined back by
+        the attention that waits for it, so the replay runs it beside the
+        other group's compute as the eager steps do.
 
         Per step, outside the graph: the page placement and residency policy
         (BatchDecode's constructor; its table writes precede the replay on
         the compute stream), the upload of the lengths and token ids into the
-        buffers the graph reads, the wait for the tables' pending events, and
-        after the replay the pages' host state and the policy tick (end()).
-        Every launch's shape depends only on the batch, the budget and the
-        requests' reserved pages, so the replayed step is the eager one. A
-        graph is reused only while the cache's device item table of the
-        composition is the same object (it holds the pointers the graph
+        buffers the graph reads, the waits for the tables' pending events,
+        and after the replay the pages' host state and the policy tick
+        (end()). Every launch's shape depends only on the batch, the budget
+        and the requests' reserved pages, so the replayed step is the eager
+        one. A graph is reused only while the cache's device item tables of
+        the groups are the same objects (they hold the pointers the graph
         read); otherwise it is captured again."""
         store = cache.storage
         store.check_stream()
         graphs = self.__dict__.setdefault("_decode_graphs", {})
-        key = (tuple(request_ids), top_k)
-        items = cache._layer_items(request_ids)
+        spans = list(zip(cuts, cuts[1:]))
+        overlap = len(spans) > 1
+        key = (tuple(request_ids), top_k, len(spans))
+        items = [cache._layer_items(request_ids[a:b]) for a, b in spans]
         entry = graphs.get(key)
-        if entry is not None and (entry["cache"] is not cache or entry["items"] is not items):
+        if entry is not None and (entry["cache"] is not cache or any(x is not y for x, y in zip(entry["items"], items))):
             del graphs[key]
             entry = None
-        n = len(tokens)
-        token_ids = torch.tensor(tokens, dtype=torch.int64).pin_memory()
+        token_ids = [torch.tensor(tokens[a:b], dtype=torch.int64).pin_memory() for a, b in spans]
+
+        def open_steps(buffers):
+            steps = []
+            for (a, b), (lengths, _) in zip(spans, buffers):
+                step = cache.decode_batch(request_ids[a:b], overlap, lengths_buffer=lengths)
+                step.sync_tables()
+                step.clear_reads()
+                steps.append(step)
+            for (_, ids), t in zip(buffers, token_ids):
+                ids.copy_(t, non_blocking=True)
+            return steps
+
         if entry is None:
-            lengths = torch.empty(2, n, dtype=torch.int64, device=cache.device)
-            ids = torch.empty(n, dtype=torch.int64, device=cache.device)
-            step = cache.decode_batch(request_ids, lengths_buffer=lengths)
-            step.sync_tables()
-            ids.copy_(token_ids, non_blocking=True)
-            fused = self._fused_projections()
+            buffers = [(torch.empty(2, b - a, dtype=torch.int64, device=cache.device),
+                        torch.empty(b - a, dtype=torch.int64, device=cache.device)) for a, b in spans]
+            steps = open_steps(buffers)
             graph = torch.cuda.CUDAGraph()
             side = torch.cuda.Stream(device=cache.device)
             side.wait_stream(store.compute)
+            if overlap:
+                side.wait_stream(store.transfer)
             with store.capturing(side), torch.cuda.graph(graph, stream=side):
-                group = _Group(self, None, request_ids, cache, False, step=step, ids=ids)
-                for index, layer in enumerate(self.model.layers):
-                    group.pre(index, layer, fused[index], top_k)
-                    group.post(layer)
-                x = group.x + group.delta
-                logits = _linear(self.model.norm(x), self.lm_head.weight, self.lm_head.bias).float()
+                groups = [_Group(self, None, request_ids[a:b], cache, overlap, step=step, ids=ids)
+                          for (a, b), step, (_, ids) in zip(spans, steps, buffers)]
+                logits = self._run_groups(groups, top_k)
+            for step in steps:
+                step.forget_capture_events()
             # the capture stream lives as long as the graph: buffers cached per stream during the capture
             # (the attention workspace) belong to the graph's memory
-            entry = {"cache": cache, "items": items, "lengths": lengths, "ids": ids, "graph": graph,
-                     "logits": logits, "stream": side}
+            entry = {"cache": cache, "items": items, "buffers": buffers, "graph": graph, "logits": logits,
+                     "stream": side}
             graphs[key] = entry
             while len(graphs) > 8:  # the most recent compositions keep their graphs
                 del graphs[next(iter(graphs))]
         else:
-            step = cache.decode_batch(request_ids, lengths_buffer=entry["lengths"])
-            step.sync_tables()
-            entry["ids"].copy_(token_ids, non_blocking=True)
-            step.account_replayed()
+            steps = open_steps(entry["buffers"])
+            for step in steps:
+                step.account_replayed()
         entry["graph"].replay()
-        step.end()
+        for step in steps:
+            step.end()
         return entry["logits"].clone()
 
 

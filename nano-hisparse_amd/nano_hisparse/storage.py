@@ -219,6 +219,11 @@ class HostStore:
         if event is not None:
             stream.wait_event(event)
 
+    def active_compute(self):
+        """The stream cache work runs on now: the capture stream while a
+        graph is being captured (capturing()), else the compute stream."""
+        return self._capture_stream if self._capture_stream is not None else self.compute
+
     def check_stream(self):
         if self.cuda and torch.cuda.current_stream(self.device) not in (self.compute, self._capture_stream):
             raise RuntimeError("cache operations must use the construction compute stream")

@@ -197,15 +197,18 @@ def test_engine_batch_decode_generates_the_sequential_tokens(gpu, micro_batches)
 
 
 @pytest.mark.gpu
-def test_graph_replayed_decode_equals_the_eager_decode(gpu):
+@pytest.mark.parametrize("micro_batches", [1, 2])
+def test_graph_replayed_decode_equals_the_eager_decode(gpu, micro_batches):
     """Engine(graph=True) replays each batch composition's step from a HIP
     graph captured at its first step. Run in lockstep with an eager batched
     engine on the same model and prompts (separate caches of one config),
     over admissions (each new composition is captured) and a finished
     request, with the engines' own host work and synchronisations between
     the replays: every step's logits are equal bit for bit, and so are the
-    tokens. Projections of this model all take nhs_linear_small_m."""
-    log_case(test="decode-graph")
+    tokens. Projections of this model all take nhs_linear_small_m. With two
+    micro-batches the graph holds both groups' schedule, each gather a branch
+    on the transfer stream beside the other group's compute."""
+    log_case(test="decode-graph", micro_batches=micro_batches)
     cfg = ModelConfig(vocab_size=32000, hidden_size=2048, intermediate_size=4096, num_hidden_layers=2,
                       num_attention_heads=16, num_key_value_heads=4)
     torch.manual_seed(7)
@@ -225,7 +228,8 @@ def test_graph_replayed_decode_equals_the_eager_decode(gpu):
     def engine(graph):
         kv = CacheConfig(gpu_pages=3 * hot.admission_blocks(P, 2) + 16, host_pages=3 * 2 * 24, page_size=P,
                          kv_heads=4, head_dim=128, dtype=torch.bfloat16, device=str(gpu))
-        e = Engine(model, HybridKVCache(kv, hot), top_k=top, batch_decode=True, graph=graph)
+        e = Engine(model, HybridKVCache(kv, hot), top_k=top, batch_decode=True, graph=graph,
+                   micro_batches=micro_batches)
         for i, (prompt, n) in enumerate(zip(prompts, budgets)):
             e.add_request(f"r{i}", prompt, n)
         return e
