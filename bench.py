@@ -175,7 +175,7 @@ class Layer:
         rng = torch.Generator().manual_seed(seed + 1)
         hot_blocks = self.H // P
         per_req_blocks = hot_blocks + resident_pages
-        self.pool = torch.empty(B * per_req_blocks, 2, P, Hkv, D, dtype=dtype, device=device)
+        self.pool = rk.padded_pool(B * per_req_blocks, P, Hkv, D, dtype, device)
         source = torch.arange(B * n_pages, dtype=torch.int32).view(B, n_pages)
         resident = torch.full((B, n_pages), -1, dtype=torch.int32)
         hot = torch.empty(B, hot_blocks, dtype=torch.int32)
@@ -375,7 +375,7 @@ def run_attention_shapes(args):
         nbytes = B * N * 2 * Hkv * D * 2 + B * (2 * Hq * D * 2 + 8 * N)
         n_sets = max(4, -(-(512 << 20) // nbytes) + 1)
         blocks = n_sets * B * pages
-        pool = torch.empty(blocks, 2, P, Hkv, D, dtype=torch.bfloat16, device=dev)
+        pool = rk.padded_pool(blocks, P, Hkv, D, torch.bfloat16, dev)
         for i in range(0, blocks, 512):
             pool[i:i + 512].normal_(generator=g)
         perm = torch.randperm(blocks, generator=g, device=dev)
@@ -522,7 +522,9 @@ def run_resolver_stress(args):
 
     # attention at the same shape (untimed by the step above): the last
     # step's rows over a pool of random bf16 K/V, per-launch time from events
-    pool = torch.randn(next_block, 2, P, Hkv, D, generator=g, device=device).to(torch.bfloat16)
+    pool = rk.padded_pool(next_block, P, Hkv, D, torch.bfloat16, device)
+    for i in range(0, next_block, 512):
+        pool[i:i + 512].copy_(torch.randn(pool[i:i + 512].shape, generator=g, device=device))
     out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=device)
     attn_q = queries[-1]
     for _ in range(3):

@@ -19,6 +19,12 @@
  *   host  [host_pages, 2, page_size, kv_heads, head_dim] (pinned, same layout)
  *   A physical row r lives in block r / page_size at offset r % page_size;
  *   its K bytes and its V bytes are each kv_heads*head_dim contiguous elements.
+ *   Host blocks are contiguous. Pool blocks are pool_block_stride bytes apart
+ *   (0: contiguous, 2*page_size*kv_heads*head_dim elements); a larger stride
+ *   leaves a gap after each block. The cache pads each block by three head
+ *   slots (3*head_dim elements), so that consecutive blocks shift a KV head's
+ *   bytes by three head slots in the address: HBM then serves every KV head
+ *   at the same rate (with contiguous blocks some heads' slots are slower).
  */
 #ifndef NHS_H
 #define NHS_H
@@ -102,7 +108,7 @@ int nhs_host_device_ptr(const void* pinned_host, void** device_alias);
 int nhs_gather_rows(const void* host_alias, void* pool,
                     const int64_t* miss_host_rows, const int64_t* miss_device_rows,
                     int64_t n_entries, int32_t page_size, int64_t plane_bytes,
-                    void* stream);
+                    int64_t pool_block_stride, void* stream);
 
 /*
  * Caps the workgroups of every later nhs_gather_rows launch (process-wide;
@@ -137,8 +143,8 @@ int64_t nhs_attend_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_
                                    int32_t n_rows);
 int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_batch_stride,
                     int64_t q_head_stride, const void* pool, int32_t kv_dtype,
-                    const int64_t* rows, int64_t rows_batch_stride, int64_t rows_head_stride,
-                    int64_t rows_col_stride, int32_t batch, int32_t n_rows, int32_t q_heads,
+                    int64_t pool_block_stride, const int64_t* rows, int64_t rows_batch_stride,
+                    int64_t rows_head_stride, int64_t rows_col_stride, int32_t batch, int32_t n_rows, int32_t q_heads,
                     int32_t kv_heads, int32_t head_dim, int32_t page_size, void* out,
                     int64_t out_batch_stride, int64_t out_head_stride, void* workspace,
                     int64_t workspace_bytes, void* stream);
@@ -157,7 +163,7 @@ int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_batch_stride,
 #define NHS_ATTEND_NOALLOC_BYTES (32ll << 20)
 int nhs_attend_rows_noalloc(const void* query, int32_t q_dtype, int64_t q_batch_stride,
                             int64_t q_head_stride, const void* pool, int32_t kv_dtype,
-                            const int64_t* rows, int64_t rows_batch_stride,
+                            int64_t pool_block_stride, const int64_t* rows, int64_t rows_batch_stride,
                             int64_t rows_head_stride, int64_t rows_col_stride, int32_t batch,
                             int32_t n_rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
                             int32_t page_size, void* out, int64_t out_batch_stride,
@@ -260,7 +266,8 @@ int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype, int64_t q
  * complete when the kernel is.
  */
 int nhs_append_page(const void* k, const void* v, int64_t token_stride, int32_t kv_dtype, int32_t row_elems,
-                    int32_t page_size, void* pool, int64_t block, int32_t within, int32_t count,
+                    int32_t page_size, void* pool, int64_t pool_block_stride, int64_t block,
+                    int32_t within, int32_t count,
                     void* host_alias, int64_t host_page, float* summary, void* minimum, void* maximum,
                     void* stream);
 
@@ -277,7 +284,8 @@ int nhs_append_page(const void* k, const void* v, int64_t token_stride, int32_t 
  * by request (storage.py:258-331); this is the batched engine step's form.
  */
 int nhs_append_items(int32_t batch, const void* k, const void* v, int64_t token_stride, int32_t kv_dtype,
-                     int32_t row_elems, int32_t page_size, void* pool, void* host_alias,
+                     int32_t row_elems, int32_t page_size, void* pool, int64_t pool_block_stride,
+                     void* host_alias,
                      const nhs_layer_item* items, const int64_t* lengths, void* stream);
 
 /*

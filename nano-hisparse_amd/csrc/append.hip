@@ -100,6 +100,7 @@ struct AppendItemsArgs {
   int64_t token_stride;  // elements between the items' rows
   int dtype, row_elems, page_size;
   char* pool;
+  int64_t pool_block_bytes;  // the pool's block stride (host blocks are contiguous)
   char* host;
   const nhs_layer_item* items;
   const int64_t* lengths;
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(kAppendThreads) void append_items_kernel(AppendItem
   a.dtype = g.dtype;
   a.row_elems = g.row_elems;
   a.plane_elems = plane;
-  a.pool_block = g.pool + (int64_t)item.resident[page] * block_bytes;
+  a.pool_block = g.pool + (int64_t)item.resident[page] * g.pool_block_bytes;
   a.host_block = g.host ? g.host + (int64_t)item.source[page] * block_bytes : nullptr;
   a.within = (int)(length - page * g.page_size);
   a.count = 1;
@@ -139,7 +140,8 @@ __global__ __launch_bounds__(kAppendThreads) void append_items_kernel(AppendItem
 }  // namespace nhs
 
 extern "C" int nhs_append_page(const void* k, const void* v, int64_t token_stride, int32_t kv_dtype,
-                               int32_t row_elems, int32_t page_size, void* pool, int64_t block, int32_t within,
+                               int32_t row_elems, int32_t page_size, void* pool, int64_t pool_block_stride,
+                               int64_t block, int32_t within,
                                int32_t count, void* host_alias, int64_t host_page, float* summary, void* minimum,
                                void* maximum, void* stream) {
   using namespace nhs;
@@ -157,7 +159,10 @@ extern "C" int nhs_append_page(const void* k, const void* v, int64_t token_strid
   a.row_elems = row_elems;
   a.plane_elems = (int64_t)page_size * row_elems;
   const int64_t block_bytes = 2 * a.plane_elems * elem_size(kv_dtype);
-  a.pool_block = static_cast<char*>(pool) + block * block_bytes;
+  if (pool_block_stride == 0) pool_block_stride = block_bytes;
+  if (pool_block_stride < block_bytes || pool_block_stride % elem_size(kv_dtype))
+    return fail(NHS_ERR_INVALID, "nhs_append_page: pool_block_stride below a block or not a whole element");
+  a.pool_block = static_cast<char*>(pool) + block * pool_block_stride;
   a.host_block = host_alias ? static_cast<char*>(host_alias) + host_page * block_bytes : nullptr;
   a.within = within;
   a.count = count;
@@ -175,7 +180,8 @@ extern "C" int nhs_append_page(const void* k, const void* v, int64_t token_strid
 }
 
 extern "C" int nhs_append_items(int32_t batch, const void* k, const void* v, int64_t token_stride, int32_t kv_dtype,
-                                int32_t row_elems, int32_t page_size, void* pool, void* host_alias,
+                                int32_t row_elems, int32_t page_size, void* pool, int64_t pool_block_stride,
+                                void* host_alias,
                                 const nhs_layer_item* items, const int64_t* lengths, void* stream) {
   using namespace nhs;
   const LaunchEvents ev = take_launch_events();
@@ -192,6 +198,11 @@ extern "C" int nhs_append_items(int32_t batch, const void* k, const void* v, int
   g.row_elems = row_elems;
   g.page_size = page_size;
   g.pool = static_cast<char*>(pool);
+  const int64_t block_bytes = 2 * (int64_t)page_size * row_elems * elem_size(kv_dtype);
+  if (pool_block_stride == 0) pool_block_stride = block_bytes;
+  if (pool_block_stride < block_bytes || pool_block_stride % elem_size(kv_dtype))
+    return fail(NHS_ERR_INVALID, "nhs_append_items: pool_block_stride below a block or not a whole element");
+  g.pool_block_bytes = pool_block_stride;
   g.host = static_cast<char*>(host_alias);
   g.items = items;
   g.lengths = lengths;

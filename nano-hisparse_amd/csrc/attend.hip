@@ -64,6 +64,8 @@ struct AttendArgs {
   int lpr_log2, lanes_used, chunks_per_kv;
   int kv_items;  // batch * kv_heads
   FastDiv page_div;
+  FastDiv plane2_div;  // by 2 * page_size: a K-plane row index -> its block
+  int64_t block_pad;   // pool block stride minus 2 * page_size rows
   float qscale;
   const char* zeros;  // kZeroBytes of zeros
   float* ws;          // partials [B, q_heads, n_splits, 2 + head_dim]
@@ -252,7 +254,9 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
       for (int u = 0; u < U; ++u) {
         okd[u] = ki[u] != 0xffffffffu;
         const bool live = okd[u] && data_lane;
-        const char* kp = live ? pool + (int64_t)ki[u] * row_bytes : a.zeros;
+        // row ki of the K planes: block ki / 2P, whose stride may exceed its rows by block_pad
+        const int64_t at = (int64_t)ki[u] * row_bytes + (int64_t)a.plane2_div.div(ki[u]) * a.block_pad;
+        const char* kp = live ? pool + at : a.zeros;
         const int64_t vo = live ? plane_bytes : 0;
 #pragma unroll
         for (int c = 0; c < C; ++c) {
@@ -606,7 +610,8 @@ extern "C" int64_t nhs_attend_workspace_bytes(int32_t batch, int32_t q_heads, in
 }
 
 extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_batch_stride, int64_t q_head_stride,
-                               const void* pool, int32_t kv_dtype, const int64_t* rows, int64_t rows_batch_stride,
+                               const void* pool, int32_t kv_dtype, int64_t pool_block_stride, const int64_t* rows,
+                               int64_t rows_batch_stride,
                                int64_t rows_head_stride, int64_t rows_col_stride, int32_t batch, int32_t n_rows,
                                int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size, void* out,
                                int64_t out_batch_stride, int64_t out_head_stride, void* workspace,
@@ -629,6 +634,10 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
   if ((head_dim * esize) % 16 || row_chunks > 128)
     return fail(NHS_ERR_UNSUPPORTED, "nhs_attend_rows: head_dim*element size must be a multiple of 16 bytes, <= 2048");
   if ((uintptr_t)pool % 16) return fail(NHS_ERR_INVALID, "nhs_attend_rows: pool must be 16-byte aligned");
+  const int64_t block_bytes = 2 * (int64_t)page_size * kv_heads * head_dim * esize;
+  if (pool_block_stride == 0) pool_block_stride = block_bytes;
+  if (pool_block_stride < block_bytes || pool_block_stride % 16)
+    return fail(NHS_ERR_INVALID, "nhs_attend_rows: pool_block_stride must be a multiple of 16 bytes, at least a block");
   const bool packed = q_dtype == kv_dtype && kv_dtype != NHS_F32 && q_head_stride % 2 == 0 &&
                       q_batch_stride % 2 == 0 && (uintptr_t)query % 4 == 0;
 
@@ -648,6 +657,8 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
   a.head_dim = head_dim;
   a.page_size = page_size;
   a.page_div = FastDiv((uint32_t)page_size);
+  a.plane2_div = FastDiv(2u * (uint32_t)page_size);
+  a.block_pad = pool_block_stride - block_bytes;
   const int C = row_chunks > 64 ? 2 : 1;
   if (row_chunks / C > 64) return fail(NHS_ERR_UNSUPPORTED, "nhs_attend_rows: rows too wide");
   a.lanes_used = row_chunks / C;
@@ -749,7 +760,8 @@ static int scratch_on_device(hipStream_t stream, void** out) {
 }  // namespace nhs
 
 extern "C" int nhs_attend_rows_noalloc(const void* query, int32_t q_dtype, int64_t q_batch_stride,
-                                       int64_t q_head_stride, const void* pool, int32_t kv_dtype, const int64_t* rows,
+                                       int64_t q_head_stride, const void* pool, int32_t kv_dtype,
+                                       int64_t pool_block_stride, const int64_t* rows,
                                        int64_t rows_batch_stride, int64_t rows_head_stride, int64_t rows_col_stride,
                                        int32_t batch, int32_t n_rows, int32_t q_heads, int32_t kv_heads,
                                        int32_t head_dim, int32_t page_size, void* out, int64_t out_batch_stride,
@@ -763,7 +775,8 @@ extern "C" int nhs_attend_rows_noalloc(const void* query, int32_t q_dtype, int64
   void* ws = nullptr;
   const int st = scratch_on_device((hipStream_t)stream, &ws);
   if (st != NHS_OK) return st;
-  return nhs_attend_rows(query, q_dtype, q_batch_stride, q_head_stride, pool, kv_dtype, rows, rows_batch_stride,
+  return nhs_attend_rows(query, q_dtype, q_batch_stride, q_head_stride, pool, kv_dtype, pool_block_stride, rows,
+                         rows_batch_stride,
                          rows_head_stride, rows_col_stride, batch, n_rows, q_heads, kv_heads, head_dim, page_size, out,
                          out_batch_stride, out_head_stride, ws, kNoAllocScratchBytes, stream);
 }

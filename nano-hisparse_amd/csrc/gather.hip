@@ -2,7 +2,9 @@
 // compute units through the host alias, over PCIe) into hot-buffer rows of
 // the device pool. A row is two planes (K and V) of plane_bytes each; in both
 // the host and the pool layout a block is [2, page_size, kv_heads, head_dim],
-// so plane `pl` of row r starts at ((r/P)*2*P + pl*P + r%P) * plane_bytes.
+// so plane `pl` of row r starts at (r/P)*block + (pl*P + r%P) * plane_bytes,
+// with block = 2*P*plane_bytes on the host and the pool's block stride
+// (which may exceed it) on the device.
 //
 // A workgroup takes groups of kRowsPerBlock consecutive plan entries, group
 // blockIdx.x, blockIdx.x + gridDim.x, ... A thread owns vector column c of
@@ -34,7 +36,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char*
                                                                      const int64_t* __restrict__ miss_host,
                                                                      const int64_t* __restrict__ miss_dev,
                                                                      int64_t n_entries, int page_size,
-                                                                     int64_t plane_bytes) {
+                                                                     int64_t plane_bytes, int64_t pool_block_bytes) {
   __shared__ int64_t src_base[kRowsPerBlock];
   __shared__ int64_t dst_base[kRowsPerBlock];
   __shared__ int live;
@@ -54,7 +56,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char*
     }
     if (s >= 0 && d >= 0) {
       src_base[threadIdx.x] = (s / page_size) * block_bytes + (s % page_size) * plane_bytes;
-      dst_base[threadIdx.x] = (d / page_size) * block_bytes + (d % page_size) * plane_bytes;
+      dst_base[threadIdx.x] = (d / page_size) * pool_block_bytes + (d % page_size) * plane_bytes;
       atomicAdd(&live, 1);
     } else {
       src_base[threadIdx.x] = -1;
@@ -96,16 +98,20 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const char*
 
 extern "C" int nhs_gather_rows(const void* host_alias, void* pool, const int64_t* miss_host_rows,
                                const int64_t* miss_device_rows, int64_t n_entries, int32_t page_size,
-                               int64_t plane_bytes, void* stream) {
+                               int64_t plane_bytes, int64_t pool_block_stride, void* stream) {
   using namespace nhs;
   const LaunchEvents ev = take_launch_events();
   if (!host_alias || !pool || !miss_host_rows || !miss_device_rows)
     return fail(NHS_ERR_INVALID, "nhs_gather_rows: null pointer");
   if (n_entries < 0 || page_size < 1 || plane_bytes < 4 || plane_bytes % 4)
     return fail(NHS_ERR_INVALID, "nhs_gather_rows: need n_entries >= 0, page_size >= 1, plane_bytes a multiple of 4");
+  const int64_t block_bytes = 2 * (int64_t)page_size * plane_bytes;
+  if (pool_block_stride == 0) pool_block_stride = block_bytes;
+  if (pool_block_stride < block_bytes)
+    return fail(NHS_ERR_INVALID, "nhs_gather_rows: pool_block_stride below 2 * page_size * plane_bytes");
   if (n_entries == 0) return NHS_OK;
   if (plane_bytes / 4 > 0x3fffffff) return fail(NHS_ERR_UNSUPPORTED, "nhs_gather_rows: rows too wide");
-  const uintptr_t align = (uintptr_t)host_alias | (uintptr_t)pool;
+  const uintptr_t align = (uintptr_t)host_alias | (uintptr_t)pool | (uintptr_t)pool_block_stride;
   int64_t blocks = (n_entries + kRowsPerBlock - 1) / kRowsPerBlock;
   const int cap = g_gather_workgroups.load(std::memory_order_relaxed);
   if (cap > 0 && blocks > cap) blocks = cap;
@@ -113,14 +119,17 @@ extern "C" int nhs_gather_rows(const void* host_alias, void* pool, const int64_t
   hipStream_t s = (hipStream_t)stream;
   if (plane_bytes % 16 == 0 && align % 16 == 0) {
     launch(gather_rows_kernel<uint4>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s, ev.start, ev.stop,
-           (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes);
+           (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes,
+           pool_block_stride);
   } else if (plane_bytes % 8 == 0 && align % 8 == 0) {
     launch(gather_rows_kernel<uint2>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s, ev.start, ev.stop,
-           (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes);
+           (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes,
+           pool_block_stride);
   } else {
     if (align % 4) return fail(NHS_ERR_INVALID, "nhs_gather_rows: host and pool must be 4-byte aligned");
     launch(gather_rows_kernel<uint32_t>, dim3((unsigned)blocks), dim3(kGatherThreads), 0, s, ev.start, ev.stop,
-           (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes);
+           (const char*)host_alias, (char*)pool, miss_host_rows, miss_device_rows, n_entries, page_size, plane_bytes,
+           pool_block_stride);
   }
   return launch_status("nhs_gather_rows");
 }

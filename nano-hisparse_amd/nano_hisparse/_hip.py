@@ -27,18 +27,19 @@ SIGNATURES = {
     "nhs_last_error": ([], ctypes.c_char_p),
     "nhs_set_launch_events": ([_p, _p], ctypes.c_int),
     "nhs_append_page": ([_p, _p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _p, ctypes.c_int64,
-                         ctypes.c_int32, ctypes.c_int32, _p, ctypes.c_int64, _p, _p, _p, _p], ctypes.c_int),
+                         ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _p, ctypes.c_int64, _p, _p, _p, _p],
+                        ctypes.c_int),
     "nhs_host_device_ptr": ([_p, ctypes.POINTER(ctypes.c_void_p)], ctypes.c_int),
-    "nhs_gather_rows": ([_p, _p, _p, _p, _i64, _i32, _i64, _p], ctypes.c_int),
+    "nhs_gather_rows": ([_p, _p, _p, _p, _i64, _i32, _i64, _i64, _p], ctypes.c_int),
     "nhs_set_gather_workgroups": ([_i32], ctypes.c_int),
     "nhs_attend_workspace_bytes": ([_i32, _i32, _i32, _i32], ctypes.c_int64),
     "nhs_attend_rows": (
-        [_p, _i32, _i64, _i64, _p, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64,
+        [_p, _i32, _i64, _i64, _p, _i32, _i64, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64,
          _i64, _p, _i64, _p],
         ctypes.c_int,
     ),
     "nhs_attend_rows_noalloc": (
-        [_p, _i32, _i64, _i64, _p, _i32, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64,
+        [_p, _i32, _i64, _i64, _p, _i32, _i64, _p, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64,
          _i64, _p],
         ctypes.c_int,
     ),
@@ -56,7 +57,7 @@ SIGNATURES = {
         [_i32, _p, _i32, _i64, _i64, _p, _i64, _i32, _i32, _i32, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p],
         ctypes.c_int,
     ),
-    "nhs_append_items": ([_i32, _p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p], ctypes.c_int),
+    "nhs_append_items": ([_i32, _p, _p, _i64, _i32, _i32, _i32, _p, _i64, _p, _p, _p, _p], ctypes.c_int),
     "nhs_quest_select_items": (
         [_i32, _p, _i32, _i64, _i64, _p, _i32, _i32, _i32, _i32, _p, _i32, _i32, _i32, _i32, _p, _p, _p, _p],
         ctypes.c_int,

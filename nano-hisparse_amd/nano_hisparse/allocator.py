@@ -36,11 +36,11 @@ class DeviceSlot:
 
 class DeviceAllocator:
     def __init__(self, config):
-        self.storage = torch.empty(
-            (config.gpu_pages, 2, config.page_size, config.kv_heads, config.head_dim),
-            device=config.device,
-            dtype=config.dtype,
-        )
+        from .row_kernels import padded_pool
+
+        # on a GPU each block is followed by a few head slots of padding (padded_pool)
+        self.storage = padded_pool(config.gpu_pages, config.page_size, config.kv_heads, config.head_dim,
+                                   config.dtype, config.device)
         self.budget = config.gpu_pages
         self.slots = [DeviceSlot() for _ in range(config.gpu_pages)]
         self.free: set[int] = set(range(config.gpu_pages))

@@ -112,6 +112,42 @@ class MappedHost:
 # ---- gather ----------------------------------------------------------------------
 
 
+POOL_PAD_SLOTS = 3  # head slots of padding after each block of a GPU pool
+
+
+def padded_pool(blocks, page_size, kv_heads, head_dim, dtype, device):
+    """A pool [blocks, 2, page_size, kv_heads, head_dim] whose blocks are each
+    followed by POOL_PAD_SLOTS head slots (head_dim elements each) of
+    padding on a GPU (a strided view of a flat buffer; contiguous
+    elsewhere). Consecutive blocks then shift every KV head's bytes by three
+    head slots in the address, so over a request's pages each head's bytes
+    take every offset within the rows. With contiguous blocks a head's bytes
+    always sit at the same offset, and HBM served the heads whose offsets
+    share address bits 8-10 (heads 1 and 5 of 8) ~20% slower, which the
+    attention launch waited for."""
+    shape = (blocks, 2, page_size, kv_heads, head_dim)
+    block = 2 * page_size * kv_heads * head_dim
+    esize = torch.empty((), dtype=dtype).element_size()
+    if torch.device(device).type != "cuda" or kv_heads < 2 or (head_dim * esize) % 16:
+        return torch.empty(shape, dtype=dtype, device=device)
+    pad = POOL_PAD_SLOTS * head_dim
+    flat = torch.empty(blocks * (block + pad), dtype=dtype, device=device)
+    return flat.as_strided(shape, (block + pad, page_size * kv_heads * head_dim, kv_heads * head_dim, head_dim, 1))
+
+
+def pool_block_stride(pool):
+    """Bytes between consecutive blocks of a pool [blocks, 2, P, Hkv, D]: each
+    block must be contiguous; a gap may follow it (stride(0) above
+    2 * P * Hkv * D elements), as in the cache's padded pool."""
+    if pool.ndim != 5:
+        raise ValueError("the pool must be [blocks, 2, page_size, kv_heads, head_dim]")
+    _, _, P, Hkv, D = pool.shape
+    if tuple(pool.stride()[1:]) != (P * Hkv * D, Hkv * D, D, 1) or pool.stride(0) < 2 * P * Hkv * D:
+        raise ValueError("the pool's blocks must be contiguous [2, P, Hkv, D] (a gap after each is allowed)")
+    return pool.stride(0) * pool.element_size()
+
+
+
 def gather_plan(host: MappedHost, pool, miss_host, miss_device, page_size):
     """Copy plan rows from the pinned host store into pool rows.
 
@@ -126,10 +162,11 @@ def gather_plan(host: MappedHost, pool, miss_host, miss_device, page_size):
     if host.dtype != pool.dtype:
         raise ValueError("host and pool dtypes differ")
     plane_bytes = pool[0, 0, 0].numel() * pool.element_size()
+    stride = pool_block_stride(pool)
     lib = _hip.load()
     status = lib.nhs_gather_rows(
         ctypes.c_void_p(host.data_ptr()), _ptr(pool), _ptr(miss_host), _ptr(miss_device), miss_host.numel(),
-        page_size, plane_bytes, _stream(device),
+        page_size, plane_bytes, stride, _stream(device),
     )
     _hip.check(status, "nhs_gather_rows")
 
@@ -165,14 +202,14 @@ def append_page(k, v, pool, block, within, host, host_page, summary, minimum, ma
     if k.stride(2) != 1 or k.stride(1) != k.shape[2] or k.stride(0) != v.stride(0) or v.stride(2) != 1 \
             or v.stride(1) != v.shape[2]:
         raise ValueError("append_page: K/V rows must be contiguous with equal token strides")
-    if not pool.is_contiguous():
-        raise ValueError("append_page: the pool must be contiguous")
+    stride = pool_block_stride(pool)
     count, row_elems, P = k.shape[0], k.shape[1] * k.shape[2], pool.shape[2]
     if host is not None and host.dtype != pool.dtype:
         raise ValueError("append_page: host and pool dtypes differ")
     lib = _hip.load()
     status = lib.nhs_append_page(
-        _ptr(k), _ptr(v), k.stride(0), dtype_code(pool.dtype), row_elems, P, _ptr(pool), int(block), int(within),
+        _ptr(k), _ptr(v), k.stride(0), dtype_code(pool.dtype), row_elems, P, _ptr(pool), stride, int(block),
+        int(within),
         count, ctypes.c_void_p(host.data_ptr() if host is not None else 0), int(host_page if host is not None else 0),
         _ptr(summary), _ptr(minimum), _ptr(maximum), _stream(device),
     )
@@ -213,8 +250,9 @@ def attend_batched(query, pool, rows, page_size, out=None, workspace=None):
     kv_heads = pool.shape[3]
     if pool.shape[4] != D or pool.shape[2] != page_size or Hq % kv_heads:
         raise ValueError("attend_rows: query/pool head shape mismatch")
-    if query.stride(2) != 1 or not pool.is_contiguous():
-        raise ValueError("attend_rows: query rows and the pool must be contiguous")
+    if query.stride(2) != 1:
+        raise ValueError("attend_rows: query rows must be contiguous")
+    stride = pool_block_stride(pool)
     if rows.shape[0] != B or (rows.ndim == 3 and rows.shape[1] != Hq):
         raise ValueError("attend_rows: rows do not match the query batch/heads")
     if pool.shape[0] * page_size >= 2**31:
@@ -236,7 +274,7 @@ def attend_batched(query, pool, rows, page_size, out=None, workspace=None):
         raise ValueError(f"attend_rows: workspace holds {workspace.numel() * workspace.element_size()} < {need} bytes")
     status = lib.nhs_attend_rows(
         _ptr(query), dtype_code(query.dtype), query.stride(0), query.stride(1), _ptr(pool), dtype_code(pool.dtype),
-        _ptr(rows), r_bs, r_hs, r_cs, B, n_rows, Hq, kv_heads, D, page_size, _ptr(out), out.stride(0),
+        stride, _ptr(rows), r_bs, r_hs, r_cs, B, n_rows, Hq, kv_heads, D, page_size, _ptr(out), out.stride(0),
         out.stride(1), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream(device),
     )
     _hip.check(status, "nhs_attend_rows")
@@ -414,9 +452,10 @@ def append_items(k, v, pool, host, items, lengths):
         raise ValueError("k/v rows must be contiguous [Hkv, D] rows of the pool's shape")
     if items.shape[0] != B or lengths.shape[0] != B or lengths.dtype != torch.int64:
         raise ValueError("one item and one int64 length per row")
+    stride = pool_block_stride(pool)
     lib = _hip.load()
     status = lib.nhs_append_items(
-        B, _ptr(k), _ptr(v), k.stride(0), dtype_code(k.dtype), row_elems, pool.shape[2], _ptr(pool),
+        B, _ptr(k), _ptr(v), k.stride(0), dtype_code(k.dtype), row_elems, pool.shape[2], _ptr(pool), stride,
         ctypes.c_void_p(host.data_ptr()) if host is not None else None, _ptr(items), _ptr(lengths),
         _stream(device),
     )

@@ -99,6 +99,8 @@ def _i64(a):
 
 def gather_rows(host, pool, miss_host, miss_device, page_size):
     """Copy plan rows host -> pool in place (both [blocks, 2, P, Hkv, D])."""
+    if not (pool.is_contiguous() and host.is_contiguous()):
+        raise ValueError("oracle gather_rows: host and pool must be contiguous (copy a padded pool first)")
     mh, md = _i64(miss_host).ravel(), _i64(miss_device).ravel()
     plane_bytes = int(np.prod(pool.shape[3:])) * pool.element_size()
     lib().oracle_gather_rows(_ptr(host), _ptr(pool), _ptr(mh), _ptr(md), mh.size, page_size, plane_bytes)
@@ -120,7 +122,7 @@ def attend_rows(query, pool, rows, page_size):
         raise ValueError("oracle attend_rows: query, rows and pool shapes disagree")
     rows = rows.contiguous()
     out = torch.empty(B, Hq, D, dtype=torch.float32)
-    query = query.contiguous()
+    query, pool = query.contiguous(), pool.contiguous()
     lib().oracle_attend_rows(
         _ptr(query), _dtype_code(query), Hq * D, D, _ptr(pool), _dtype_code(pool), _ptr(rows),
         Hq * rows.shape[-1], rows.shape[-1], 1, B, rows.shape[-1], Hq, kv_heads, D, page_size, _ptr(out),

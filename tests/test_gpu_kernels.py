@@ -52,6 +52,59 @@ def test_gather_rows_bit_exact(gpu, dtype, page, kv_heads, head_dim):
     assert torch.equal(pool.cpu().view(torch.uint8), expected.view(torch.uint8))
 
 
+@pytest.mark.parametrize("dtype,page,kv_heads,head_dim", [(torch.bfloat16, 64, 8, 128), (torch.float16, 16, 2, 64),
+                                                      (torch.float32, 8, 4, 32)])
+def test_padded_pool_reads_and_writes_as_the_contiguous_pool(gpu, dtype, page, kv_heads, head_dim):
+    """The cache's pool leaves rk.POOL_PAD_SLOTS head slots of padding after
+    every block (rk.padded_pool). Gather, append and attention on it write and read the
+    same rows as on a contiguous pool: the gathered and appended bytes, the
+    bounds and the attention outputs are bit-identical, and the padding is
+    never written."""
+    log_case(test="padded-pool", dtype=dtype, page=page, kv_heads=kv_heads, head_dim=head_dim)
+    g = torch.Generator().manual_seed(5)
+    blocks, host_pages = 24, 40
+    padded = rk.padded_pool(blocks, page, kv_heads, head_dim, dtype, gpu)
+    block, pad = 2 * page * kv_heads * head_dim, rk.POOL_PAD_SLOTS * head_dim
+    assert padded.stride(0) == block + pad and rk.pool_block_stride(padded) == (block + pad) * padded.element_size()
+    flat = torch.as_strided(padded, (blocks * (block + pad),), (1,))
+    flat.fill_(7.0)  # the padding must keep this
+    start = torch.randn(blocks, 2, page, kv_heads, head_dim, generator=g).to(dtype)
+    padded.copy_(start.to(gpu))
+    plain = start.to(gpu)
+    host = torch.randn(host_pages, 2, page, kv_heads, head_dim, generator=g).to(dtype).pin_memory()
+    alias = rk.MappedHost(host)
+    n = 3 * page + 5
+    md = torch.randperm(blocks * page, generator=g)[:n]
+    mh = torch.randint(0, host_pages * page, (n,), generator=g)
+    mh[n // 2:], md[n // 2:] = -1, -1
+    for pool in (padded, plain):
+        rk.gather_plan(alias, pool, mh.to(gpu), md.to(gpu), page)
+    # append three tokens into block 5 of each, with bounds
+    k = torch.randn(3, kv_heads, head_dim, generator=g).to(dtype).to(gpu)
+    v = torch.randn(3, kv_heads, head_dim, generator=g).to(dtype).to(gpu)
+    bounds = []
+    for pool in (padded, plain):
+        summary = torch.zeros(kv_heads, head_dim, dtype=torch.float32, device=gpu)
+        lo = torch.full((kv_heads, head_dim), float("inf"), device=gpu).to(dtype)
+        hi = torch.full((kv_heads, head_dim), float("-inf"), device=gpu).to(dtype)
+        rk.append_page(k, v, pool, 5, 2, None, 0, summary, lo, hi)
+        bounds.append((summary, lo, hi))
+    torch.cuda.synchronize()
+    assert torch.equal(padded.cpu().view(torch.uint8), plain.cpu().view(torch.uint8))
+    for x, y in zip(*bounds):
+        assert torch.equal(x.view(torch.uint8), y.view(torch.uint8))
+    gaps = flat.view(blocks, block + pad)[:, block:]
+    assert bool((gaps == 7.0).all())
+    if (head_dim * padded.element_size()) % 16 == 0:
+        q = torch.randn(2, 2 * kv_heads, head_dim, generator=g).to(dtype).to(gpu)
+        rows = torch.randint(0, blocks * page, (2, 3 * page), generator=g)
+        rows[0, ::5] = -1
+        a = rk.attend_batched(q, padded, rows.to(gpu), page)
+        b = rk.attend_batched(q, plain, rows.to(gpu), page)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+
+
 # ---- attention ------------------------------------------------------------------
 
 

@@ -39,7 +39,7 @@ def _noalloc(lib, q, pool, rows, P, out, stream):
     B, Hq, D = q.shape
     Hkv = pool.shape[3]
     return lib.nhs_attend_rows_noalloc(
-        q.data_ptr(), _hip.NHS_BF16, q.stride(0), q.stride(1), pool.data_ptr(), _hip.NHS_BF16, rows.data_ptr(),
+        q.data_ptr(), _hip.NHS_BF16, q.stride(0), q.stride(1), pool.data_ptr(), _hip.NHS_BF16, 0, rows.data_ptr(),
         rows.stride(0), 0, rows.stride(1), B, rows.shape[1], Hq, Hkv, D, P, out.data_ptr(), out.stride(0),
         out.stride(1), stream,
     )
