@@ -71,6 +71,7 @@ typedef struct nhs_layer_item {
   int64_t n_pages;
 } nhs_layer_item;
 
+/* 2: the pool block stride arguments of the gather, attention and appends */
 int nhs_abi_version(void);
 const char* nhs_last_error(void);
 
@@ -392,6 +393,27 @@ int nhs_silu_mul(int32_t rows, int32_t inter, int32_t dtype, const void* gate_up
  */
 int nhs_linear_small_m(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, const void* bias,
                        int32_t dtype, int32_t m, int32_t n, int32_t k, void* y, int64_t y_row_stride, void* stream);
+
+/*
+ * nhs_linear_small_m followed by nhs_silu_mul in one launch, bit-identical
+ * to the two: w is the fused [gate; up] weight [2 * inter, k] (no bias) and
+ * y[m, inter] = round(round(silu(g)) * u) for g, u the rounded gate and up
+ * outputs (MLP.forward, model.py:70-71). inter a multiple of 8.
+ */
+int nhs_linear_silu_mul(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, int32_t dtype,
+                        int32_t m, int32_t inter, int32_t k, void* y, int64_t y_row_stride, void* stream);
+
+/*
+ * nhs_linear_small_m followed by nhs_rope on the first rope_heads heads of
+ * each output row, in one launch, bit-identical to the two: y[m, n] holds
+ * n / head_dim heads of head_dim (a fused q/k/v projection: the q and k
+ * heads rotate, the v heads do not); cos/sin are [m, head_dim / 2]
+ * (Model._project's q/k/v projections and rope closure, model.py:134-153).
+ * head_dim a multiple of 16, n of head_dim.
+ */
+int nhs_linear_rope(const void* x, int64_t x_row_stride, const void* w, int64_t w_row_stride, const void* bias,
+                    int32_t dtype, int32_t m, int32_t n, int32_t k, int32_t head_dim, int32_t rope_heads,
+                    const void* cos, const void* sin, void* y, int64_t y_row_stride, void* stream);
 
 /*
  * Causal GQA self-attention over one prompt (prefill), flash-attention style

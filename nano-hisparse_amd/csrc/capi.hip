@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void expand_columns_kernel(const int64_t* __re
 
 extern "C" {
 
-int nhs_abi_version(void) { return 1; }
+int nhs_abi_version(void) { return 2; }
 
 const char* nhs_last_error(void) { return nhs::g_last_error; }
 

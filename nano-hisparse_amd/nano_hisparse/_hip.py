@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(_DIR, "libnhs_hip.so")
 HEADER_PATH = os.path.normpath(os.path.join(_DIR, "..", "..", "include", "nhs.h"))
 
 NHS_F32, NHS_F16, NHS_BF16 = 0, 1, 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i32, _i64, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p
 
@@ -79,6 +79,9 @@ SIGNATURES = {
     "nhs_rope": ([_i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p], ctypes.c_int),
     "nhs_silu_mul": ([_i32, _i32, _i32, _p, _p, _p], ctypes.c_int),
     "nhs_linear_small_m": ([_p, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _p, _i64, _p], ctypes.c_int),
+    "nhs_linear_silu_mul": ([_p, _i64, _p, _i64, _i32, _i32, _i32, _i32, _p, _i64, _p], ctypes.c_int),
+    "nhs_linear_rope": (
+        [_p, _i64, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _i64, _p], ctypes.c_int),
     "nhs_prefill_attention": (
         [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _i64, _p],
         ctypes.c_int,

@@ -426,8 +426,11 @@ class _Group:
         qkv_w, qkv_b, _ = fused
         self.gu_w = fused[2]
         h = rk.add_rmsnorm(self.x, self.delta, layer.input_layernorm.weight, _eps(layer.input_layernorm, cfg))
-        qkv = _linear(h, qkv_w, qkv_b)
-        rk.rope_(qkv, Hq + Hkv, D, self.cos, self.sin)
+        if _small_m(h, qkv_w, qkv_b) and D % 16 == 0:  # projection and RoPE in one launch
+            qkv = rk.linear_rope(h, qkv_w, qkv_b, Hq + Hkv, D, self.cos, self.sin)
+        else:
+            qkv = _linear(h, qkv_w, qkv_b)
+            rk.rope_(qkv, Hq + Hkv, D, self.cos, self.sin)
         q = qkv[:, : Hq * D].view(B, Hq, D)
         k = qkv[:, Hq * D: (Hq + Hkv) * D].view(B, Hkv, D)
         v = qkv[:, (Hq + Hkv) * D:].view(B, Hkv, D)
@@ -445,7 +448,11 @@ class _Group:
         norm2 = layer.post_attention_layernorm
         h = rk.add_rmsnorm(self.x, o, norm2.weight, _eps(norm2, cfg))
         down = layer.mlp.down_proj
-        self.delta = _linear(rk.silu_mul(_linear(h, self.gu_w, None)), down.weight, down.bias)
+        if _small_m(h, self.gu_w, None) and self.gu_w.shape[0] % 16 == 0:  # gate/up and SiLU in one launch
+            act = rk.linear_silu_mul(h, self.gu_w)
+        else:
+            act = rk.silu_mul(_linear(h, self.gu_w, None))
+        self.delta = _linear(act, down.weight, down.bias)
 
 def _linear(x, weight, bias):
     """x @ weight.T + bias for a decode batch: the MFMA weight-stream kernel
@@ -453,13 +460,19 @@ def _linear(x, weight, bias):
     it takes, else torch."""
     from . import row_kernels as rk
 
-    m, k = x.shape
-    n = weight.shape[0]
-    if (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and weight.dtype == x.dtype and m <= 16
-            and n % 16 == 0 and k % 2048 == 0 and x.stride(1) == 1 and weight.is_contiguous()
-            and (bias is None or bias.is_contiguous())):
+    if _small_m(x, weight, bias):
         return rk.linear_small_m(x, weight, bias)
     return F.linear(x, weight, bias)
+
+
+def _small_m(x, weight, bias):
+    """Whether the decode projection x @ weight.T (+ bias) fits the
+    weight-stream kernels (nhs_linear_small_m and its fused forms)."""
+    m, k = x.shape
+    n = weight.shape[0]
+    return (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and weight.dtype == x.dtype and m <= 16
+            and n % 16 == 0 and k % 2048 == 0 and x.stride(1) == 1 and weight.is_contiguous()
+            and (bias is None or bias.is_contiguous()))
 
 
 def _eps(norm, cfg):

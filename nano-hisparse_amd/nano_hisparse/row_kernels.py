@@ -670,3 +670,54 @@ def linear_small_m(x, weight, bias=None, out=None):
     )
     _hip.check(status, "nhs_linear_small_m")
     return out
+
+
+def _linear_operands(who, x, weight):
+    if x.ndim != 2 or weight.ndim != 2 or x.shape[1] != weight.shape[1]:
+        raise ValueError(f"{who}: x [m, k], weight [n, k]")
+    if x.dtype != weight.dtype or x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"{who}: bf16 or fp16 x and weight of one dtype")
+    if x.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError(f"{who}: rows must be contiguous")
+
+
+def linear_silu_mul(x, gate_up_weight):
+    """silu(x @ gate.T) * (x @ up.T) for the fused [gate; up] weight
+    [2 * inter, k]: linear_small_m then silu_mul in one launch, bit-identical
+    to the two."""
+    device = _require_gpu("linear_silu_mul", x, gate_up_weight)
+    _linear_operands("linear_silu_mul", x, gate_up_weight)
+    if gate_up_weight.shape[0] % 2:
+        raise ValueError("linear_silu_mul: gate_up_weight [2 * inter, k]")
+    m, k = x.shape
+    inter = gate_up_weight.shape[0] // 2
+    out = torch.empty(m, inter, dtype=x.dtype, device=device)
+    lib = _hip.load()
+    status = lib.nhs_linear_silu_mul(_ptr(x), x.stride(0), _ptr(gate_up_weight), gate_up_weight.stride(0),
+                                     dtype_code(x.dtype), m, inter, k, _ptr(out), out.stride(0), _stream(device))
+    _hip.check(status, "nhs_linear_silu_mul")
+    return out
+
+
+def linear_rope(x, weight, bias, rope_heads, head_dim, cos, sin):
+    """x @ weight.T (+ bias) with the rotary embedding applied to the first
+    rope_heads heads of head_dim of each row (cos/sin [m, head_dim / 2] in
+    x's dtype): linear_small_m then rope_ in one launch, bit-identical to the
+    two."""
+    device = _require_gpu("linear_rope", x, weight, cos, sin)
+    _linear_operands("linear_rope", x, weight)
+    m, k = x.shape
+    n = weight.shape[0]
+    if bias is not None and (bias.shape != (n,) or bias.dtype != x.dtype or not bias.is_contiguous()):
+        raise ValueError("linear_rope: bias must be a contiguous [n] vector of the same dtype")
+    if cos.shape != (m, head_dim // 2) or sin.shape != cos.shape or cos.dtype != x.dtype or sin.dtype != x.dtype:
+        raise ValueError("linear_rope: cos/sin [m, head_dim/2] in x's dtype")
+    if not (cos.is_contiguous() and sin.is_contiguous()):
+        raise ValueError("linear_rope: cos/sin must be contiguous")
+    out = torch.empty(m, n, dtype=x.dtype, device=device)
+    lib = _hip.load()
+    status = lib.nhs_linear_rope(_ptr(x), x.stride(0), _ptr(weight), weight.stride(0), _ptr(bias),
+                                 dtype_code(x.dtype), m, n, k, head_dim, rope_heads, _ptr(cos), _ptr(sin), _ptr(out),
+                                 out.stride(0), _stream(device))
+    _hip.check(status, "nhs_linear_rope")
+    return out
