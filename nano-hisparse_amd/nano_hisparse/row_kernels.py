@@ -147,7 +147,6 @@ def pool_block_stride(pool):
     return pool.stride(0) * pool.element_size()
 
 
-
 def gather_plan(host: MappedHost, pool, miss_host, miss_device, page_size):
     """Copy plan rows from the pinned host store into pool rows.
 

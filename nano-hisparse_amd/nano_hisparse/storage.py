@@ -493,7 +493,8 @@ class HostStore:
         locations = Counter(p.location.value for p in self.pages.values() if p.valid_tokens)
         return {
             "budget_pages": self.budget,
-            "allocated_device_bytes": self.pool.numel() * self.pool.element_size(),
+            # the pool's whole allocation, its blocks' padding included (row_kernels.padded_pool)
+            "allocated_device_bytes": self.pool.untyped_storage().nbytes(),
             "allocated_host_bytes": self.host.numel() * self.host.element_size(),
             "index_bytes": self.index_bytes,
             "index_budget_bytes": self.config.index_budget_bytes,
