@@ -878,6 +878,10 @@ def main():
         # others from a second pass of K steps that stamps every launch (its
         # step time: stamped_step_us)
         "kernel_us": {n: round(v, 2) for n, v in kernel_us.items()},
+        # the sparse-attention + gather step: resolve (with the page selection
+        # in the same launch) + gather + attention, the launches that follow
+        # the Quest scoring on the step's critical path
+        "sparse_attn_gather_step_us": round(sum(kernel_us[n] for n in ("resolve", "gather", "attention")), 2),
         "stamped_step_us": round(stamped_ms * 1e3, 2),
         "roofline": {
             "kernel": "nhs_attend_rows (attend_kernel)",
