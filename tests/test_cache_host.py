@@ -160,3 +160,23 @@ def test_overlapping_leases_balance_pins_and_released_handles_fail():
                 call()
     assert store.allocator.slots[0].ref_cnt == 1
     store.assert_invariants()
+
+
+def test_pool_block_stride_of_contiguous_and_gapped_pools():
+    """The launchers pass a pool's block stride to the C ABI: a contiguous
+    pool (the CPU cache's) has one block per stride; a pool whose blocks are
+    followed by a gap (the GPU cache's padded pool, a strided view) has a
+    larger stride; a pool whose blocks are not contiguous is rejected."""
+    from nano_hisparse import row_kernels as rk
+
+    pool = rk.padded_pool(6, 4, 2, 8, torch.bfloat16, "cpu")  # contiguous off the GPU
+    assert pool.is_contiguous() and pool.shape == (6, 2, 4, 2, 8)
+    block = 2 * 4 * 2 * 8
+    assert rk.pool_block_stride(pool) == block * 2
+    flat = torch.zeros(6 * (block + 3 * 8), dtype=torch.bfloat16)
+    gapped = flat.as_strided(pool.shape, (block + 3 * 8, 4 * 2 * 8, 2 * 8, 8, 1))
+    assert rk.pool_block_stride(gapped) == (block + 3 * 8) * 2
+    with pytest.raises(ValueError, match="contiguous"):
+        rk.pool_block_stride(pool.transpose(1, 2))
+    with pytest.raises(ValueError, match="blocks"):
+        rk.pool_block_stride(pool[0])

@@ -105,6 +105,52 @@ def test_padded_pool_reads_and_writes_as_the_contiguous_pool(gpu, dtype, page, k
         assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
 
 
+def test_pool_block_stride_is_checked_by_the_c_abi(gpu):
+    """Every entry point that takes the pool's block stride rejects one below
+    a block (the attention also one that is not a multiple of 16 bytes),
+    before it launches anything; 0 means contiguous blocks."""
+    import ctypes
+
+    from nano_hisparse import _hip
+
+    lib = _hip.load()
+    P, Hkv, D = 4, 2, 8  # bf16: a block is 2 * 4 * 2 * 8 * 2 = 256 bytes
+    pool = torch.zeros(4, 2, P, Hkv, D, dtype=torch.bfloat16, device=gpu)
+    host = torch.zeros(4, 2, P, Hkv, D, dtype=torch.bfloat16).pin_memory()
+    alias = rk.MappedHost(host)
+    plan = torch.full((4,), -1, dtype=torch.int64, device=gpu)
+    q = torch.zeros(1, 2 * Hkv, D, dtype=torch.bfloat16, device=gpu)
+    rows = torch.zeros(1, 8, dtype=torch.int64, device=gpu)
+    out = torch.empty_like(q)
+    ws = torch.zeros(lib.nhs_attend_workspace_bytes(1, 2 * Hkv, D, 8), dtype=torch.uint8, device=gpu)
+    kv = torch.zeros(1, Hkv, D, dtype=torch.bfloat16, device=gpu)
+    lo = torch.full((Hkv, D), float("inf"), dtype=torch.bfloat16, device=gpu)
+    hi = torch.full((Hkv, D), float("-inf"), dtype=torch.bfloat16, device=gpu)
+    summary = torch.zeros(Hkv, D, dtype=torch.float32, device=gpu)
+    s = ctypes.c_void_p(torch.cuda.current_stream(gpu).cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    bf16 = 2
+
+    def gather(stride):
+        return lib.nhs_gather_rows(ctypes.c_void_p(alias.data_ptr()), p(pool), p(plan), p(plan), 4, P,
+                                   Hkv * D * 2, stride, s)
+
+    def attend(stride):
+        return lib.nhs_attend_rows(p(q), bf16, 0, D, p(pool), bf16, stride, p(rows), 0, 0, 1, 1, 8, 2 * Hkv, Hkv, D,
+                                   P, p(out), 0, D, p(ws), ws.numel(), s)
+
+    def append(stride):
+        return lib.nhs_append_page(p(kv), p(kv), Hkv * D, bf16, Hkv * D, P, p(pool), stride, 1, 0, 1, None, 0,
+                                   p(summary), p(lo), p(hi), s)
+
+    for call in (gather, attend, append):
+        assert call(255) != 0, call.__name__
+        assert b"pool_block_stride" in lib.nhs_last_error(), call.__name__
+        assert call(0) == 0 and call(256) == 0 and call(512) == 0, call.__name__
+    assert attend(264) != 0 and b"multiple of 16" in lib.nhs_last_error()
+    torch.cuda.synchronize()
+
+
 # ---- attention ------------------------------------------------------------------
 
 
