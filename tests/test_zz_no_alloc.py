@@ -2,6 +2,8 @@
 nhs_attend_rows with a caller workspace, through the C ABI: two calls in a
 row on the one scratch array, the second with a smaller input, each equal
 bit for bit to the workspace entry point and within tolerance of the oracle.
+The first call reads the cache's padded pool (a gap after each block), the
+second a contiguous one.
 """
 
 import ctypes
@@ -39,7 +41,8 @@ def _noalloc(lib, q, pool, rows, P, out, stream):
     B, Hq, D = q.shape
     Hkv = pool.shape[3]
     return lib.nhs_attend_rows_noalloc(
-        q.data_ptr(), _hip.NHS_BF16, q.stride(0), q.stride(1), pool.data_ptr(), _hip.NHS_BF16, 0, rows.data_ptr(),
+        q.data_ptr(), _hip.NHS_BF16, q.stride(0), q.stride(1), pool.data_ptr(), _hip.NHS_BF16,
+        rk.pool_block_stride(pool), rows.data_ptr(),
         rows.stride(0), 0, rows.stride(1), B, rows.shape[1], Hq, Hkv, D, P, out.data_ptr(), out.stride(0),
         out.stride(1), stream,
     )
@@ -55,10 +58,17 @@ def test_noalloc_attention_equals_the_workspace_entry_point():
         dict(seed=1, B=16, Hq=32, Hkv=8, D=128, P=64, blocks=600, n_rows=2048),
         dict(seed=2, B=3, Hq=28, Hkv=4, D=128, P=32, blocks=300, n_rows=500),
     ]
-    for shape in shapes:
+    for k, shape in enumerate(shapes):
         print("case:", shape, flush=True)
         q, pool, rows = _case(**shape)
-        gq, gpool, grows = q.to(dev), pool.to(dev), rows.to(dev)
+        gq, grows = q.to(dev), rows.to(dev)
+        if k == 0:  # the cache's padded pool (a gap after each block)
+            blocks, _, P, Hkv, D = pool.shape
+            gpool = rk.padded_pool(blocks, P, Hkv, D, pool.dtype, dev)
+            gpool.copy_(pool.to(dev))
+            assert rk.pool_block_stride(gpool) > pool[0].numel() * pool.element_size()
+        else:
+            gpool = pool.to(dev)
         need = lib.nhs_attend_workspace_bytes(q.shape[0], q.shape[1], q.shape[2], rows.shape[1])
         assert 0 < need <= _max_bytes()
         expected = rk.attend_batched(gq, gpool, grows, shape["P"])  # the workspace entry point
