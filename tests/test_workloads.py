@@ -8,7 +8,10 @@
   128 (the reference's minimum legal value); a pool of exactly one hot
   region + 2 tails per layer would admit one request at a time, so the pool
   is 3x that. The GPU engine must generate the CPU (oracle) engine's tokens
-  and row counters.
+  and row counters, and both must equal the reference package's own run of
+  this config (tests/golden/reference_plumbing_tokens.json, written by
+  tests/golden/make_reference_tokens.py from the reference on the CPU): all
+  192 tokens and the resident / hot / miss row counters.
 
 - Resolver stress: 64 requests with Qwen2-7B heads (28 query / 4 KV heads x
   128, bf16), contexts uniform in [4096, 65536], pages of 32, a 1024-row
@@ -22,6 +25,9 @@
   N(0, 0.5) so Quest scores are spread out. Selection, rows and gathered
   bytes bit-exact; attention within 2e-2.
 """
+
+import json
+import os
 
 import numpy as np
 import pytest
@@ -61,10 +67,22 @@ def run_plumbing_config(device):
     return out, cache.snapshot()["row_stats"]
 
 
+def reference_plumbing_run():
+    """Tokens and row counters of the reference package's own run of the
+    plumbing config (a fixture; the reference is not imported here)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_plumbing_tokens.json")
+    with open(path) as f:
+        record = json.load(f)
+    return record["tokens"], record["row_stats"]
+
+
 def test_plumbing_config_runs_on_the_oracle(cpu_kernels):
     out, stats = run_plumbing_config("cpu")
     assert sorted(out) == ["p0", "p1", "p2"] and all(len(v) == 64 for v in out.values())
     assert stats["misses"] > 0 and stats["hot_hits"] > 0
+    tokens, ref_stats = reference_plumbing_run()
+    assert {k: list(v) for k, v in out.items()} == tokens
+    assert dict(stats) == ref_stats
 
 
 @pytest.mark.gpu
@@ -80,6 +98,9 @@ def test_plumbing_config_matches_the_oracle_engine(gpu):
     got, got_stats = run_plumbing_config(gpu)
     assert got == want
     assert got_stats == want_stats
+    tokens, ref_stats = reference_plumbing_run()
+    assert {k: list(v) for k, v in got.items()} == tokens
+    assert dict(got_stats) == ref_stats
 
 
 @pytest.mark.gpu
