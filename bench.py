@@ -18,7 +18,9 @@ each with its own query, Quest bounds, KV pool and tables over one shared
 pinned host store, and step i runs layer i mod 4: between two visits of a
 layer ~600 MB of other layers' data pass through the caches, more than the
 256 MB Infinity Cache holds, so every launch reads cold data as in a real
-multi-layer decode. `value` is the batch divided by one layer's step time;
+multi-layer decode. `value` is that step's time in microseconds (the
+metric's "sparse-attn+gather step µs": one layer's quest select + resolve +
+gather + attention for the whole batch of 16, lower is better);
 `roofline_warm` repeats layer 0 alone for comparison. With --chunks n the
 gathers run on a side stream in n groups of requests and each group's
 attention starts when its gather event fires, overlapping the next group's
@@ -28,10 +30,13 @@ resolves against its own copy of its layer's starting tags/LRU, made before
 the timed region, so every step has the same 25% misses. In the timed
 region the gather and attention launches stamp timing events (the two
 roofline kernels' launch times); the Quest and resolver times come from a
-second, fully stamped pass. The CPU oracle then runs layer 0's step on 16
-host threads and on one, and its rows and attention outputs are checked
-against the GPU's. The default line ends with `model_decode`: the
-whole-model decode below at 16 timed steps.
+second, fully stamped pass. The CPU baseline then runs layer 0's step on
+16 host threads and on one: the C port of the reference CPU path (Quest
+select, resolver, gather loop, and the reference's float32 masked-softmax
+attention), in microseconds per step like `value`; its rows and attention
+outputs are checked against the GPU's. The default line ends with
+`model_decode`: the whole-model decode below at the workload's 256 decode
+steps (decode tokens/s).
 Prints one JSON line.
 
 `--workload attention-shapes` times the row attention alone, cold, at four
@@ -92,7 +97,7 @@ def parse_args():
                     "a kernel-trace profile whose attention dispatches should all be cold)")
     ap.add_argument("--cold-layers", type=int, default=4,
                     help="kernel workloads: layers with their own device state cycled by the timed steps")
-    ap.add_argument("--model-steps", type=int, default=16,
+    ap.add_argument("--model-steps", type=int, default=256,
                     help="default line: timed steps of the whole-model decode (model_decode key; 0 to skip)")
     ap.add_argument("--layers", type=int, default=32, help="model workload: decoder layers")
     ap.add_argument("--prompt", type=int, default=16384, help="model workload: prompt tokens per request")
@@ -284,7 +289,7 @@ def cpu_threads(batch):
 
 def cpu_baseline(w, steps, threads):
     """The C oracle (a port of the reference CPU path: Quest select, resolve,
-    gather and float64-accumulated attention) on layer w's inputs, one
+    gather and the reference's float32 attention arithmetic) on layer w's inputs, one
     request per task on `threads` host threads (the oracle's C calls release
     the GIL; a request's gather writes only its own hot blocks, which only
     its attention reads). Returns (median step seconds, physical rows
@@ -312,7 +317,7 @@ def cpu_baseline(w, steps, threads):
             positions[0].numpy(), source[b], resident[b], hot[b], tags[b], lru[b], int(lengths[b]), w.page
         )
         oracle.gather_rows(w.host, pool, mh, md, w.page)
-        out = oracle.attend_rows(q[b : b + 1], pool, torch.from_numpy(ph[None]), w.page)
+        out = oracle.attend_rows(q[b : b + 1], pool, torch.from_numpy(ph[None]), w.page, arithmetic="float32")
         return ph, out[0]
 
     times = []
@@ -840,13 +845,13 @@ def main():
     )
     result = {
         "metric": METRIC,
-        "value": round(w.batch / (ms_per_step * 1e-3), 1),
-        "unit": "tokens/s",
+        "value": round(step_us, 2),
+        "unit": "µs per step",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
+        "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
@@ -861,8 +866,8 @@ def main():
                 "64 pages = 4096 rows selected of 131072, selected pages: 2 tail pages resident, 4 hot, 58 host "
                 "misses; K/V N(0,1) plus a per-page offset N(0, 0.5); hot rows 8192 per request"
             ),
-            "value": "batch / one layer's step time: the sparse decode rate of one layer; a token of an "
-                     "N-layer model passes N such steps (whole-model decode: model_decode)",
+            "value": "one layer's sparse decode step for the whole batch (quest select + resolve + host-row "
+                     "gather + attention), microseconds per step; whole-model decode tokens/s: model_decode",
             "step": f"one layer's step; step i runs layer i mod {L}, each layer with its own device pool, "
                     "bounds and tables (shared pinned host store), so every step reads data the other layers "
                     "evicted from the 256 MB Infinity Cache",
@@ -932,16 +937,16 @@ def main():
         one_steps = max(1, min(3, args.cpu_steps))
         cpu1_s, _, _ = cpu_baseline(w, one_steps, 1)
         result["cpu_baseline"] = {
-            "value": round(w.batch / cpu_s, 2),
-            "unit": "tokens/s",
+            "value": round(cpu_s * 1e6, 1),
+            "unit": "µs per step",
             "cores": threads,
             "kind": "port",
-            "sample": f"{args.cpu_steps} full steps of layer 0's inputs, one request per thread "
-                      f"(median step {cpu_s:.3f} s)",
-            "arithmetic": "the C oracle: fp32 Quest scores, integer resolver, byte gather, attention "
-                          "accumulated in float64",
-            "single_thread": {"value": round(w.batch / cpu1_s, 2), "cores": 1,
-                              "sample": f"{one_steps} full steps (median {cpu1_s:.3f} s)"},
+            "sample": f"{args.cpu_steps} full steps of layer 0's inputs (the whole batch of {w.batch}), one "
+                      f"request per thread; median step",
+            "arithmetic": "the C port of the reference CPU path: fp32 Quest scores, integer resolver, byte "
+                          "gather loop, the reference's float32 masked-softmax attention (attention.py:26-35)",
+            "single_thread": {"value": round(cpu1_s * 1e6, 1), "unit": "µs per step", "cores": 1,
+                              "sample": f"{one_steps} full steps, median"},
             "host": f"{cpu_model_name()} ({os.cpu_count()} CPUs visible)",
         }
         result["parity"] = {"rows_bit_exact": True, "attention_max_abs": float(f"{attn_err:.3g}")}

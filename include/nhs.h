@@ -224,9 +224,9 @@ int nhs_resolve_rows(int32_t batch, int32_t n, const void* positions, int32_t po
  * ascending to pages[b, :top_pages]
  * (-1 padded when count < top_pages) and expanded to causal token positions
  * positions[b, :top_pages*page_size] (ascending, -1 padded). scores[b, :]
- * (max_pages floats) keeps the scores. With pages and positions both NULL
- * only the scores are computed (nothing runs when top_pages >= max_pages:
- * every page is then kept), for nhs_select_resolve_rows / _items.
+ * (max_pages floats) keeps the scores, also when top_pages >= max_pages
+ * (every page is then kept). With pages and positions both NULL only the
+ * scores are computed, for nhs_select_resolve_rows / _items.
  * minimum/maximum are [max_pages, kv_heads, head_dim] per request.
  * Replaces quest_selection, nano_hisparse/selection.py:69-91.
  */

@@ -740,7 +740,8 @@ __global__ __launch_bounds__(kResolveThreads) void resolve_large_kernel(ResolveA
         const uint32_t pg = a.page_div.div((uint32_t)lg);
         const int32_t off = (int32_t)((uint32_t)lg - pg * (uint32_t)P);
         const int64_t page = pg < (uint32_t)(n_pages - 1) ? (int64_t)pg : (int64_t)(n_pages - 1);
-        const int64_t src = source[page], res = resident[page];
+        // an item with no pages reads no table: every entry stays unset (-1)
+        const int64_t src = n_pages >= 1 ? source[page] : -1, res = n_pages >= 1 ? resident[page] : -1;
         const bool valid = lg < length && run && src >= 0;
         const bool rhit = valid && res >= 0;
         const bool nhot = valid && !rhit;
@@ -1012,8 +1013,9 @@ extern "C" int nhs_select_resolve_rows(int32_t batch, const float* scores, int32
   using namespace nhs;
   const LaunchEvents ev = take_launch_events();
   const char* who = "nhs_select_resolve_rows";
-  if (top_pages < 1 || page_size < 1 || (int64_t)top_pages * page_size > kLargeMaxK)
-    return fail(NHS_ERR_INVALID, "%s: need top_pages, page_size >= 1", who);
+  if (top_pages < 1 || page_size < 1) return fail(NHS_ERR_INVALID, "%s: need top_pages, page_size >= 1", who);
+  if ((int64_t)top_pages * page_size > kLargeMaxK)
+    return fail(NHS_ERR_UNSUPPORTED, "%s: top_pages * page_size must be <= %d", who, kLargeMaxK);
   const int32_t n = top_pages * page_size;
   int st = check_resolve(who, batch, n, scores, hot_rows, lengths, length, page_size, physical, miss_host,
                          miss_device, plan_stride, counts);
@@ -1046,8 +1048,9 @@ extern "C" int nhs_select_resolve_items(int32_t batch, const float* scores, int3
   using namespace nhs;
   const LaunchEvents ev = take_launch_events();
   const char* who = "nhs_select_resolve_items";
-  if (top_pages < 1 || page_size < 1 || (int64_t)top_pages * page_size > kLargeMaxK)
-    return fail(NHS_ERR_INVALID, "%s: need top_pages, page_size >= 1", who);
+  if (top_pages < 1 || page_size < 1) return fail(NHS_ERR_INVALID, "%s: need top_pages, page_size >= 1", who);
+  if ((int64_t)top_pages * page_size > kLargeMaxK)
+    return fail(NHS_ERR_UNSUPPORTED, "%s: top_pages * page_size must be <= %d", who, kLargeMaxK);
   const int32_t n = top_pages * page_size;
   int st = check_resolve(who, batch, n, scores, hot_rows, lengths, 0, page_size, physical, miss_host, miss_device,
                          plan_stride, counts);

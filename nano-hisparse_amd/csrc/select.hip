@@ -1096,13 +1096,14 @@ static int quest_select(const char* who, int32_t batch, const void* query, int32
 #undef NHS_QUEST_CASE
     }
   }
-  if (top_pages < max_pages) {  // scores are not needed when every page is kept
-    if (!kernel) return fail(NHS_ERR_UNSUPPORTED, "%s: no scoring kernel", who);
-    launch(kernel, grid, block, lds, s, ev.start, pages ? nullptr : ev.stop, a);
-    ev.start = nullptr;  // the start event belongs to the first kernel
-    st = launch_status(who);
-    if (st != NHS_OK) return st;
-  }
+  // The scores are computed also when every page is kept (top_pages >=
+  // max_pages): scores[b, :] then still holds them, and the caller's start
+  // event always stamps this first kernel.
+  if (!kernel) return fail(NHS_ERR_UNSUPPORTED, "%s: no scoring kernel", who);
+  launch(kernel, grid, block, lds, s, ev.start, pages ? nullptr : ev.stop, a);
+  ev.start = nullptr;  // the start event belongs to the first kernel
+  st = launch_status(who);
+  if (st != NHS_OK) return st;
   if (!pages) return NHS_OK;  // scores only
   SelectArgs sa;
   sa.scores = scores;
@@ -1185,7 +1186,7 @@ extern "C" int nhs_mean_select(int32_t batch, const void* query, int32_t q_dtype
   a.scores = scores;
   dim3 grid((unsigned)((max_pages + kPagesPerBlock - 1) / kPagesPerBlock), (unsigned)batch);
   size_t lds = ((size_t)kv_heads * head_dim + (size_t)kScoreWaves * kv_heads) * sizeof(float);
-  if (top_pages < max_pages) {
+  {  // computed also when every page is kept, as the Quest scores are
     hipEvent_t stop = pages ? nullptr : ev.stop;
     if (vec)
       launch(mean_score_kernel<4>, grid, dim3(kScoreThreads), lds, s, ev.start, stop, a);

@@ -2,10 +2,13 @@
 
 The row lease resolves the selection and gathers the missed rows; the
 attention itself is libnhs_hip.so's split-K GQA row kernel on the compute
-stream. `backend` keeps the reference's argument: "auto", "hip" and
-"triton" all name the HIP kernels on a GPU cache; "torch", the reference's
-torch path, is not part of this build on the GPU. CPU caches compute only
-through a CPU kernel provider that a test harness installs.
+stream. `backend` keeps the reference's argument (`auto|torch|triton`,
+reference attention.py:8-9, cli.py:48, engine.py:30) plus "hip": on a GPU
+cache every one of them runs the HIP kernel, so a caller that asks for the
+reference's torch path or its Triton kernels gets the same masked softmax
+over the same rows from the one GPU implementation (no second code path).
+CPU caches compute only through a CPU kernel provider that a test harness
+installs.
 """
 
 import torch
@@ -25,8 +28,6 @@ def row_attention(query, cache, request_id, layer, topk, backend="auto"):
         raise ValueError("selection must have one row per query head")
     if backend == "triton" and not cache.storage.cuda:
         raise ValueError("Triton requires CUDA")
-    if backend == "torch" and cache.storage.cuda:
-        raise ValueError("backend 'torch' is the reference's CPU path; on the GPU use 'auto' (libnhs_hip.so)")
     with cache.resolve(request_id, layer, topk) as lease:
         rows = lease.plan.physical_rows
         if rows.ndim == 1:

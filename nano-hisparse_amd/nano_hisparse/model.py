@@ -322,6 +322,11 @@ class Model(nn.Module):
         return _linear(self.model.norm(x), self.lm_head.weight, self.lm_head.bias).float()
 
 
+    def clear_decode_graphs(self):
+        """Drops every captured decode-step graph, with the cache, buffers and
+        graph memory each one holds."""
+        self.__dict__.pop("_decode_graphs", None)
+
     def _decode_batch_graph(self, tokens, request_ids, cache, top_k, cuts):
         """decode_batch with the step's launches (every layer of every group,
         the final norm and the lm_head) captured once per batch composition
@@ -344,6 +349,10 @@ class Model(nn.Module):
         store = cache.storage
         store.check_stream()
         graphs = self.__dict__.setdefault("_decode_graphs", {})
+        # graphs captured against another cache hold that cache (its pool),
+        # their buffers and their private memory: drop them
+        for stale in [k for k, e in graphs.items() if e["cache"] is not cache]:
+            del graphs[stale]
         spans = list(zip(cuts, cuts[1:]))
         overlap = len(spans) > 1
         key = (tuple(request_ids), top_k, len(spans))

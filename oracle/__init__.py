@@ -52,6 +52,7 @@ def lib():
         _lib.oracle_attend_rows.argtypes = [
             p, i32, i64, i64, p, i32, p, i64, i64, i64, i32, i32, i32, i32, i32, i32, f32p,
         ]
+        _lib.oracle_attend_rows_f32.argtypes = _lib.oracle_attend_rows.argtypes
         _lib.oracle_quest_select.argtypes = [
             i32, p, i32, i64, i64, p, p, i32, i64, i32, i32, i32, p, i32, i32, i32, i32, p, p, p,
         ]
@@ -63,6 +64,7 @@ def lib():
         for name in (
             "oracle_gather_rows",
             "oracle_attend_rows",
+            "oracle_attend_rows_f32",
             "oracle_quest_select",
             "oracle_mean_select",
             "oracle_resolve_rows",
@@ -109,8 +111,11 @@ def gather_rows(host, pool, miss_host, miss_device, page_size):
 # ---- attention (attention.py:26-35) ----------------------------------------------
 
 
-def attend_rows(query, pool, rows, page_size):
-    """query [B, Hq, D]; rows [B, Hq, N] int64 (or [B, N] shared); fp32 out."""
+def attend_rows(query, pool, rows, page_size, arithmetic="float64"):
+    """query [B, Hq, D]; rows [B, Hq, N] int64 (or [B, N] shared); fp32 out.
+    arithmetic "float64": the masked softmax accumulated in double (the
+    checker); "float32": the reference CPU path's own float32 arithmetic
+    (oracle_attend_rows_f32, the CPU baseline's attention)."""
     import torch
 
     B, Hq, D = query.shape
@@ -123,7 +128,8 @@ def attend_rows(query, pool, rows, page_size):
     rows = rows.contiguous()
     out = torch.empty(B, Hq, D, dtype=torch.float32)
     query, pool = query.contiguous(), pool.contiguous()
-    lib().oracle_attend_rows(
+    fn = {"float64": lib().oracle_attend_rows, "float32": lib().oracle_attend_rows_f32}[arithmetic]
+    fn(
         _ptr(query), _dtype_code(query), Hq * D, D, _ptr(pool), _dtype_code(pool), _ptr(rows),
         Hq * rows.shape[-1], rows.shape[-1], 1, B, rows.shape[-1], Hq, kv_heads, D, page_size, _ptr(out),
     )

@@ -8,6 +8,8 @@
  *   oracle_gather_rows   nano_hisparse/hybrid.py:452-459 (CPU gather loop)
  *   oracle_attend_rows   nano_hisparse/attention.py:26-35 (masked softmax);
  *                        computed in double precision
+ *   oracle_attend_rows_f32  the same, in the reference path's float32
+ *                        arithmetic (the CPU baseline's attention)
  *   oracle_quest_select  nano_hisparse/selection.py:69-91 + :44-62
  *   oracle_mean_select   nano_hisparse/selection.py:119-145
  *   oracle_resolve_rows  nano_hisparse/row_index.py:62-140
@@ -161,6 +163,62 @@ void oracle_attend_rows(const void* q, int q_dtype, int64_t q_bs, int64_t q_hs, 
     }
   free(s);
   free(acc);
+}
+
+/* The reference's CPU attention (attention.py:26-35) in its own float32
+   arithmetic: K and V widened to float32; a row's score is the float32 sum
+   over d of q[d] * k[d] (products rounded, summed in d order) times the
+   float32 value of head_dim^-0.5; masked rows get -inf; softmax as
+   exp(s - max) / sum in float32; NaN weights (every row masked) become 0
+   (nan_to_num); the output is the float32 sum of weight * v in row order. */
+void oracle_attend_rows_f32(const void* q, int q_dtype, int64_t q_bs, int64_t q_hs, const void* pool, int kv_dtype,
+                            const int64_t* rows, int64_t r_bs, int64_t r_hs, int64_t r_cs, int batch, int n_rows,
+                            int q_heads, int kv_heads, int head_dim, int page_size, float* out) {
+  const int group = q_heads / kv_heads;
+  const float scale = (float)(1.0 / sqrt((double)head_dim));
+  float* s = (float*)malloc(sizeof(float) * (size_t)n_rows);
+  float* qv = (float*)malloc(sizeof(float) * (size_t)head_dim);
+  for (int b = 0; b < batch; ++b)
+    for (int h = 0; h < q_heads; ++h) {
+      const int kh = h / group;
+      for (int d = 0; d < head_dim; ++d) qv[d] = load_elem(q, q_dtype, (int64_t)b * q_bs + (int64_t)h * q_hs + d);
+      float mx = -INFINITY;
+      for (int c = 0; c < n_rows; ++c) {
+        int64_t r = rows[(int64_t)b * r_bs + (int64_t)h * r_hs + (int64_t)c * r_cs];
+        s[c] = -INFINITY;
+        if (r < 0) continue;
+        int64_t k0 = ((r / page_size) * 2 * page_size + r % page_size) * (int64_t)kv_heads * head_dim +
+                     (int64_t)kh * head_dim;
+        float dot = 0.0f;
+        for (int d = 0; d < head_dim; ++d) {
+          const float prod = load_elem(pool, kv_dtype, k0 + d) * qv[d];
+          dot += prod;
+        }
+        s[c] = dot * scale;
+        if (s[c] > mx) mx = s[c];
+      }
+      float* o = out + ((int64_t)b * q_heads + h) * head_dim;
+      for (int d = 0; d < head_dim; ++d) o[d] = 0.0f;
+      if (mx == -INFINITY) continue;  /* softmax of all -inf is NaN, then 0 */
+      float den = 0.0f;
+      for (int c = 0; c < n_rows; ++c) {
+        s[c] = s[c] == -INFINITY ? 0.0f : expf(s[c] - mx);
+        den += s[c];
+      }
+      for (int c = 0; c < n_rows; ++c) {
+        int64_t r = rows[(int64_t)b * r_bs + (int64_t)h * r_hs + (int64_t)c * r_cs];
+        if (r < 0) continue;
+        const float w = s[c] / den;
+        int64_t v0 = ((r / page_size) * 2 * page_size + page_size + r % page_size) * (int64_t)kv_heads * head_dim +
+                     (int64_t)kh * head_dim;
+        for (int d = 0; d < head_dim; ++d) {
+          const float prod = w * load_elem(pool, kv_dtype, v0 + d);
+          o[d] += prod;
+        }
+      }
+    }
+  free(s);
+  free(qv);
 }
 
 /* ---- selectors ---------------------------------------------------------------- */

@@ -25,6 +25,8 @@ OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "reference_plumbi
 
 
 def main():
+    # the reference tree is read-only: importing it must not write bytecode there
+    sys.dont_write_bytecode = True
     # the reference's package, not this repository's (same package name)
     sys.path[:] = [REFERENCE] + [p for p in sys.path if "nano-hisparse_amd" not in p and p not in ("", ".")]
     import torch

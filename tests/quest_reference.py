@@ -1,5 +1,5 @@
-"""The reference's Quest page choice, evaluated with torch operations, and a
-tie-aware comparison of page sets against it.
+"""The reference's Quest and page-mean page choices, evaluated with torch
+operations, and a tie-aware comparison of page sets against them.
 
 reference_scores() evaluates nano_hisparse/selection.py:82-85 as written
 there (torch.maximum of the two products per query head, summed over the
@@ -8,6 +8,15 @@ no fp32 rounding; 0 * inf, NaN and opposite infinities behave as in float32.
 reference_ranked() applies selection.py:86-89 (forced pages set to +inf).
 torch.topk ranks NaN above every number (aten's CPU comparator tests isnan
 before >), so check_page_set() orders NaN > +inf > finite > -inf.
+
+mean_reference_ranked() evaluates the page-mean selector,
+nano_hisparse/selection.py:131-143: the early returns (every page when
+top_k >= count; the required pages alone when top_k equals their number),
+the required pages ([count - 1] for top_k == 1, else [0, count - 1]), the
+group-mean query in float32 as written there, its dot products with the
+summaries in float64, and the required pages set to -inf before
+torch.topk; check_mean_pages() applies check_page_set() to the pages chosen
+beside the required ones.
 
 Where the k-th and (k+1)-th reference keys tie (equal class, or finite
 scores closer than `tol`), torch's choice inside the tie is not defined by
@@ -148,3 +157,35 @@ def special_case(seed, Hq, Hkv, D, n_pages, nan_pages, inf_query=False, dtype=to
     if inf_query:  # a zero bound against the infinite query would make p_zero NaN
         lo[p_zero, kq, 3], hi[p_zero, kq, 3] = 1.0, 2.0
     return q.to(dtype), lo.to(dtype), hi.to(dtype), set(nan_set)
+
+
+def mean_reference_ranked(q, summaries, length, page_size, top_k):
+    """q [Hq, D]; summaries [pages, Hkv, D]. Returns (pages, None) for the
+    early returns of selection.py:131-137, else (required, ranked): the
+    scores [count] in float64 with the required pages at -inf
+    (selection.py:138-143)."""
+    count = quest_count(length, page_size)
+    if top_k >= count:
+        return list(range(count)), None
+    required = [count - 1] if top_k == 1 else [0, count - 1]
+    if top_k == len(required):
+        return sorted(required), None
+    kv_heads = summaries.shape[1]
+    grouped = q.float().reshape(kv_heads, q.shape[0] // kv_heads, -1).mean(1)
+    scores = torch.einsum("hd,phd->p", grouped.double(), summaries[:count].double())
+    scores[required] = -math.inf
+    return required, scores
+
+
+def check_mean_pages(got, q, summaries, length, page_size, top_k, tol=1e-5):
+    """Asserts that `got` is the reference's page-mean choice: the required
+    pages plus a top-(top_k - len(required)) of the reference scores,
+    tie-aware; returns True when that choice is unique."""
+    required, ranked = mean_reference_ranked(q, summaries, length, page_size, top_k)
+    got = sorted(int(p) for p in got if int(p) >= 0)
+    if ranked is None:
+        assert got == required, (got, required)
+        return True
+    assert set(required) <= set(got), (got, required)
+    chosen = [p for p in got if p not in required]
+    return check_page_set(chosen, ranked, top_k - len(required), tol)

@@ -260,3 +260,23 @@ def test_graph_replayed_decode_equals_the_eager_decode(gpu, micro_batches):
         assert torch.equal(le.view(torch.int32), lr.view(torch.int32)), i
     graphs = model.__dict__["_decode_graphs"]
     assert 1 <= len(graphs) < len(pairs)  # most steps replayed an existing graph
+    # A step on another cache drops the graphs captured against the old one,
+    # which then keep neither that cache (its pool) nor their memory alive;
+    # clear_decode_graphs() drops the rest.
+    import gc
+    import weakref
+
+    old_cache = weakref.ref(replayed.cache)
+    del replayed
+    fresh = engine(True)
+    for _ in range(2):
+        fresh.step()
+    torch.cuda.synchronize()
+    graphs = model.__dict__["_decode_graphs"]
+    assert graphs and all(e["cache"] is fresh.cache for e in graphs.values())
+    gc.collect()
+    assert old_cache() is None
+    model.clear_decode_graphs()
+    assert "_decode_graphs" not in model.__dict__
+    fresh.step()  # captures again
+    assert len(model.__dict__["_decode_graphs"]) == 1

@@ -136,6 +136,13 @@ def test_fused_select_resolve_rejects_shapes_beyond_its_selection(gpu):
     with pytest.raises(RuntimeError, match="4096"):  # more positions than the LDS holds
         rk.select_resolve_batched(scores[:, :512], tabs[0][:, :512], tabs[1][:, :512], hot, tags, lru, 512 * P, P,
                                   513)
+    # beyond the resolver's 32768 positions: NHS_ERR_UNSUPPORTED (the caller
+    # may fall back to two launches); a budget below 1 is NHS_ERR_INVALID
+    with pytest.raises(RuntimeError, match=r"status -2: .*32768"):
+        rk.select_resolve_batched(scores[:, :1024], tabs[0][:, :1024], tabs[1][:, :1024], hot, tags, lru,
+                                  1024 * 64, 64, 520)
+    with pytest.raises(RuntimeError, match=r"status -1: .*top_pages"):
+        rk.select_resolve_batched(scores[:, :512], tabs[0][:, :512], tabs[1][:, :512], hot, tags, lru, 512 * P, P, 0)
 
 
 @pytest.mark.gpu

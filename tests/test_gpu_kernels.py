@@ -7,6 +7,8 @@ order; attention must be within max-abs 2e-2 (bf16/fp16) or 1e-4 (fp32) of
 the oracle's float64 masked softmax.
 """
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -517,6 +519,68 @@ def test_mean_select_bit_exact(gpu, B, Hq, Hkv, D, P, n_pages, top):
     pages, pos, scores = rk.mean_batched(q.to(gpu), summ.to(gpu), lengths.to(gpu), P, top)
     assert torch.equal(pages.cpu(), e_pages)
     assert torch.equal(pos.cpu(), e_pos)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("top", [1, 2, 3, 6, 29])
+def test_mean_select_nan_summaries_match_oracle_and_reference(gpu, top):
+    """NaN page summaries (below, at and above the budget) and NaN summaries
+    on the required first and last pages: pages, positions and every score
+    (NaN as 0x7fc00000) equal the oracle's, and the pages are the reference
+    page-mean choice (selection.py:131-145 with torch ops), tie-aware."""
+    from quest_reference import check_mean_pages
+
+    log_case(test="mean-nan", top=top)
+    B, Hq, Hkv, D, P, n_pages = 4, 8, 2, 16, 4, 30
+    g = torch.Generator().manual_seed(40 + top)
+    q = torch.randn(B, Hq, D, generator=g)
+    summ = torch.randn(B, n_pages, Hkv, D, generator=g)
+    for b, n_nan in enumerate((0, 3, 9, 27)):
+        for p in (torch.randperm(n_pages - 2, generator=g)[:n_nan] + 1).tolist():
+            summ[b, p, p % Hkv, p % D] = math.nan
+    summ[2, 0, 0, 1] = math.nan  # required pages: kept whatever their summary
+    summ[2, n_pages - 1, 1, 3] = math.nan
+    lengths = torch.tensor([n_pages * P, n_pages * P - 3, n_pages * P - 1, 20 * P + 2])
+    e_scores, e_pages, e_pos = oracle.mean_select(q, summ, lengths, P, top)
+    pages, pos, scores = rk.mean_batched(q.to(gpu), summ.to(gpu), lengths.to(gpu), P, top)
+    pages, pos, scores = pages.cpu(), pos.cpu(), scores.cpu()
+    assert torch.equal(pages, e_pages)
+    assert torch.equal(pos, e_pos)
+    for b in range(B):
+        count = -(-int(lengths[b]) // P)
+        if top < count:
+            assert torch.equal(scores[b, :count].view(torch.int32), e_scores[b, :count].view(torch.int32))
+        check_mean_pages(pages[b], q[b], summ[b], int(lengths[b]), P, top)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["quest", "mean"])
+def test_scores_are_kept_when_every_page_is_selected(gpu, mode):
+    """top_pages >= max_pages keeps every page; the scores output still holds
+    every page's score, bit-identical to the oracle's (computed there with a
+    smaller budget: the scores do not depend on it)."""
+    log_case(test="scores-all-pages", mode=mode)
+    B, Hq, Hkv, D, P, n_pages = 2, 8, 2, 64, 16, 12
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(B, Hq, D, generator=g).to(torch.bfloat16)
+    lengths = torch.tensor([n_pages * P, n_pages * P - 9])
+    if mode == "quest":
+        mn, mx = _bounds(g, B, n_pages, Hkv, D, torch.bfloat16, offsets=True)
+        e_scores, _, _ = oracle.quest_select(q, mn, mx, lengths, P, 1)
+        run = lambda top, select: rk.quest_batched(q.to(gpu), mn.to(gpu), mx.to(gpu), lengths.to(gpu), P, top,
+                                                   select=select)
+    else:
+        summ = torch.randn(B, n_pages, Hkv, D, generator=g)
+        e_scores, _, _ = oracle.mean_select(q, summ, lengths, P, 1)
+        run = lambda top, select: rk.mean_batched(q.to(gpu), summ.to(gpu), lengths.to(gpu), P, top, select=select)
+    for top in (n_pages, n_pages + 5):
+        for select in (True, False):
+            pages, _, scores = run(top, select)
+            for b in range(B):
+                count = -(-int(lengths[b]) // P)
+                assert torch.equal(scores.cpu()[b, :count].view(torch.int32), e_scores[b, :count].view(torch.int32))
+                if select:
+                    assert pages.cpu()[b].tolist() == list(range(count)) + [-1] * (top - count)
 
 
 # ---- append ---------------------------------------------------------------------------

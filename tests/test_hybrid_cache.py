@@ -225,6 +225,29 @@ def test_low_precision_rows_gather_and_attend(gpu, dtype):
 
 
 @pytest.mark.gpu
+def test_every_reference_backend_name_runs_the_hip_kernel_on_a_gpu_cache(gpu):
+    """The reference accepts backend auto|torch|triton on CUDA tensors
+    (attention.py:8-35, cli.py:48, engine.py:30); on a GPU cache each name,
+    and "hip", runs the one HIP kernel, so the outputs are bit-identical and
+    match the dense reference; an unknown name still raises."""
+    torch.manual_seed(11)
+    cache = make("cuda:0", dtype=torch.bfloat16, page_size=8, head_dim=64, kv_heads=2)
+    cache.reserve("a", 120, 1)
+    k, v = append(cache, count=100)
+    q = torch.randn(8, 64, device="cuda", dtype=torch.bfloat16)
+    chosen = [0, 9, 63, 99]  # HotConfig(4, 4): at most 4 rows
+    outs = {}
+    for backend in ("auto", "torch", "triton", "hip"):
+        outs[backend] = row_attention(q, cache, "a", 0, positions(cache, chosen), backend=backend)
+    for backend, out in outs.items():
+        assert torch.equal(out, outs["auto"]), backend
+    torch.testing.assert_close(outs["torch"], dense_attention(q, k[chosen], v[chosen]), atol=0.004, rtol=0.02)
+    with pytest.raises(ValueError, match="invalid attention backend"):
+        row_attention(q, cache, "a", 0, positions(cache, chosen), backend="cuda")
+    cache.assert_invariants()
+
+
+@pytest.mark.gpu
 def test_resolver_replays_in_a_captured_graph_without_host_reads(gpu):
     cache = make("cuda:0")
     cache.reserve("a", 40, 1)

@@ -179,6 +179,62 @@ def test_mean_select_forces_first_and_last_page():
         assert pages[0].tolist() == want
 
 
+def _mean_case(seed, n_pages=30, Hq=8, Hkv=2, D=16, nan_pages=0, nan_required=False, tie_groups=0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(Hq, D, generator=g)
+    summ = torch.randn(n_pages, Hkv, D, generator=g)
+    if tie_groups:  # pages that repeat a few summary rows tie exactly
+        idx = torch.randint(0, tie_groups, (n_pages,), generator=g)
+        summ = summ[idx].clone()
+    for p in (torch.randperm(n_pages - 2, generator=g)[:nan_pages] + 1).tolist():
+        summ[p, p % Hkv, p % D] = math.nan
+    if nan_required:  # the reference sets the required pages to -inf whatever their summary
+        summ[0, 0, 1] = math.nan
+        summ[n_pages - 1, Hkv - 1, 3] = math.nan
+    return q, summ
+
+
+@pytest.mark.parametrize("seed,nan_pages,nan_required,tie_groups",
+                         [(0, 0, False, 0), (1, 3, False, 0), (2, 9, True, 0), (3, 0, True, 4), (4, 27, False, 0),
+                          (5, 5, True, 3)])
+def test_mean_select_matches_the_reference_formula_tie_aware(seed, nan_pages, nan_required, tie_groups):
+    """oracle.mean_select against the reference's page-mean selector
+    (selection.py:131-145) evaluated with torch ops (quest_reference): budgets
+    1 and 2 (the required pages alone), 3 .. count - 1, and >= count (every
+    page); NaN summaries below, at and above the budget (torch.topk ranks
+    NaN above every number), required pages whose own summary is NaN (set to
+    -inf, still kept), and exact ties between repeated summary rows. The
+    chosen pages beside the required ones must be a top-k of the reference
+    scores, with any choice inside a tie at the k-th rank accepted."""
+    from quest_reference import check_mean_pages
+
+    n_pages, P = 30, 4
+    q, summ = _mean_case(seed, n_pages, nan_pages=nan_pages, nan_required=nan_required, tie_groups=tie_groups)
+    for length in (n_pages * P, n_pages * P - 3, 9 * P + 1):
+        count = -(-length // P)
+        for top in (1, 2, 3, 5, 8, count - 1, count, count + 4):
+            _, pages, positions = oracle.mean_select(q[None], summ[None], [length], P, top)
+            got = [p for p in pages[0].tolist() if p >= 0]
+            assert len(got) == min(top, count), (length, top, got)
+            check_mean_pages(got, q, summ, length, P, top)
+            want_pos = [t for p in got for t in range(p * P, min((p + 1) * P, length))]
+            assert [t for t in positions[0].tolist() if t >= 0] == want_pos
+    # a planted mistake in the oracle's output fails the check: a NaN page
+    # dropped for the best finite one
+    if nan_pages and not tie_groups:
+        from quest_reference import mean_reference_ranked
+
+        top = 3 + min(nan_pages, 3)
+        _, pages, _ = oracle.mean_select(q[None], summ[None], [n_pages * P], P, top)
+        required, ranked = mean_reference_ranked(q, summ, n_pages * P, P, top)
+        nan_chosen = [p for p in pages[0].tolist() if p not in required and math.isnan(ranked[p])]
+        assert nan_chosen
+        finite = [p for p in range(n_pages) if p not in pages[0].tolist() and math.isfinite(ranked[p])]
+        bad = sorted(set(pages[0].tolist()) - {nan_chosen[0]} | {max(finite, key=lambda p: ranked[p])})
+        with pytest.raises(AssertionError):
+            check_mean_pages(bad, q, summ, n_pages * P, P, top)
+
+
 # ---- attention and gather ---------------------------------------------------------------
 
 
@@ -207,6 +263,47 @@ def test_attention_single_row_and_uniform_keys_closed_forms():
     torch.testing.assert_close(out[0, 0], mean_v, atol=1e-6, rtol=1e-6)
     out = oracle.attend_rows(q, pool, torch.tensor([[-1, 6, -1]]), P)
     torch.testing.assert_close(out[0, 1], pool[1, 1, 2, 0], atol=1e-6, rtol=1e-6)
+
+
+def _reference_attention_torch(q, pool, rows, P):
+    """The reference's CPU attention formula (attention.py:26-35) evaluated
+    with torch's own float32 kernels: q [Hq, D], rows [Hq, N]."""
+    Hq, D = q.shape
+    Hkv = pool.shape[3]
+    safe = rows.clamp(min=0)
+    kv_head = (torch.arange(Hq) // (Hq // Hkv))[:, None]
+    k = pool[safe // P, 0, safe % P, kv_head].float()
+    v = torch.where((rows >= 0)[..., None], pool[safe // P, 1, safe % P, kv_head].float(), 0.0)
+    scores = (k * q.float()[:, None]).sum(-1) * D**-0.5
+    weights = scores.masked_fill(rows < 0, -torch.inf).softmax(-1).nan_to_num()
+    return (weights[..., None] * v).sum(1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_float32_attention_follows_the_reference_cpu_arithmetic(dtype):
+    """oracle_attend_rows_f32 (the CPU baseline's attention) against the
+    reference formula run by torch in float32 and against the float64
+    numpy softmax: within float32 rounding (1e-5), masked and fully masked
+    heads included; dropping the scale or the max shift would fail it."""
+    g = torch.Generator().manual_seed(3)
+    P, Hkv, D, Hq, N = 8, 2, 64, 8, 300
+    pool = (torch.randn(60, 2, P, Hkv, D, generator=g) * 2).to(dtype)
+    q = torch.randn(2, Hq, D, generator=g).to(dtype)
+    rows = torch.randint(-1, 60 * P, (2, Hq, N), generator=g)
+    rows[1, 3] = -1  # a head with every row masked: 0
+    out = oracle.attend_rows(q, pool, rows, P, arithmetic="float32")
+    exact = oracle.attend_rows_float64(q, pool, rows, P)
+    assert np.abs(out.numpy() - exact).max() < 1e-5
+    assert not out[1, 3].any()
+    for b in range(2):
+        ref = _reference_attention_torch(q[b], pool, rows[b], P)
+        torch.testing.assert_close(out[b], ref, atol=1e-5, rtol=1e-5)
+    # a single valid row returns its V exactly (weight 1)
+    one = torch.full((1, Hq, 5), -1, dtype=torch.int64)
+    one[0, :, 2] = 17
+    out1 = oracle.attend_rows(q[:1], pool, one, P, arithmetic="float32")
+    for h in range(Hq):
+        assert torch.equal(out1[0, h], pool[17 // P, 1, 17 % P, h // (Hq // Hkv)].float())
 
 
 def test_gather_closed_form_matches_fancy_indexing():
