@@ -25,6 +25,7 @@
 // zero block) must be zero before the first call; every call leaves them so.
 #include <math.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -549,6 +550,458 @@ __global__ __launch_bounds__(kAttendThreads) void attend_kernel(AttendArgs a) {
   if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- attend_mfma_kernel: Q K^T on MFMA, P V on the VALU ---------------------
+//
+// Serves 16-bit KV with a query of the same dtype, head_dim 128, one row list
+// shared by the query heads of a request and at most 8 query heads per KV
+// head (the GQA shapes of Llama-3-8B and Qwen2-7B). A workgroup of 8 waves
+// (two per SIMD) owns one (request, KV head, row split): every row is read
+// once per KV head, and the row-level work (addresses, score reduction,
+// softmax) is done once per row instead of once per 16-lane row slot. Wave w
+// takes tiles w, w + 8, ... of 16 rows, stages their K / V byte offsets in
+// its own part of LDS, and works in rounds: the loads of kMDepth tiles, then
+// their computation (no loaded register is carried across rounds). The two
+// waves of a SIMD are kept level by issue priorities. Per tile, in one wave:
+//  - lane l loads chunk l % 16 (16 bytes) of K and of V of rows 4i + l / 16,
+//    i = 0..3: each load instruction covers 4 whole 256-byte head rows;
+//  - the K chunks go through the wave's LDS tile (chunk c of row r at slot
+//    c ^ r: both the writes and the reads below are free of bank conflicts)
+//    into the MFMA operand layout of v_mfma_f32_16x16x32 (measured on gfx950:
+//    lane l supplies A[l % 16][8 (l / 16) + j] and B[8 (l / 16) + j][l % 16],
+//    j = 0..7, and holds D[4 (l / 16) + i][l % 16], i = 0..3): A = the query
+//    (head l % 16, zero beyond the group), B = K^T (row l % 16), four k-steps
+//    of 32 dims, so lane l ends with the scores of heads 4 (l / 16) + i against
+//    row l % 16;
+//  - a DPP max over the 16 lanes that share a head gives the tile's max, and
+//    the online softmax in base 2 (scale * log2 e applied to the scores)
+//    updates the head's running max, its per-lane partial denominators, and
+//    P = exp2(score - max);
+//  - P goes through LDS to the layout of the V chunks: lane l accumulates
+//    P[h][row] * V[row][8 (l % 16) + e] in fp32 for every head h of the group
+//    over its rows 4i + l / 16 (the weights stay fp32, as the reference's
+//    numerator, row_kernels.py:109-110). When a head's running max moves, its
+//    accumulators are scaled by exp2(m_old - m_new), read to a scalar from a
+//    lane that holds the head (a factor of exactly 1 is skipped: the bits
+//    are the same).
+// At the end the four row classes of a wave (lanes l, l ^ 16, l ^ 32, l ^ 48,
+// whose accumulators share each head's running max) are summed, the waves
+// merge through LDS, and a row split is merged across workgroups by the last
+// one to arrive, as in attend_kernel.
+constexpr int kMThreads = 512;
+constexpr int kMWaves = kMThreads / kWave;
+constexpr int kMD = 128;       // head_dim
+constexpr int kMTile = 16;     // rows per tile: the MFMA's N
+constexpr int kMStage = 1024;  // rows staged in LDS per pass
+constexpr int kMMaxGroup = 8;
+constexpr int kMDepth = 2;  // tiles whose loads a wave issues together
+constexpr int kMWs = kMD + 4;     // floats per partial row in the workspace: m, l, 2 unused, acc
+constexpr int kMMaxSplits = 16;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+struct AttendMArgs {
+  const void* q;
+  int64_t q_bs, q_hs;
+  const char* pool;
+  const int64_t* rows;
+  int64_t r_bs, r_cs;
+  int n_rows, rows_per_split, n_splits;
+  int q_heads, kv_heads, group, page_size;
+  int kv_items;
+  FastDiv page_div;
+  int64_t block_stride;  // pool block stride, bytes
+  int64_t row_bytes;     // one plane row, all KV heads, bytes
+  float qscale;
+  const char* zeros;  // kZeroBytes of zeros
+  float* ws;          // partials [B, q_heads, n_splits, 2 + head_dim]
+  int* counters;      // [B, kv_heads]
+  void* out;
+  int64_t out_bs, out_hs;
+};
+
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  if constexpr (T::dtype == NHS_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+}
+
+// max over the 16 lanes of a DPP row, in every lane of the row
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp_f32<0xB1>(x));   // lane ^ 1
+  x = fmaxf(x, dpp_f32<0x4E>(x));   // lane ^ 2
+  x = fmaxf(x, dpp_f32<0x141>(x));  // quads swap within 8
+  x = fmaxf(x, dpp_f32<0x140>(x));  // halves swap within 16
+  return x;
+}
+
+__device__ __forceinline__ float readlane_f32(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Keeps the compiler from moving memory accesses across this point: the
+// LDS tiles are written by some lanes of a wave and read by others, which
+// the hardware orders (a wave's LDS instructions execute in order) but the
+// compiler cannot see.
+__device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
+
+// Four 16-byte agent-coherent (sc1) loads, waited for before the asm ends
+// (so the compiler never sees registers with loads in flight).
+__device__ __forceinline__ void ld4x16_coherent(const u32x4_t* p0, const u32x4_t* p1, const u32x4_t* p2,
+                                                const u32x4_t* p3, u32x4_t (&o)[4]) {
+  asm volatile(
+      "global_load_dwordx4 %0, %4, off sc1\n\t"
+      "global_load_dwordx4 %1, %5, off sc1\n\t"
+      "global_load_dwordx4 %2, %6, off sc1\n\t"
+      "global_load_dwordx4 %3, %7, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3])
+      : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
+      : "memory");
+}
+
+// one tile's loaded chunks: K and V of rows 4i + lane / 16
+struct MTile {
+  u32x4_t k[4], v[4];
+};
+
+template <typename T, int G, int DEPTH>
+__global__ __launch_bounds__(kMThreads) void attend_mfma_kernel(AttendMArgs a) {
+  constexpr int GQ = (G + 3) / 4;  // 4-head groups of MFMA output lanes
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int lrow = lane & 15;  // MFMA row / chunk of a loaded row
+  const int lgrp = lane >> 4;  // MFMA k-group / loaded row within 4
+  // grid: id = kv_item + kv_items * split, so the splits of a (request, KV
+  // head) are kv_items apart (on one XCD when kv_items is a multiple of 8)
+  const int kv_item = (int)(blockIdx.x % (unsigned)a.kv_items);
+  const int split = (int)(blockIdx.x / (unsigned)a.kv_items);
+  const int b = kv_item / a.kv_heads;
+  const int kh = kv_item - b * a.kv_heads;
+  const int h0 = kh * a.group;
+  const int64_t* rows = a.rows + (int64_t)b * a.r_bs;
+
+  // the query as the MFMA A operand: head lrow, dims 8 lgrp + 32 ks .. +8
+  u32x4_t qa[kMD / 32];
+#pragma unroll
+  for (int ks = 0; ks < kMD / 32; ++ks) {
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (lrow < G) {
+      const uint16_t* qp = static_cast<const uint16_t*>(a.q) + (int64_t)b * a.q_bs + (int64_t)(h0 + lrow) * a.q_hs +
+                           8 * lgrp + 32 * ks;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = (uint32_t)qp[2 * e] | ((uint32_t)qp[2 * e + 1] << 16);
+    }
+    qa[ks] = (u32x4_t){w[0], w[1], w[2], w[3]};
+  }
+
+  float m[4], lsum[4];  // heads 4 lgrp + i: running max, this lane's partial denominator
+  float acc[G][8];      // heads 0..G-1, dims 8 lrow + e, over this lane's rows
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    lsum[i] = 0.f;
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+
+  // K, V byte offsets from the head's pool base and 1 for a valid row, of a
+  // pass's rows, padded with masked rows to whole rounds of DEPTH tiles per
+  // wave
+  constexpr int kRound = DEPTH * kMTile * kMWaves;
+  __shared__ __attribute__((aligned(16))) int64_t soff[kMStage + kRound][2];
+  __shared__ uint8_t sok[kMStage + kRound];
+  __shared__ u32x4_t ktile[kMWaves][kMTile][16];                      // K chunks, swizzled
+  __shared__ __attribute__((aligned(16))) float ptile[kMWaves][kMTile][16];  // P[row][head]
+  __shared__ int progress[kMWaves];                                           // tiles each wave has started
+
+  const char* pool_kh = a.pool + (int64_t)kh * kMD * T::bytes;
+  const int64_t zoff = a.zeros - pool_kh;  // masked rows read the zero block
+  const char* pool_lane = pool_kh + lrow * 16;
+  const int64_t plane = (int64_t)a.page_size * a.row_bytes;
+  const int row_begin = split * a.rows_per_split;
+  const int row_end = min(a.n_rows, row_begin + a.rows_per_split);
+
+  if (threadIdx.x < kMWaves) progress[threadIdx.x] = 0;
+  __syncthreads();
+  int started = 0;  // tiles this wave has started, over all passes
+  for (int s0 = row_begin; s0 < row_end; s0 += kMStage) {
+    const int len = min(kMStage, row_end - s0);
+    const int padded = (len + kRound - 1) / kRound * kRound;
+    const int ntw = padded / (kMTile * kMWaves);  // tiles of each wave, a multiple of DEPTH
+    // Each wave stages the rows of its own tiles t = wave + kMWaves * j
+    // (lane: tile j0 + l / 16, row l % 16), so no workgroup barrier waits
+    // for the slowest wave's index loads; only this wave reads them.
+    for (int j0 = 0; j0 < ntw; j0 += 4) {
+      const int j = j0 + lgrp;
+      const int i = (wave + kMWaves * j) * kMTile + lrow;
+      const int64_t r = j < ntw && i < len ? rows[(int64_t)(s0 + i) * a.r_cs] : -1;
+      if (j < ntw) {
+        int64_t ko = zoff, vo = zoff;
+        if (r >= 0) {
+          const uint32_t blk = a.page_div.div((uint32_t)r);
+          ko = (int64_t)blk * a.block_stride + (int64_t)((uint32_t)r - blk * (uint32_t)a.page_size) * a.row_bytes;
+          vo = ko + plane;
+        }
+        soff[i][0] = ko;
+        soff[i][1] = vo;
+        sok[i] = r >= 0;
+      }
+    }
+    lds_order();
+
+    auto load = [&](int j, MTile& d) __attribute__((always_inline)) {
+      const int t = wave + kMWaves * j;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = t * kMTile + 4 * i + lgrp;
+        const int64_t ko = soff[r][0], vo = soff[r][1];
+        d.k[i] = *reinterpret_cast<const u32x4_t*>(pool_lane + ko);
+        d.v[i] = *reinterpret_cast<const u32x4_t*>(pool_lane + vo);
+      }
+    };
+    auto compute = [&](int j, const MTile& d) __attribute__((always_inline)) {
+      const int t = wave + kMWaves * j;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * i + lgrp;
+        ktile[wave][r][lrow ^ r] = d.k[i];
+      }
+      const bool ok = sok[t * kMTile + lrow];
+      lds_order();
+      f32x4_t s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kMD / 32; ++ks) s = mfma_16x16x32<T>(qa[ks], ktile[wave][lrow][(4 * ks + lgrp) ^ lrow], s);
+      float p[4], alpha[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float sc = ok ? s[i] * a.qscale : -INFINITY;
+        const float mx = fmaxf(m[i], row_max16(sc));
+        const float ref = mx == -INFINITY ? 0.f : mx;  // keeps exp2 arguments finite
+        // arguments are <= 0: v_exp_f32 without range reduction (a weight
+        // below 2^-126 flushes to 0)
+        alpha[i] = __builtin_amdgcn_exp2f(m[i] - ref);
+        p[i] = __builtin_amdgcn_exp2f(sc - ref);
+        lsum[i] = lsum[i] * alpha[i] + p[i];
+        m[i] = mx;
+      }
+      *reinterpret_cast<float4*>(&ptile[wave][lrow][4 * lgrp]) = make_float4(p[0], p[1], p[2], p[3]);
+      float al[G];
+      bool moved = false;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        al[h] = readlane_f32(alpha[h & 3], 16 * (h >> 2));
+        moved |= al[h] != 1.f;
+      }
+      if (moved) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[h][e] *= al[h];
+      }
+      lds_order();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * i + lgrp;
+        float ph[GQ * 4];
+#pragma unroll
+        for (int gq = 0; gq < GQ; ++gq) {
+          const float4 v = *reinterpret_cast<const float4*>(&ptile[wave][r][4 * gq]);
+          ph[4 * gq] = v.x, ph[4 * gq + 1] = v.y, ph[4 * gq + 2] = v.z, ph[4 * gq + 3] = v.w;
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t x = d.v[i][w];
+          const float lo = pair_lo<T>(x), hi = pair_hi<T>(x);
+#pragma unroll
+          for (int h = 0; h < G; ++h) {
+            acc[h][2 * w] = __builtin_fmaf(ph[h], lo, acc[h][2 * w]);
+            acc[h][2 * w + 1] = __builtin_fmaf(ph[h], hi, acc[h][2 * w + 1]);
+          }
+        }
+      }
+      lds_order();
+    };
+
+    // Each round issues the loads of DEPTH tiles, then computes them in
+    // order; no loaded register is carried into the next round (a carried
+    // register makes the compiler wait for every load in flight at the loop
+    // edge).
+    // The two waves of a SIMD share its issue slots; the one that wins
+    // arbitration would run far ahead and leave the CU with too few loads
+    // in flight at the end. Each wave publishes the tiles it has started and
+    // sets its issue priority by its lead over the slowest wave of the
+    // workgroup (3 when level, 1 one round ahead, 0 beyond). The tile
+    // assignment stays static, so the result does not depend on timing.
+    for (int j = 0; j < ntw; j += DEPTH) {
+      MTile t[DEPTH];
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) load(j + d, t[d]);
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        if (lane == 0) progress[wave] = started;
+        int slowest = started;
+#pragma unroll
+        for (int w = 0; w < kMWaves; ++w) slowest = min(slowest, progress[w]);
+        if (started > slowest + DEPTH)
+          __builtin_amdgcn_s_setprio(0);
+        else if (started > slowest)
+          __builtin_amdgcn_s_setprio(1);
+        else
+          __builtin_amdgcn_s_setprio(3);
+        compute(j + d, t[d]);
+        ++started;
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+
+  // denominators over the 16 lanes of each head; accumulators over the four
+  // row classes of the wave
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lsum[i] = group_sum(lsum[i], 16);
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      acc[h][e] += __shfl_xor(acc[h][e], 16);
+      acc[h][e] += __shfl_xor(acc[h][e], 32);
+    }
+
+  // merge the waves through LDS: [wave][g][2 + head_dim]
+  extern __shared__ float lds[];
+  __shared__ int last_arrival;
+  constexpr int stride = 2 + kMD;
+  if (lgrp == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float* w = lds + (wave * G + h) * stride + 2 + 8 * lrow;
+      *reinterpret_cast<float4*>(w) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+      *reinterpret_cast<float4*>(w + 4) = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+    }
+  }
+  if (lrow == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * lgrp + i;
+      if (h < G) {
+        lds[(wave * G + h) * stride] = m[i];
+        lds[(wave * G + h) * stride + 1] = lsum[i];
+      }
+    }
+  }
+  __syncthreads();
+  if (a.n_splits == 1) {  // the workgroup saw every row: normalise and store
+    for (int idx = threadIdx.x; idx < G * kMD; idx += kMThreads) {
+      const int g = idx / kMD;
+      const int d = idx - g * kMD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kMWaves; ++w) M = fmaxf(M, lds[(w * G + g) * stride]);
+      float L = 0.f, v = 0.f;
+      if (M != -INFINITY)
+#pragma unroll
+        for (int w = 0; w < kMWaves; ++w) {
+          const float* src = lds + (w * G + g) * stride;
+          const float f = exp2f(src[0] - M);
+          L += src[1] * f;
+          v += src[2 + d] * f;
+        }
+      v = L > 0.f ? v / L : 0.f;
+      store_elem(a.out, T::dtype, (int64_t)b * a.out_bs + (int64_t)(h0 + g) * a.out_hs + d, v);
+    }
+    return;
+  }
+  // this split's partial: a row of kMWs floats per head, [m, l, 0, 0, acc]
+  // (16-byte aligned). The rows of a (request, KV head) form one block
+  // starting at row (b * q_heads + h0) * n_splits, ordered [head][split].
+  float* part = a.ws + (((int64_t)b * a.q_heads + h0) * a.n_splits + split) * kMWs;
+  for (int idx = threadIdx.x; idx < G * kMWs; idx += kMThreads) {
+    const int g = idx / kMWs;
+    const int j = idx - g * kMWs;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kMWaves; ++w) M = fmaxf(M, lds[(w * G + g) * stride]);
+    float o = 0.f;
+    if (j == 0) {
+      o = M;
+    } else if (j == 1 || j >= 4) {
+      const int c = j == 1 ? 1 : j - 2;  // column of the waves' rows
+      if (M != -INFINITY)
+#pragma unroll
+        for (int w = 0; w < kMWaves; ++w) {
+          const float* src = lds + (w * G + g) * stride;
+          o += src[c] * exp2f(src[0] - M);
+        }
+    }
+    st_coherent(part + (int64_t)g * a.n_splits * kMWs + j, o);
+  }
+  // the last workgroup of this (request, KV head) merges the splits; the
+  // partials' agent-coherent stores complete before the arrival
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  int* counter = a.counters + (int64_t)b * a.kv_heads + kh;
+  if (threadIdx.x == 0)
+    last_arrival = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.n_splits - 1;
+  __syncthreads();
+  if (!last_arrival) return;
+  // every partial row of this (request, KV head) into LDS (the waves' rows
+  // are no longer read), four 16-byte coherent loads per thread at a time
+  const int ns = a.n_splits;
+  const u32x4_t* block = reinterpret_cast<const u32x4_t*>(a.ws + ((int64_t)b * a.q_heads + h0) * ns * kMWs);
+  const int nvec = G * ns * (kMWs / 4);
+  for (int v0 = 0; v0 < nvec; v0 += 4 * kMThreads) {
+    u32x4_t o[4];
+    const u32x4_t* p[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) p[k] = block + min(v0 + k * kMThreads + (int)threadIdx.x, nvec - 1);
+    ld4x16_coherent(p[0], p[1], p[2], p[3], o);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = v0 + k * kMThreads + (int)threadIdx.x;
+      if (i < nvec) reinterpret_cast<u32x4_t*>(lds)[i] = o[k];
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < G * kMD; idx += kMThreads) {
+    const int g = idx / kMD;
+    const int d = idx - g * kMD;
+    const float* hp = lds + g * ns * kMWs;
+    float M = -INFINITY;
+    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, hp[sp * kMWs]);
+    float L = 0.f, v = 0.f;
+    if (M != -INFINITY)
+      for (int sp = 0; sp < ns; ++sp) {
+        const float w = exp2f(hp[sp * kMWs] - M);
+        L += hp[sp * kMWs + 1] * w;
+        v += hp[sp * kMWs + 4 + d] * w;
+      }
+    v = L > 0.f ? v / L : 0.f;
+    store_elem(a.out, T::dtype, (int64_t)b * a.out_bs + (int64_t)(h0 + g) * a.out_hs + d, v);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+typedef void (*AttendMKernel)(AttendMArgs);
+
+static AttendMKernel pick_mfma(int kv_dtype, int G) {
+#define NHS_M_CASE(GG) \
+  case GG: return kv_dtype == NHS_BF16 ? attend_mfma_kernel<BF16, GG, kMDepth> : attend_mfma_kernel<F16, GG, kMDepth>;
+  switch (G) {
+    NHS_M_CASE(1) NHS_M_CASE(2) NHS_M_CASE(3) NHS_M_CASE(4) NHS_M_CASE(5) NHS_M_CASE(6) NHS_M_CASE(7) NHS_M_CASE(8)
+  }
+#undef NHS_M_CASE
+  return nullptr;
+}
+
 typedef void (*AttendKernel)(AttendArgs);
 
 template <typename T, int G, int C, bool PK>
@@ -581,6 +1034,14 @@ static AttendKernel pick_kernel(int kv_dtype, bool packed, int G, int C) {
   }
 }
 
+// Shapes served by attend_mfma_kernel: 16-bit KV with a query of the same
+// dtype, head_dim 128, one row list per request, at most 8 query heads per
+// KV head. Every other shape runs attend_kernel.
+static bool mfma_shape(int kv_dtype, int q_dtype, int64_t rows_head_stride, int head_dim, int group) {
+  return (kv_dtype == NHS_BF16 || kv_dtype == NHS_F16) && q_dtype == kv_dtype && rows_head_stride == 0 &&
+         head_dim == kMD && group >= 1 && group <= kMMaxGroup;
+}
+
 static int max_splits_for(int n_rows) {
   int s = n_rows / kMinRowsPerSplit;
   return s < 1 ? 1 : s > kMaxSplits ? kMaxSplits : s;
@@ -605,7 +1066,7 @@ static int device_cus() {
 
 extern "C" int64_t nhs_attend_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_dim, int32_t n_rows) {
   if (batch < 1 || q_heads < 1 || head_dim < 1 || n_rows < 1) return 0;
-  int64_t partials = (int64_t)batch * q_heads * nhs::max_splits_for(n_rows) * (head_dim + 2) * (int64_t)sizeof(float);
+  int64_t partials = (int64_t)batch * q_heads * nhs::max_splits_for(n_rows) * (head_dim + 4) * (int64_t)sizeof(float);
   return nhs::kHeaderBytes + partials;
 }
 
@@ -672,6 +1133,52 @@ extern "C" int nhs_attend_rows(const void* query, int32_t q_dtype, int64_t q_bat
   // the last workgroup to finish).
   const int cus = device_cus();
   const int kv_items = batch * kv_heads;
+  if (mfma_shape(kv_dtype, q_dtype, rows_head_stride, head_dim, a.group)) {
+    // attend_mfma_kernel: one workgroup per (request, KV head, row split),
+    // about one per CU; splits of whole 128-row blocks (every wave gets
+    // whole tiles), at most kMMaxSplits
+    AttendMArgs m;
+    m.q = query;
+    m.q_bs = q_batch_stride;
+    m.q_hs = q_head_stride;
+    m.pool = static_cast<const char*>(pool);
+    m.rows = rows;
+    m.r_bs = rows_batch_stride;
+    m.r_cs = rows_col_stride;
+    m.n_rows = n_rows;
+    m.q_heads = q_heads;
+    m.kv_heads = kv_heads;
+    m.group = a.group;
+    m.page_size = page_size;
+    m.kv_items = kv_items;
+    m.page_div = a.page_div;
+    m.block_stride = pool_block_stride;
+    m.row_bytes = (int64_t)kv_heads * head_dim * esize;
+    m.qscale = a.qscale;
+    const int target = cus > 0 ? cus : 256;
+    int splits = (target + kv_items / 2) / kv_items;
+    if (splits < 1) splits = 1;
+    if (splits > max_splits_for(n_rows)) splits = max_splits_for(n_rows);
+    if (splits > kMMaxSplits) splits = kMMaxSplits;
+    const int block = kMTile * kMWaves;
+    int per = (n_rows + splits - 1) / splits;
+    per = (per + block - 1) / block * block;
+    splits = (n_rows + per - 1) / per;
+    if ((int64_t)kv_items * splits > 0x7fffffff) return fail(NHS_ERR_UNSUPPORTED, "nhs_attend_rows: grid too large");
+    m.n_splits = splits;
+    m.rows_per_split = per;
+    m.counters = static_cast<int*>(workspace);
+    m.zeros = static_cast<const char*>(workspace) + kCounterBytes;
+    m.ws = reinterpret_cast<float*>(static_cast<char*>(workspace) + kHeaderBytes);
+    m.out = out;
+    m.out_bs = out_batch_stride;
+    m.out_hs = out_head_stride;
+    AttendMKernel kernel = pick_mfma(kv_dtype, a.group);
+    const size_t lds = (size_t)std::max(kMWaves * a.group * (2 + kMD), a.group * splits * kMWs) * sizeof(float);
+    launch(kernel, dim3((unsigned)(kv_items * splits)), dim3(kMThreads), lds, (hipStream_t)stream, ev.start, ev.stop,
+           m);
+    return launch_status("nhs_attend_rows");
+  }
   const int share = cus > 0 ? (cus + kv_items / 2) / kv_items : 1;  // workgroups per (request, KV head)
   int G;
   if (rows_head_stride != 0) {

@@ -196,6 +196,42 @@ def test_attend_rows_matches_oracle(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, N, pe
     assert err <= ATOL[dtype if dtype != torch.float32 else q_dtype], err
 
 
+@pytest.mark.parametrize(
+    "dtype,B,Hq,Hkv,P,N,all_masked",
+    [
+        (torch.bfloat16, 1, 8, 8, 64, 33000, False),  # 1 head per KV head; 16 splits of 3 passes each
+        (torch.float16, 2, 16, 8, 16, 1500, True),  # 2 heads; request 0 has no valid row
+        (torch.bfloat16, 3, 24, 8, 32, 600, False),  # 3 heads
+        (torch.float16, 4, 32, 8, 64, 2048, False),  # Llama-3-8B heads in fp16
+        (torch.bfloat16, 2, 20, 4, 16, 900, True),  # 5 heads
+        (torch.bfloat16, 2, 24, 4, 8, 100, False),  # 6 heads, one tile per wave at most
+        (torch.bfloat16, 1, 7, 1, 32, 5, False),  # 7 heads, five rows
+        (torch.bfloat16, 5, 64, 8, 64, 1200, False),  # 8 heads
+    ],
+)
+def test_attend_mfma_shapes_match_oracle(gpu, dtype, B, Hq, Hkv, P, N, all_masked):
+    """head_dim 128 with 16-bit KV and query and one row list per request
+    runs attend_mfma_kernel (QK^T on MFMA): every group size 1-8 it serves,
+    fp16 and bf16, row splits merged across workgroups (up to 16), several
+    LDS passes per split, a few rows only, 20% masked rows and requests with
+    none valid; within the bf16/fp16 tolerance of the float64 oracle, and a
+    second call gives the same bits."""
+    log_case(test="attend-mfma", dtype=dtype, B=B, Hq=Hq, Hkv=Hkv, P=P, N=N)
+    pool, q, rows = _attention_case(gpu, dtype, dtype, B, Hq, Hkv, 128, P, N, False, seed=N + Hq)
+    if all_masked:
+        rows[0] = -1
+    expected = oracle.attend_rows(q, pool, rows, P)
+    g_q, g_pool, g_rows = q.to(gpu), pool.to(gpu), rows.to(gpu)
+    out = rk.attend_batched(g_q, g_pool, g_rows, P)
+    again = rk.attend_batched(g_q, g_pool, g_rows, P)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)
+    err = (out.cpu().float() - expected).abs().max().item()
+    assert err <= ATOL[dtype], err
+    if all_masked:
+        assert not out[0].any()
+
+
 @pytest.mark.parametrize("N", [16, 64, 256, 2048])
 @pytest.mark.parametrize("score_std,v_std", [(4.0, 4.0), (4.0, 8.0), (3.0, 8.0)])
 def test_attend_rows_precision_with_peaky_scores_and_large_values(gpu, N, score_std, v_std):
