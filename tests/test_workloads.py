@@ -26,6 +26,7 @@
   bytes bit-exact; attention within 2e-2.
 """
 
+import gc
 import json
 import os
 
@@ -250,17 +251,9 @@ def test_miss_heavy_long_context(gpu):
     assert (out.float().cpu() - e_out).abs().max().item() <= 2e-2
 
 
-def _llama8b_width_engine(device, layers, prompt, new_tokens, B=8):
+def _llama8b_width_model(device, layers):
     """A random-init decoder of Llama-3-8B width (hidden 4096, 32/8 heads x
-    128, MLP 14336, vocab 128256, bf16, seed 42) with `layers` layers, B
-    requests of `prompt` seeded random tokens, pages of 64, 2048 hot rows,
-    Quest top-32 pages and a pool of the admission credits plus 30% of the
-    history, through the batched engine."""
-    from math import ceil
-
-    from nano_hisparse.config import CacheConfig
-    from nano_hisparse.engine import Engine
-    from nano_hisparse.hybrid import HotConfig, HybridKVCache
+    128, MLP 14336, vocab 128256, bf16, seed 42) with `layers` layers."""
     from nano_hisparse.model import Model, ModelConfig
 
     cfg = ModelConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=layers,
@@ -270,21 +263,38 @@ def _llama8b_width_engine(device, layers, prompt, new_tokens, B=8):
     torch.set_default_dtype(torch.bfloat16)
     try:
         with torch.device(device):
-            model = Model(cfg).eval()
+            return Model(cfg).eval()
     finally:
         torch.set_default_dtype(default_dtype)
+
+
+def _llama8b_width_engine(device, layers, prompt, new_tokens, B=8, model=None, resident=0.3, admit=True):
+    """B requests of `prompt` seeded random tokens through the batched
+    engine on a Llama-3-8B-width decoder (_llama8b_width_model): pages of
+    64, 2048 hot rows, Quest top-32 pages and a pool of the admission
+    credits plus `resident` of the history. With `admit`, steps the engine
+    until every request is admitted (admitted requests decode meanwhile)."""
+    from math import ceil
+
+    from nano_hisparse.config import CacheConfig
+    from nano_hisparse.engine import Engine
+    from nano_hisparse.hybrid import HotConfig, HybridKVCache
+
+    if model is None:
+        model = _llama8b_width_model(device, layers)
     P, H, top = 64, 2048, 32
     pages = ceil((prompt + new_tokens) / P)
     hot = HotConfig(H, H)
-    kv = CacheConfig(gpu_pages=B * hot.admission_blocks(P, layers) + int(0.3 * B * layers * pages),
+    kv = CacheConfig(gpu_pages=B * hot.admission_blocks(P, layers) + int(resident * B * layers * pages),
                      host_pages=B * layers * pages, page_size=P, kv_heads=8, head_dim=128, dtype=torch.bfloat16,
-                     device=str(device))
+                     device=str(device), index_budget_bytes=1 << 31)
     cache = HybridKVCache(kv, hot)
     engine = Engine(model, cache, top_k=top, batch_decode=True)
     g = torch.Generator().manual_seed(42)
     for b in range(B):
-        engine.add_request(f"r{b}", torch.randint(0, cfg.vocab_size, (prompt,), generator=g).tolist(), new_tokens)
-    while engine.waiting:
+        engine.add_request(f"r{b}", torch.randint(0, model.config.vocab_size, (prompt,), generator=g).tolist(),
+                           new_tokens)
+    while admit and engine.waiting:
         engine.step()
     return engine, cache
 
@@ -384,3 +394,137 @@ def test_llama8b_width_batched_decode_matches_the_oracle_per_layer(gpu, monkeypa
     assert len(checked) == 2 * steps and not expected_out
     assert sum(m for _, m in checked) > 0  # rows were gathered from the host store
     cache.assert_invariants()
+
+
+def _compact_rows(pool, physical, P):
+    """The pool rows that `physical` [B, K] (-1 masked) names, copied to the
+    host as a compact pool of their own, and the same rows renumbered into
+    it: attention over them equals attention over the whole pool."""
+    B, K = physical.shape
+    valid = physical >= 0
+    rows = physical[valid]
+    blocks = -(-max(1, rows.numel()) // P)
+    flat = torch.zeros(blocks * P, 2, pool.shape[3], pool.shape[4], dtype=pool.dtype)
+    if rows.numel():
+        flat[: rows.numel()] = pool[rows // P, :, rows % P].cpu()
+    compact = flat.view(blocks, P, 2, pool.shape[3], pool.shape[4]).transpose(1, 2).contiguous()
+    renum = torch.full((B, K), -1, dtype=torch.int64)
+    renum[valid.cpu()] = torch.arange(rows.numel())
+    return compact, renum
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(900)
+def test_llama8b_full_size_decode_matches_the_oracle_per_layer(gpu, monkeypatch):
+    """Config 4 at full size: 32 layers, 8 requests x 16384-token prompts,
+    2048 hot rows, Quest top-32 pages, a pool of the admission credits plus
+    30% of the history. For every layer of two batched decode steps, the
+    selected pages and positions, resolved rows, miss plans, counts, tags
+    and LRU order equal the oracle's on the same inputs; every gathered pool
+    row equals its host row byte for byte; and attention is within 2e-2 of
+    the oracle's over the selected rows (copied to the host on their own:
+    only the rows a layer's plan touches leave the device, not the pool)."""
+    from nano_hisparse import batched
+
+    log_case(test="llama8b-full", layers=32, requests=8, prompt=16384)
+    steps, layers = 2, 32
+    engine, cache = _llama8b_width_engine(gpu, layers=layers, prompt=16384, new_tokens=8 + steps + 2)
+    store = cache.storage
+    P = cache.config.page_size
+    expected_out = {}
+    checked = []
+    orig_select, orig_finish = batched.BatchDecode.select, batched.BatchDecode.finish
+    rk_fused = rk.select_resolve_items
+
+    def select(self, layer, query, top_pages, keep_sink=True):
+        torch.cuda.synchronize()
+        reqs = [store.requests[r] for r in self.ids]
+        lengths = torch.tensor([r.lengths[layer] for r in reqs])
+        mn = torch.stack([r.minimum[layer][: self.max_pages] for r in reqs]).cpu()
+        mx = torch.stack([r.maximum[layer][: self.max_pages] for r in reqs]).cpu()
+        tables = [cache.tables[r, layer] for r in self.ids]
+        src = [t.source.cpu().numpy() for t in tables]
+        res = [t.resident.cpu().numpy() for t in tables]
+        hot = [t.hot.cpu().numpy() for t in tables]
+        tags = [t.tags.cpu().numpy().astype(np.int64) for t in tables]
+        lru = [t.lru.cpu().numpy().copy() for t in tables]
+        q = query.cpu()
+        seen = {}
+
+        def select_resolve_items(*a, **k):
+            seen["fused"] = rk_fused(*a, **k)
+            return seen["fused"]
+
+        monkeypatch.setattr(rk, "select_resolve_items", select_resolve_items)
+        try:
+            handle = orig_select(self, layer, query, top_pages, keep_sink)
+        finally:
+            monkeypatch.setattr(rk, "select_resolve_items", rk_fused)
+        torch.cuda.synchronize()  # the gather has landed
+        _, e_pages, e_pos = oracle.quest_select(q, mn, mx, lengths, P, top_pages, keep_sink)
+        assert "fused" in seen, layer
+        pages, positions = seen["fused"][:2]
+        assert torch.equal(pages.cpu(), e_pages) and torch.equal(positions.cpu(), e_pos), layer
+        physical_dev = seen["fused"][2]
+        physical, mh, md, counts = (t.cpu().numpy() for t in seen["fused"][2:])
+        for b, t in enumerate(tables):
+            want = oracle.resolve_rows(e_pos[b].numpy(), src[b], res[b], hot[b], tags[b], lru[b],
+                                       int(lengths[b]), P)
+            for got, exp in zip((physical[b], mh[b], md[b], counts[b]), want):
+                np.testing.assert_array_equal(got, exp)
+            np.testing.assert_array_equal(t.tags.cpu().numpy(), tags[b])
+            np.testing.assert_array_equal(t.lru.cpu().numpy(), lru[b])
+        # gathered rows: pool row md holds host row mh, both planes, byte for byte
+        miss = mh.reshape(-1) >= 0
+        h_rows, d_rows = torch.from_numpy(mh.reshape(-1)[miss]), torch.from_numpy(md.reshape(-1)[miss])
+        got = cache.pool[d_rows.to(gpu) // P, :, d_rows.to(gpu) % P].cpu()
+        want = store.host[h_rows // P, :, h_rows % P]
+        assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), layer
+        compact, renum = _compact_rows(cache.pool, physical_dev, P)
+        expected_out[id(self), layer] = oracle.attend_rows(q, compact, renum, P)
+        checked.append((layer, int(miss.sum())))
+        return handle
+
+    def finish(self, handle):
+        out = orig_finish(self, handle)
+        torch.cuda.synchronize()
+        want = expected_out.pop((id(self), handle[0]))
+        assert (out.cpu().float() - want).abs().max().item() <= 2e-2, handle[0]
+        return out
+
+    monkeypatch.setattr(batched.BatchDecode, "select", select)
+    monkeypatch.setattr(batched.BatchDecode, "finish", finish)
+    for step in range(steps):
+        assert len(engine.step()) == 8
+        print(f"step {step}: {layers} layers checked", flush=True)
+    assert len(checked) == layers * steps and not expected_out
+    assert sum(m for _, m in checked) > 0  # rows were gathered from the host store
+    cache.assert_invariants()
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(900)
+def test_llama8b_full_size_tokens_do_not_depend_on_the_pool_size(gpu):
+    """Config 4 at full size (32 layers, 8 x 16384-token prompts, 2048 hot
+    rows, Quest top-32) generates the same greedy tokens with a pool of the
+    admission credits plus 30% of the history (most selected rows gathered
+    from the host) as with a pool that keeps the whole history resident: the
+    reference's partial-residency property (tests/test_engine.py:27-64) at
+    config 4's size, over 24 tokens per request."""
+    log_case(test="llama8b-pool-sizes", layers=32, requests=8, prompt=16384)
+    model = _llama8b_width_model(gpu, 32)
+    outputs, misses = [], []
+    for resident in (0.3, 1.0):
+        engine, cache = _llama8b_width_engine(gpu, layers=32, prompt=16384, new_tokens=24, model=model,
+                                              resident=resident, admit=False)
+        outputs.append(engine.run())
+        misses.append(cache.snapshot()["row_stats"]["misses"])
+        cache.assert_invariants()
+        print(f"pool {resident}: misses {misses[-1]}", flush=True)
+        del engine, cache
+        gc.collect()  # the cache's pinned host store is released before the next one is allocated
+        torch.cuda.empty_cache()
+        torch._C._host_emptyCache()
+    assert misses[0] > 0
+    assert outputs[0] == outputs[1]
+    assert all(len(t) == 24 for t in outputs[0].values())
