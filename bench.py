@@ -838,7 +838,7 @@ def main():
                          gather_bytes / PCIE_PEAK)
     # the committed PMC summaries cover the default workload only
     default = (not miss_heavy and (args.batch, args.context, args.seed, n_chunks, L) == (16, 32768, 42, 1, 4))
-    traffic = traffic_from_profile("attend_kernel") if default else None
+    traffic = traffic_from_profile("attend_mfma_kernel") if default else None
     host_traffic = (
         traffic_from_profile("gather_rows_kernel", "sparse_decode_b16_ctx32k_pmc_host_link.txt", "host_read_bytes")
         if default else None
@@ -889,7 +889,7 @@ def main():
         "sparse_attn_gather_step_us": round(sum(kernel_us[n] for n in ("resolve", "gather", "attention")), 2),
         "stamped_step_us": round(stamped_ms * 1e3, 2),
         "roofline": {
-            "kernel": "nhs_attend_rows (attend_kernel)",
+            "kernel": "nhs_attend_rows (attend_mfma_kernel)",
             "bound": "hbm",
             "achieved": round(attn_launch_bytes / (attn_us * 1e-6) / 1e9, 1),
             "peak": HBM_PEAK / 1e9,
