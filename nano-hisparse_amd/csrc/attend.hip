@@ -616,7 +616,7 @@ struct AttendMArgs {
   int64_t row_bytes;     // one plane row, all KV heads, bytes
   float qscale;
   const char* zeros;  // kZeroBytes of zeros
-  float* ws;          // partials [B, q_heads, n_splits, 2 + head_dim]
+  float* ws;          // partials [B, q_heads, n_splits, head_dim + 4]
   int* counters;      // [B, kv_heads]
   void* out;
   int64_t out_bs, out_hs;
