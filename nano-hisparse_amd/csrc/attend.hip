@@ -596,6 +596,7 @@ constexpr int kMMaxGroup = 8;
 constexpr int kMDepth = 2;  // tiles whose loads a wave issues together
 constexpr int kMWs = kMD + 4;     // floats per partial row in the workspace: m, l, 2 unused, acc
 constexpr int kMMaxSplits = 16;
+static_assert(kMStage / (kMTile * kMWaves) <= 8, "a wave stages at most two groups of four tiles per pass");
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -730,20 +731,31 @@ __global__ __launch_bounds__(kMThreads) void attend_mfma_kernel(AttendMArgs a) {
   const int row_begin = split * a.rows_per_split;
   const int row_end = min(a.n_rows, row_begin + a.rows_per_split);
 
-  if (threadIdx.x < kMWaves) progress[threadIdx.x] = 0;
-  __syncthreads();
+  // Each wave clears its own slot; another wave's slot may hold an older
+  // value until that wave starts its first tile, which only shifts issue
+  // priorities for a moment, so no barrier holds back the first loads.
+  if (lane == 0) progress[wave] = 0;
   int started = 0;  // tiles this wave has started, over all passes
   for (int s0 = row_begin; s0 < row_end; s0 += kMStage) {
     const int len = min(kMStage, row_end - s0);
     const int padded = (len + kRound - 1) / kRound * kRound;
-    const int ntw = padded / (kMTile * kMWaves);  // tiles of each wave, a multiple of DEPTH
+    const int ntw = padded / (kMTile * kMWaves);  // tiles of each wave, a multiple of DEPTH, at most 8
     // Each wave stages the rows of its own tiles t = wave + kMWaves * j
     // (lane: tile j0 + l / 16, row l % 16), so no workgroup barrier waits
-    // for the slowest wave's index loads; only this wave reads them.
-    for (int j0 = 0; j0 < ntw; j0 += 4) {
-      const int j = j0 + lgrp;
+    // for the slowest wave's index loads; only this wave reads them. Both
+    // index loads of a lane are issued before either is used.
+    int64_t r2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 4 * h + lgrp;
       const int i = (wave + kMWaves * j) * kMTile + lrow;
-      const int64_t r = j < ntw && i < len ? rows[(int64_t)(s0 + i) * a.r_cs] : -1;
+      r2[h] = j < ntw && i < len ? rows[(int64_t)(s0 + i) * a.r_cs] : -1;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 4 * h + lgrp;
+      const int i = (wave + kMWaves * j) * kMTile + lrow;
+      const int64_t r = r2[h];
       if (j < ntw) {
         int64_t ko = zoff, vo = zoff;
         if (r >= 0) {
