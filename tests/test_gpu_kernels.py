@@ -207,6 +207,10 @@ def test_attend_rows_matches_oracle(gpu, dtype, q_dtype, B, Hq, Hkv, D, P, N, pe
         (torch.bfloat16, 2, 24, 4, 8, 100, False),  # 6 heads, one tile per wave at most
         (torch.bfloat16, 1, 7, 1, 32, 5, False),  # 7 heads, five rows
         (torch.bfloat16, 5, 64, 8, 64, 1200, False),  # 8 heads
+        # (request, KV head) counts that are not a multiple of 8: the splits of
+        # one item land on different XCDs, so the merge crosses their L2s
+        (torch.bfloat16, 3, 12, 3, 64, 1500, False),  # 9 items x 12 splits
+        (torch.float16, 5, 35, 5, 32, 2000, True),  # 7 heads, 25 items x 8 splits
     ],
 )
 def test_attend_mfma_shapes_match_oracle(gpu, dtype, B, Hq, Hkv, P, N, all_masked):

@@ -13,6 +13,10 @@
   tests/golden/make_reference_tokens.py from the reference on the CPU): all
   192 tokens and the resident / hot / miss row counters.
 
+- Default benchmark step: 16 requests of 32K tokens, Llama-3-8B heads,
+  top-32 pages, the selected pages 16 resident / 8 hot / 8 in host memory:
+  one step bit-exact (positions, rows, tags, LRU, pool bytes), attention
+  within 2e-2.
 - Resolver stress: 64 requests with Qwen2-7B heads (28 query / 4 KV heads x
   128, bf16), contexts uniform in [4096, 65536], pages of 32, a 1024-row
   budget (32 pages), 2048 hot rows per request all occupied, 16 decode steps
@@ -169,6 +173,46 @@ def test_resolver_stress_64_requests_16_steps(gpu):
         np.testing.assert_array_equal(g_tags.cpu().numpy(), o_tags, err_msg=f"step {step}: tags")
         np.testing.assert_array_equal(g_lru.cpu().numpy(), o_lru, err_msg=f"step {step}: lru")
     assert replaced > 0  # every step evicts from a full hot buffer
+
+
+@pytest.mark.gpu
+def test_default_step_full_size_matches_the_oracle(gpu):
+    """The benchmark's default step at full size (16 requests, 32K context,
+    Llama-3-8B heads, bf16, top-32 pages = 2048 rows, of the selected pages
+    16 resident / 8 hot / 8 in host memory, 4096 hot rows), built by
+    bench.py's workload classes, one step of SparseDecodeBatch against the C
+    oracle request by request: positions, physical rows, tags, LRU order and
+    the whole pool after the gather bit-exact; attention within 2e-2 of the
+    float64 oracle."""
+    log_case(test="default-step", B=16, context=32768)
+    import bench
+
+    store = bench.HostStore(16, 32768, 1234, gpu)
+    w = bench.Layer(store, 1234)
+    B, P, top = w.batch, w.page, w.top_pages
+    cpool = w.pool.cpu()
+    q, mn, mx, lengths = w.q.cpu(), w.minimum.cpu(), w.maximum.cpu(), w.lengths.cpu()
+    result = bench.run_step(w)
+    torch.cuda.synchronize()
+    _, _, e_pos = oracle.quest_select(q, mn, mx, lengths, P, top)
+    assert torch.equal(result.positions.cpu(), e_pos)
+    source, resident, hot = w.source.cpu().numpy(), w.resident.cpu().numpy(), w.hot.cpu().numpy()
+    tags, lru = w.tags0.cpu().numpy().astype(np.int64), w.lru0.cpu().numpy().copy()
+    e_phys = np.empty((B, w.K), np.int64)
+    counts = np.zeros(3, np.int64)
+    for b in range(B):
+        ph, mh, md, cnt = oracle.resolve_rows(e_pos[b].numpy(), source[b], resident[b], hot[b], tags[b], lru[b],
+                                               int(lengths[b]), P)
+        oracle.gather_rows(w.host, cpool, mh, md, P)
+        e_phys[b] = ph
+        counts += cnt
+    assert counts.tolist() == [16 * 16 * P, 16 * 8 * P, 16 * 8 * P]  # resident / hot / missed rows, as built
+    np.testing.assert_array_equal(result.physical.cpu().numpy(), e_phys)
+    np.testing.assert_array_equal(w.tables.tags.cpu().numpy(), tags)
+    np.testing.assert_array_equal(w.tables.lru.cpu().numpy(), lru)
+    assert torch.equal(w.pool.cpu().view(torch.uint8), cpool.view(torch.uint8))
+    e_out = oracle.attend_rows(q, cpool, torch.from_numpy(e_phys), P)
+    assert (w.out.float().cpu() - e_out).abs().max().item() <= 2e-2
 
 
 @pytest.mark.gpu
