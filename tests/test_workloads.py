@@ -42,6 +42,14 @@ import oracle
 from nano_hisparse import row_kernels as rk
 
 
+def _release_memory():
+    """Frees what earlier tests left cached: device blocks and the pinned host
+    blocks of their host stores (the full-size tests pin up to 16 GiB each)."""
+    gc.collect()
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
+
+
 def log_case(**kw):
     print("case:", kw, flush=True)
 
@@ -213,6 +221,8 @@ def test_default_step_full_size_matches_the_oracle(gpu):
     assert torch.equal(w.pool.cpu().view(torch.uint8), cpool.view(torch.uint8))
     e_out = oracle.attend_rows(q, cpool, torch.from_numpy(e_phys), P)
     assert (w.out.float().cpu() - e_out).abs().max().item() <= 2e-2
+    del w, store, result, cpool
+    _release_memory()
 
 
 @pytest.mark.gpu
@@ -471,6 +481,7 @@ def test_llama8b_full_size_decode_matches_the_oracle_per_layer(gpu, monkeypatch)
     from nano_hisparse import batched
 
     log_case(test="llama8b-full", layers=32, requests=8, prompt=16384)
+    _release_memory()
     steps, layers = 2, 32
     engine, cache = _llama8b_width_engine(gpu, layers=layers, prompt=16384, new_tokens=8 + steps + 2)
     store = cache.storage
@@ -556,6 +567,7 @@ def test_llama8b_full_size_tokens_do_not_depend_on_the_pool_size(gpu):
     reference's partial-residency property (tests/test_engine.py:27-64) at
     config 4's size, over 24 tokens per request."""
     log_case(test="llama8b-pool-sizes", layers=32, requests=8, prompt=16384)
+    _release_memory()
     model = _llama8b_width_model(gpu, 32)
     outputs, misses = [], []
     for resident in (0.3, 1.0):
@@ -566,9 +578,7 @@ def test_llama8b_full_size_tokens_do_not_depend_on_the_pool_size(gpu):
         cache.assert_invariants()
         print(f"pool {resident}: misses {misses[-1]}", flush=True)
         del engine, cache
-        gc.collect()  # the cache's pinned host store is released before the next one is allocated
-        torch.cuda.empty_cache()
-        torch._C._host_emptyCache()
+        _release_memory()  # the cache's pinned host store is released before the next one is allocated
     assert misses[0] > 0
     assert outputs[0] == outputs[1]
     assert all(len(t) == 24 for t in outputs[0].values())
