@@ -182,7 +182,8 @@ int nhs_attend_rows_noalloc(const void* query, int32_t q_dtype, int64_t q_batch_
  * logical order, then -1) and counts[b, 0:3] = unique resident hits, hot
  * hits, misses; counts_total[0:3] (may be NULL) is incremented by them.
  * lengths[b] (int64, may be NULL to use `length` for every item) is the
- * causal length. n <= NHS_MAX_POSITIONS, hot_rows <= NHS_MAX_HOT_ROWS;
+ * causal length. n <= hot_rows (the reference's max_union_rows <=
+ * hot_rows), n <= NHS_MAX_POSITIONS, hot_rows <= NHS_MAX_HOT_ROWS;
  * with batch > 1, plan_stride >= n. Above 4096 positions the item's
  * physical / miss_host / miss_device rows also serve as scratch during the
  * call (sorted keys, per-entry state) before they receive the results.

@@ -862,6 +862,9 @@ static int check_resolve(const char* who, int32_t batch, int32_t n, const void* 
     return fail(NHS_ERR_INVALID, "%s: need n, n_pages, hot_rows, page_size >= 1", who);
   if (n > kLargeMaxK || hot_rows > kMaxH)
     return fail(NHS_ERR_UNSUPPORTED, "%s: n <= %d and hot_rows <= %d required", who, kLargeMaxK, kMaxH);
+  // a selection names at most max_union_rows <= hot_rows rows (HotConfig,
+  // hybrid.py:36-37), so its misses always fit the hot buffer
+  if (n > hot_rows) return fail(NHS_ERR_INVALID, "%s: n (%d) must be <= hot_rows (%d)", who, n, hot_rows);
   if (!lengths && (length < 0 || length >= (1ll << 31)))
     return fail(NHS_ERR_INVALID, "%s: length must be in [0, 2^31)", who);
   if (batch > 1 && plan_stride < n)

@@ -112,6 +112,53 @@ def test_item_entry_points_match_the_strided_ones(gpu, dtype):
             assert torch.equal(t["tags"], tags) and torch.equal(t["lru"], lru)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("K", [96, 4608])  # resolve_rows_kernel, and resolve_large_kernel beyond 4096 positions
+def test_resolve_items_with_an_item_of_no_pages(gpu, K):
+    """An item with no pages (n_pages 0, length 0) beside normal items in one
+    nhs_resolve_items launch: its table pointers are never read, every entry
+    of its plan is unset (-1), its counts are zero and its tags and LRU order
+    are unchanged; the other items resolve as the strided kernel does."""
+    log_case(test="resolve-empty-item", K=K)
+    g = torch.Generator(device=gpu).manual_seed(11)
+    P, H = 16, max(512, 2 * K)  # hot rows cover the selection (max_union_rows <= hot_rows)
+    n_pages = [K // P + 4, 0, K // P + 9]
+    blocks = 4 * max(n_pages) + 64
+    tabs = []
+    for b, n in enumerate(n_pages):
+        m = max(n, 1)  # a one-element table for the empty item: a valid pointer it must not read
+        source = torch.arange(m, dtype=torch.int32, device=gpu) + 1000 * b
+        resident = torch.randperm(blocks, generator=g, device=gpu)[:m].to(torch.int32)
+        resident[::2] = -1
+        hot = torch.randperm(blocks, generator=g, device=gpu)[: H // P].to(torch.int32)
+        tags = torch.full((H,), -1, dtype=torch.int32, device=gpu)
+        lru = torch.randperm(H, generator=g, device=gpu)
+        tabs.append(dict(source=source, resident=resident, hot=hot, tags=tags, lru=lru, minimum=source,
+                         maximum=source, summaries=source, n_pages=n))
+    items = rk.layer_items([tabs], gpu)[0]
+    lengths = torch.tensor([n * P for n in n_pages], dtype=torch.int64, device=gpu)
+    positions = torch.stack([torch.randperm(max(n, 1) * P, generator=g, device=gpu)[:K] if n else
+                             torch.randint(0, 1 << 20, (K,), generator=g, device=gpu) for n in n_pages]).to(torch.int32)
+    positions = positions.sort(1).values.contiguous()
+    before = [(t["tags"].clone(), t["lru"].clone()) for t in tabs]
+    with pytest.raises(RuntimeError, match="hot_rows"):  # more positions than hot rows: rejected, nothing runs
+        rk.resolve_items(positions, items, K - 1, lengths, P)
+    phys, mh, md, cnt = rk.resolve_items(positions, items, H, lengths, P)
+    torch.cuda.synchronize()
+    assert (phys[1] == -1).all() and (mh[1] == -1).all() and (md[1] == -1).all()
+    assert not cnt[1].any()
+    assert torch.equal(tabs[1]["tags"], before[1][0]) and torch.equal(tabs[1]["lru"], before[1][1])
+    for b in (0, 2):
+        t = tabs[b]
+        tags, lru = before[b]
+        e = rk.resolve_batched(positions[b: b + 1], t["source"][None], t["resident"][None], t["hot"][None],
+                               tags[None], lru[None], int(lengths[b]), P)
+        for got, want in zip((phys[b], mh[b], md[b], cnt[b]), (x[0] for x in e)):
+            assert torch.equal(got, want)
+        assert torch.equal(t["tags"], tags) and torch.equal(t["lru"], lru)
+        assert int(cnt[b, 2]) > 0
+
+
 def _prefill(caches, names, lengths, layers, g, device, dtype):
     cfg = caches[0].config
     for name, n in zip(names, lengths):

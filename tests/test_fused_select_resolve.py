@@ -35,9 +35,9 @@ CASES = [
     # mode, B, Hq, Hkv, D, P, n_pages, top, H, keep_sink, nan_pages, steps
     ("quest", 16, 32, 8, 128, 64, 512, 32, 2048, True, 0, 3),  # Llama-3-8B heads at 32K context
     ("quest", 4, 32, 8, 128, 64, 1024, 64, 4096, True, 0, 2),  # 16 pages per lane, 4096 positions
-    ("quest", 3, 8, 2, 64, 16, 700, 100, 1500, False, 5, 3),  # NaN pages, no sink
+    ("quest", 3, 8, 2, 64, 16, 700, 100, 1600, False, 5, 3),  # NaN pages, no sink
     ("quest", 2, 8, 2, 64, 16, 200, 8, 300, True, 20, 2),  # more NaN pages than the budget: last page may lose
-    ("quest", 2, 4, 2, 64, 16, 40, 100, 300, True, 0, 2),  # budget above the page count: -1 padding
+    ("quest", 2, 4, 2, 64, 16, 40, 100, 1600, True, 0, 2),  # budget above the page count: -1 padding
     ("quest", 3, 4, 2, 32, 7, 300, 1, 64, True, 2, 3),  # one page, odd page size
     ("mean", 4, 8, 2, 64, 32, 400, 20, 700, True, 3, 3),  # page-mean selector
     ("mean", 2, 4, 1, 32, 16, 900, 1, 128, True, 0, 2),
@@ -122,10 +122,10 @@ def test_fused_select_resolve_equals_select_then_resolve(gpu, mode, B, Hq, Hkv, 
 @pytest.mark.gpu
 def test_fused_select_resolve_rejects_shapes_beyond_its_selection(gpu):
     log_case(test="select-resolve-limits")
-    B, H, P = 1, 64, 8
+    B, H, P = 1, 8192, 8
     scores = torch.zeros(B, 4097, dtype=torch.float32, device=gpu)
     tabs = [torch.zeros(B, 4097, dtype=torch.int32, device=gpu) for _ in range(2)]
-    hot = torch.zeros(B, 8, dtype=torch.int32, device=gpu)
+    hot = torch.zeros(B, H // P, dtype=torch.int32, device=gpu)
     tags = torch.full((B, H), -1, dtype=torch.int32, device=gpu)
     lru = torch.arange(H, device=gpu)[None].clone()
     with pytest.raises(RuntimeError, match="4096"):  # too many pages
@@ -143,6 +143,11 @@ def test_fused_select_resolve_rejects_shapes_beyond_its_selection(gpu):
                                   1024 * 64, 64, 520)
     with pytest.raises(RuntimeError, match=r"status -1: .*top_pages"):
         rk.select_resolve_batched(scores[:, :512], tabs[0][:, :512], tabs[1][:, :512], hot, tags, lru, 512 * P, P, 0)
+    # a budget of more rows than the hot buffer holds: the reference's
+    # max_union_rows <= hot_rows (HotConfig) is violated, NHS_ERR_INVALID
+    with pytest.raises(RuntimeError, match=r"status -1: .*hot_rows"):
+        rk.select_resolve_batched(scores[:, :512], tabs[0][:, :512], tabs[1][:, :512], hot[:, :4], tags[:, :32],
+                                  lru[:, :32].clone(), 512 * P, P, 5)
 
 
 @pytest.mark.gpu
