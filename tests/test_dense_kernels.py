@@ -4,8 +4,12 @@ batched model step against per-request decoding.
 
 RoPE and the residual adds reproduce torch's roundings exactly (bit-exact);
 RMSNorm's mean and SiLU's exp may differ from torch's by their last fp32
-bits, which shows as at most one unit in the last place after rounding to
-bf16/fp16 (fp32: a relative 1e-6).
+bits. For SiLU that shows as at most one unit in the last place after
+rounding to bf16/fp16; RMSNorm rounds twice after the mean
+(round(round(h * r) * weight)), so a flip of the inner rounding by one unit
+can become two units of the output (seen at fp16, 4 x 8192: 0.46 * r rounds
+one unit apart, times a weight of 1.06 two units apart). fp32: a relative
+1e-6.
 """
 
 import pytest
@@ -20,10 +24,12 @@ from nano_hisparse.model import Model, ModelConfig, RMSNorm
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
 
 
-def ulp_close(a, b):
-    """|a - b| within one unit in the last place of b's dtype."""
+def ulp_close(a, b, units=1):
+    """|a - b| within `units` units in the last place of b's dtype (fp32: a
+    relative 1e-6 per unit, the spread of the mean's reduction order over
+    rows of thousands)."""
     a, b = a.float(), b.float()
-    eps = {torch.float32: 2.0**-22, torch.float16: 2.0**-10, torch.bfloat16: 2.0**-7}[ULP_DTYPE[0]]
+    eps = units * {torch.float32: 1e-6, torch.float16: 2.0**-10, torch.bfloat16: 2.0**-7}[ULP_DTYPE[0]]
     tiny = {torch.float32: 1e-30, torch.float16: 6e-8, torch.bfloat16: 1e-30}[ULP_DTYPE[0]]
     return bool(((a - b).abs() <= eps * b.abs() + tiny).all())
 
@@ -36,7 +42,7 @@ ULP_DTYPE = [torch.float32]
 def test_add_rmsnorm_matches_torch(gpu, dtype):
     ULP_DTYPE[0] = dtype
     g = torch.Generator(device=gpu).manual_seed(1)
-    for rows, width in ((8, 4096), (3, 96), (1, 1000)):
+    for rows, width in ((8, 4096), (16, 3584), (2, 512), (4, 8192), (3, 96), (1, 1000), (2, 8704)):
         x = torch.randn(rows, width, generator=g, device=gpu).to(dtype)
         delta = torch.randn(rows, width, generator=g, device=gpu).to(dtype)
         norm = RMSNorm(width, 1e-6).to(gpu)
@@ -46,9 +52,9 @@ def test_add_rmsnorm_matches_torch(gpu, dtype):
         got_x = x.clone()
         got = rk.add_rmsnorm(got_x, delta, norm.weight, 1e-6)
         assert torch.equal(got_x, want_h)  # the residual add is exact
-        assert ulp_close(got, want), (rows, width)
+        assert ulp_close(got, want, units=2), (rows, width)
         plain = rk.add_rmsnorm(x.clone(), None, norm.weight, 1e-6)
-        assert ulp_close(plain, norm(x))
+        assert ulp_close(plain, norm(x), units=2), (rows, width)
 
 
 @pytest.mark.gpu
