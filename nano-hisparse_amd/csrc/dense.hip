@@ -8,8 +8,8 @@
 
 namespace nhs {
 
-constexpr int kNormThreads = 256;
-constexpr int kNormHeld = 32;  // elements per thread held in registers (rows up to 8192)
+constexpr int kNormThreads = 512;
+constexpr int kNormHeld = 32;  // elements per thread held in registers (rows up to 16384)
 
 template <typename T>
 __device__ __forceinline__ float rnd(float v) {
@@ -109,9 +109,10 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(typename T::B
   }
 }
 
-// add_rmsnorm for 16-bit rows of V * kNormThreads * 8 elements: thread t
-// owns the 8-element chunks t, t + kNormThreads, ... and moves them with
-// 16-byte loads and stores. Same arithmetic as add_rmsnorm_kernel.
+// add_rmsnorm for 16-bit rows of a multiple of 8 elements, at most
+// V * kNormThreads * 8: thread t owns the 8-element chunks t,
+// t + kNormThreads, ... below width / 8 and moves them with 16-byte loads
+// and stores. Same arithmetic as add_rmsnorm_kernel.
 template <typename T, int V>
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_vec_kernel(uint16_t* x, const uint16_t* delta,
                                                                        const uint16_t* weight, uint16_t* out,
@@ -122,12 +123,16 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_vec_kernel(uint16_t*
   uint4* xr = reinterpret_cast<uint4*>(x + (int64_t)row * width);
   const uint4* dr = delta ? reinterpret_cast<const uint4*>(delta + (int64_t)row * width) : nullptr;
   const uint4* wr = reinterpret_cast<const uint4*>(weight);
+  const int chunks = width >> 3;
   uint4 xv[V], dv[V], wv[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) {
-    xv[j] = xr[threadIdx.x + j * kNormThreads];
-    wv[j] = wr[threadIdx.x + j * kNormThreads];
-    if (dr) dv[j] = dr[threadIdx.x + j * kNormThreads];
+    // a chunk past the row reads as zeros and adds nothing to the sum
+    const int c = threadIdx.x + j * kNormThreads;
+    const bool ok = c < chunks;
+    xv[j] = ok ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    wv[j] = ok ? wr[c] : make_uint4(0u, 0u, 0u, 0u);
+    dv[j] = dr && ok ? dr[c] : make_uint4(0u, 0u, 0u, 0u);
   }
   float h[V][8];
   float acc = 0.f;
@@ -145,7 +150,8 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_vec_kernel(uint16_t*
       const uint32_t bits = T::from_float(v);
       o[e >> 1] = (e & 1) ? (o[e >> 1] | (bits << 16)) : bits;
     }
-    if (dr && write_back) xr[threadIdx.x + j * kNormThreads] = make_uint4(o[0], o[1], o[2], o[3]);
+    if (dr && write_back && threadIdx.x + j * kNormThreads < chunks)
+      xr[threadIdx.x + j * kNormThreads] = make_uint4(o[0], o[1], o[2], o[3]);
   }
   acc = group_sum(acc, kWave);
   if ((threadIdx.x & (kWave - 1)) == 0) partial[threadIdx.x / kWave] = acc;
@@ -165,7 +171,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_vec_kernel(uint16_t*
       const uint32_t bits = T::from_float(rnd<T>(h[j][e] * r) * w);
       o[e >> 1] = (e & 1) ? (o[e >> 1] | (bits << 16)) : bits;
     }
-    orow[threadIdx.x + j * kNormThreads] = make_uint4(o[0], o[1], o[2], o[3]);
+    if (threadIdx.x + j * kNormThreads < chunks) orow[threadIdx.x + j * kNormThreads] = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -219,10 +225,10 @@ extern "C" int nhs_add_rmsnorm(int32_t rows, int32_t width, int32_t dtype, void*
   const int wb = delta && write_back ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)rows), block(kNormThreads);
-  const int chunk = kNormThreads * 8;
+  const int per_pass = kNormThreads * 8;  // elements of one chunk per thread
   const bool aligned = (((uintptr_t)x | (uintptr_t)delta | (uintptr_t)weight | (uintptr_t)out) % 16) == 0;
-  if (dtype != NHS_F32 && aligned && width % chunk == 0 && width / chunk <= 4) {
-    const int v = width / chunk;
+  if (dtype != NHS_F32 && aligned && width % 8 == 0 && (width + per_pass - 1) / per_pass <= 4) {
+    const int v = (width + per_pass - 1) / per_pass;
     auto* xp = static_cast<uint16_t*>(x);
     auto* dp = static_cast<const uint16_t*>(delta);
     auto* wp = static_cast<const uint16_t*>(weight);

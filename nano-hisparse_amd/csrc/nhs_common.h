@@ -82,10 +82,11 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
 }
 
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;  // round to nearest even
+  const uint32_t quiet_nan = (u >> 16) | 0x40u;
+  // a select, not a branch, so that unrolled conversions stay straight-line
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? quiet_nan : rounded);
 }
 
 __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
