@@ -14,6 +14,7 @@ from __future__ import annotations
 import ctypes
 
 import torch
+from torch._C import _cuda_getCurrentRawStream as _raw_stream
 
 from . import _hip
 
@@ -57,7 +58,14 @@ def _ptr(t: torch.Tensor | None):
 
 
 def _stream(device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The calling thread's current stream on `device` as a raw handle (what
+    torch.cuda.current_stream(device).cuda_stream returns, without building
+    a Stream object: every launch from Python asks for it)."""
+    return ctypes.c_void_p(_raw_stream(_device_index(device)))
+
+
+def _device_index(device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
 
 
 def _require_gpu(what, *tensors):
@@ -228,8 +236,8 @@ def attend_workspace(device, nbytes):
     so one buffer serves every call on a stream (calls on one stream never
     overlap). A larger request replaces the buffer.
     """
-    stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
+    index = _device_index(device)
+    key = (index, _raw_stream(index))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
