@@ -223,6 +223,58 @@ def append_page(k, v, pool, block, within, host, host_page, summary, minimum, ma
     _hip.check(status, "nhs_append_page")
 
 
+class PageAppender:
+    """append_page for the pages of one multi-page write (a prompt's K/V):
+    the operands that stay fixed over the write (K/V rows, pool, host alias,
+    the request's bounds [layers, pages, kv_heads, head_dim], the stream) are
+    checked and turned into launch arguments once, so that each page costs
+    one library call."""
+
+    def __init__(self, k, v, pool, host, summaries, minimum, maximum):
+        device = _require_gpu("append_page", k, v, pool, summaries, minimum, maximum)
+        if k.shape != v.shape or k.ndim != 3 or tuple(k.shape[1:]) != tuple(pool.shape[3:]):
+            raise ValueError("append_page: K/V must be [tokens, kv_heads, head_dim] of the pool")
+        if k.dtype != pool.dtype or v.dtype != pool.dtype or minimum.dtype != pool.dtype or maximum.dtype != pool.dtype:
+            raise ValueError("append_page: K/V and bounds must have the pool dtype")
+        if summaries.dtype != torch.float32:
+            raise ValueError("append_page: the summary is float32")
+        row_elems = k.shape[1] * k.shape[2]
+        for t in (summaries, minimum, maximum):
+            if not t.is_contiguous() or t.shape[-2:] != k.shape[1:]:
+                raise ValueError("append_page: summaries and bounds are contiguous [..., kv_heads, head_dim]")
+        if k.stride(2) != 1 or k.stride(1) != k.shape[2] or k.stride(0) != v.stride(0) or v.stride(2) != 1 \
+                or v.stride(1) != v.shape[2]:
+            raise ValueError("append_page: K/V rows must be contiguous with equal token strides")
+        if host is not None and host.dtype != pool.dtype:
+            raise ValueError("append_page: host and pool dtypes differ")
+        self.lib = _hip.load()
+        self.k, self.v = k, v  # held for the write
+        self.esize = k.element_size()
+        self.k_ptr, self.v_ptr, self.token_stride = k.data_ptr(), v.data_ptr(), k.stride(0)
+        self.dtype, self.row_elems, self.page_size = dtype_code(pool.dtype), row_elems, pool.shape[2]
+        self.pool_ptr, self.pool_stride = pool.data_ptr(), pool_block_stride(pool)
+        self.host_ptr = host.data_ptr() if host is not None else 0
+        self.sum_ptr, self.min_ptr, self.max_ptr = summaries.data_ptr(), minimum.data_ptr(), maximum.data_ptr()
+        self.stream = _stream(device)
+
+    def __call__(self, first, count, block, within, host_page, bounds_index):
+        """Rows first..first+count-1 of the write into rows within.. of pool
+        block `block` (and host block `host_page`); bounds_index is the
+        page's index in the flattened [layers, pages] bounds."""
+        if not (0 <= first and count >= 1 and first + count <= self.k.shape[0]):
+            raise ValueError("append_page: rows outside the write")
+        off = bounds_index * self.row_elems
+        status = self.lib.nhs_append_page(
+            ctypes.c_void_p(self.k_ptr + first * self.token_stride * self.esize),
+            ctypes.c_void_p(self.v_ptr + first * self.token_stride * self.esize), self.token_stride, self.dtype,
+            self.row_elems, self.page_size, ctypes.c_void_p(self.pool_ptr), self.pool_stride, int(block), int(within),
+            int(count), ctypes.c_void_p(self.host_ptr), int(host_page if self.host_ptr else 0),
+            ctypes.c_void_p(self.sum_ptr + off * 4), ctypes.c_void_p(self.min_ptr + off * self.esize),
+            ctypes.c_void_p(self.max_ptr + off * self.esize), self.stream,
+        )
+        _hip.check(status, "nhs_append_page")
+
+
 # ---- attention ------------------------------------------------------------------
 
 _workspaces: dict = {}

@@ -341,6 +341,13 @@ class HostStore:
         if len(self.pinned) >= self.budget:
             raise CapacityError("no slot available for append")
         P = cfg.page_size
+        appender = None
+        if self.cuda:
+            from .row_kernels import PageAppender
+
+            # one kernel per page: pool rows, host mirror rows, bounds and summary
+            appender = PageAppender(k.contiguous(), v.contiguous(), self.pool, self.host_alias, request.summaries,
+                                    request.minimum, request.maximum)
         done = 0
         while done < len(k):
             index, within = divmod(start + done, P)
@@ -361,15 +368,8 @@ class HostStore:
             page.content_version += 1
             page.sealed = page.valid_tokens == P
             page.location = Location.RESIDENT
-            if self.cuda:
-                # one kernel: pool rows, host mirror rows, bounds and summary
-                from .row_kernels import append_page
-
-                append_page(
-                    k[done : done + count].contiguous(), v[done : done + count].contiguous(), self.pool, page.slot,
-                    within, self.host_alias, page.host_slot, request.summaries[layer, index],
-                    request.minimum[layer, index], request.maximum[layer, index],
-                )
+            if appender is not None:
+                appender(done, count, page.slot, within, page.host_slot, layer * request.page_count + index)
                 page.ready = self.event(self.compute)
                 page.host_ready = page.ready
                 page.host_enqueued_version = page.content_version
